@@ -1,0 +1,143 @@
+/*
+ * laplacianformer_amd.h - C ABI of the MI355X (gfx950) LaplaceSubtraction and
+ * NewtonInverse operators.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*, a hipStream_t; NULL means the null stream). Nothing here
+ * depends on PyTorch. All launches are asynchronous on the given stream; no
+ * entry point synchronises the host. Outputs are caller-allocated and are
+ * fully overwritten (no pre-zeroing needed), exactly like the reference ops.
+ *
+ * Tensor layouts (contiguous, row-major), B = batch, H = heads:
+ *   query      [B, H, N, C]      key / grad_key  [B, H, C, M]   (channel-major)
+ *   output     [B, H, N, M]      grad_output     [B, H, N, M]
+ *   grad_query [B, H, N, C]
+ *   mat / out / grad [B*H, n, n]
+ *
+ * Every function returns LFAMD_OK (0) or one of the LFAMD_ERR_* codes;
+ * lfamd_last_error() gives a message for the calling thread's last failure.
+ */
+#ifndef LAPLACIANFORMER_AMD_H
+#define LAPLACIANFORMER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. All tensors of one call share one type. */
+#define LFAMD_F32 0
+#define LFAMD_F16 1
+#define LFAMD_BF16 2
+#define LFAMD_F64 3
+
+/* Status codes. */
+#define LFAMD_OK 0
+#define LFAMD_ERR_ARG 1         /* bad size, null pointer or workspace too small */
+#define LFAMD_ERR_DTYPE 2       /* element type not supported by this entry point */
+#define LFAMD_ERR_UNSUPPORTED 3 /* size outside the supported envelope */
+#define LFAMD_ERR_HIP 4         /* HIP runtime or launch failure */
+
+/* ---- LaplaceSubtraction ------------------------------------------------ */
+
+/* out[b,h,i,j] = sum_c |query[b,h,i,c] - key[b,h,c,j]|, fp32 accumulation
+ * (fp64 for LFAMD_F64), c ascending, rounded once to the element type.
+ * Replaces laplace::LaplaceSubtraction_forward_cuda
+ * (reference include/LaplaceSubtraction.h:9-13, src/LaplaceSubtraction_cuda.cu:55-67,
+ *  src/LaplaceSubtraction_cuda_kernel.cu:455-485). */
+int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* output,
+                          int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                          int64_t channels, void* stream);
+
+/* grad_query[b,h,i,c] = sum_j grad_output[b,h,i,j] * sgn(query[b,h,i,c] - key[b,h,c,j]),
+ * sgn(0) = 0. Replaces laplace::LaplaceSubtraction_backward_query_cuda
+ * (reference include/LaplaceSubtraction.h:15-20, src/LaplaceSubtraction_cuda.cu:69-84,
+ *  src/LaplaceSubtraction_cuda_kernel.cu:487-547). */
+int lfamd_laplace_backward_query(int dtype, const void* grad_output, const void* query,
+                                 const void* key, void* grad_query, int64_t batch,
+                                 int64_t heads, int64_t q_len, int64_t k_len,
+                                 int64_t channels, void* stream);
+
+/* Bytes of device workspace lfamd_laplace_backward_key / lfamd_laplace_backward
+ * need for these sizes (fp32 per-workgroup partial sums of grad_key). No
+ * counterpart in the reference, which split-K atomically adds into the output
+ * (src/LaplaceSubtraction_cuda_kernel.cu:568-591). */
+size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t heads,
+                                             int64_t q_len, int64_t k_len,
+                                             int64_t channels);
+
+/* grad_key[b,h,c,j] = -sum_i grad_output[b,h,i,j] * sgn(query[b,h,i,c] - key[b,h,c,j]).
+ * Deterministic: per-workgroup fp32 partials in `workspace`, summed in a fixed
+ * order by the last workgroup of each (b,h) slice, rounded once.
+ * Replaces laplace::LaplaceSubtraction_backward_key_cuda
+ * (reference include/LaplaceSubtraction.h:22-27, src/LaplaceSubtraction_cuda.cu:86-101,
+ *  src/LaplaceSubtraction_cuda_kernel.cu:549-609). */
+int lfamd_laplace_backward_key(int dtype, const void* grad_output, const void* query,
+                               const void* key, void* grad_key, int64_t batch,
+                               int64_t heads, int64_t q_len, int64_t k_len,
+                               int64_t channels, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* Fused backward: grad_query and grad_key in one pass over (i, j, c), computing
+ * sgn(query - key) once per triple. Superset export (no single reference entry
+ * point); equals lfamd_laplace_backward_query + lfamd_laplace_backward_key. */
+int lfamd_laplace_backward(int dtype, const void* grad_output, const void* query,
+                           const void* key, void* grad_query, void* grad_key,
+                           int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                           int64_t channels, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Legacy "reduce" forward: the same distance, accumulated in the element type
+ * by min(C,256) partial sums folded by a halving tree, exactly as the reference
+ * kernel does (including its behaviour when min(C,256) is not a power of two).
+ * Replaces laplace::LaplaceSubtraction_reduce_forward_cuda
+ * (reference include/LaplaceSubtraction.h:29-33, src/LaplaceSubtraction_cuda.cu:103-116,
+ *  src/LaplaceSubtraction_cuda_kernel.cu:399-447,611-647). */
+int lfamd_laplace_reduce_forward(int dtype, const void* query, const void* key,
+                                 void* output, int64_t batch, int64_t heads,
+                                 int64_t q_len, int64_t k_len, int64_t channels,
+                                 void* stream);
+
+/* ---- NewtonInverse ------------------------------------------------------ */
+
+/* Newton-Schulz inverse of P = mat + 0.01*I for each of the batch_heads n x n
+ * matrices: alpha = 1.8 / (max_i sum_j P_ij)^2, V0 = alpha*P,
+ * V <- 2V - V(PV) `iters` times (fp32 accumulation; fp64 for LFAMD_F64).
+ * Supported for 1 <= n <= 128. Replaces laplace::NewtonInverse_forward_cuda
+ * (reference include/NewtonInverse.h:9-12, src/NewtonInverse_cuda_kernel.cu:764-794). */
+int lfamd_newton_forward(int dtype, const void* mat, void* output, int64_t batch_heads,
+                         int64_t n, int iters, void* stream);
+
+/* grad_mat = -(V^T G) V^T for V = inverse, G = grad_output.
+ * Replaces laplace::NewtonInverse_backward_cuda
+ * (reference include/NewtonInverse.h:14-17, src/NewtonInverse_cuda_kernel.cu:796-833). */
+int lfamd_newton_backward(int dtype, const void* grad_output, const void* inverse,
+                          void* grad_mat, int64_t batch_heads, int64_t n, void* stream);
+
+/* 1 if n is inside the NewtonInverse envelope on this build, else 0.
+ * Replaces laplace::NewtonInverse_supports
+ * (reference include/NewtonInverse.h:19, src/NewtonInverse_cuda_kernel.cu:753-762). */
+int lfamd_newton_is_supported(int64_t n);
+
+/* ---- Runtime ------------------------------------------------------------ */
+
+/* HIP runtime version as major*100 + minor (e.g. 700 for 7.0), the convention
+ * the reference's version probe uses for HIP. Replaces laplace::get_cudart_version
+ * (reference src/cuda_version.cu:7-26). */
+int lfamd_runtime_version(void);
+
+/* Static text for a status code. No reference counterpart. */
+const char* lfamd_status_string(int status);
+
+/* Message for the calling thread's most recent failing call ("" if none).
+ * No reference counterpart (the reference printf's launch errors,
+ * src/LaplaceSubtraction_cuda_kernel.cu:481-484). */
+const char* lfamd_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAPLACIANFORMER_AMD_H */

@@ -1,0 +1,14 @@
+"""MI355X-native LaplaceSubtraction and NewtonInverse for LaplacianFormer.
+
+Drop-in for the reference's ``Laplace_subtraction_cuda`` extension: ``ext()``
+returns a module with the same name and exports, backed by hand-written gfx950
+HIP kernels behind the C ABI of ``include/laplacianformer_amd.h``.
+"""
+from ._lib import EXT_PATH, LIB_PATH, capi, check, dtype_code, ext
+from .functional import (LaplaceSubtractionFunction, NewtonInverseFunction, laplace_subtraction,
+                         newton_inverse)
+
+__all__ = [
+    "EXT_PATH", "LIB_PATH", "capi", "check", "dtype_code", "ext", "LaplaceSubtractionFunction",
+    "NewtonInverseFunction", "laplace_subtraction", "newton_inverse",
+]

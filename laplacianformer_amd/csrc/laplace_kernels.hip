@@ -1,0 +1,701 @@
+// LaplaceSubtraction on gfx950: pairwise L1 distance and its sign-weighted
+// backward, on the vector ALU.
+//
+// Reference semantics (src/LaplaceSubtraction_cuda_kernel.cu):
+//   forward  out[i,j] = cast(sum_c |f32(q[i,c]) - f32(k[c,j])|), c ascending      (:84-140)
+//   dq       dq[i,c]  = cast(sum_j f32(g[i,j]) * sgn(f32(q[i,c]) - f32(k[c,j])))   (:183-266)
+//   dk       dk[c,j]  = cast(-sum_i f32(g[i,j]) * sgn(f32(q[i,c]) - f32(k[c,j])))  (:309-392)
+//   sgn(0) = 0 (:34-38); fp32 accumulation, fp64 for double (:17-19).
+//
+// Forward mapping: one wave = 64 consecutive query rows (one per lane) x JB key
+// columns; the key tile sits in LDS and every lane reads the same address
+// (broadcast), so each (c, j) step costs one subtract and one |.|-add per lane.
+// For fp16 the subtract is v_fma_mix_f32 on the packed halves: no conversions.
+//
+// Backward mapping: one lane per channel c, one wave per run of query rows,
+// key column held in registers, the grad_output row broadcast from LDS. dq is a
+// lane-local sum over j; dk is a lane-local sum over the wave's rows, reduced
+// across the workgroup's waves in LDS in a fixed order and across workgroups by
+// the last workgroup of each slice (fixed order again), so results are
+// deterministic.
+#include <algorithm>
+
+#include "lf_common.h"
+#include "lf_internal.h"
+
+namespace lfamd {
+
+// ---------------------------------------------------------------------------
+// Staged element type for the forward key tile.
+// ---------------------------------------------------------------------------
+template <typename T> struct StageOf { using type = float; };
+template <> struct StageOf<f16s> { using type = uint16_t; };
+template <> struct StageOf<double> { using type = double; };
+
+__device__ __forceinline__ float stage_val(float v) { return v; }
+__device__ __forceinline__ float stage_val(bf16s v) { return to_acc(v); }
+__device__ __forceinline__ uint16_t stage_val(f16s v) { return v.bits; }
+__device__ __forceinline__ double stage_val(double v) { return v; }
+
+// Query elements per vector load in the forward (16 bytes).
+template <typename T> struct QChunk { static constexpr int value = 16 / sizeof(T); };
+
+constexpr int kFwdKC = 64;  // channels staged per LDS pass
+
+template <typename T, int JB>
+__global__ void __launch_bounds__(1024)
+laplace_fwd_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out,
+                   int N, int M, int C, int colsPerGroup, int vecq) {
+  using S = typename StageOf<T>::type;
+  using A = typename AccOf<T>::type;
+  constexpr int SV = 16 / (int)sizeof(S);  // staged elements per 16-byte LDS read
+  constexpr int JBP = round_up(JB, SV);
+  constexpr int CK = QChunk<T>::value;
+
+  const int W = blockDim.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.z;
+  const int row0 = blockIdx.x * 64;
+  const int jg0 = blockIdx.y * colsPerGroup;
+  const int row = row0 + lane;
+  const int rowc = row < N ? row : N - 1;  // rows past N compute garbage that is never stored
+  const int ldsCols = W * JBP;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  S* kt = reinterpret_cast<S*>(smem);  // [kFwdKC][ldsCols]
+  T* ot = reinterpret_cast<T*>(smem + (size_t)kFwdKC * ldsCols * sizeof(S));  // [64][colsPerGroup]
+
+  const T* qrow = query + ((size_t)bh * N + rowc) * C;
+  const T* kb = key + (size_t)bh * C * M;
+
+  A acc[JB];
+#pragma unroll
+  for (int j = 0; j < JB; ++j) acc[j] = A(0);
+
+  for (int c0 = 0; c0 < C; c0 += kFwdKC) {
+    const int kc = min(kFwdKC, C - c0);
+    __syncthreads();
+    for (int e = threadIdx.x; e < kFwdKC * ldsCols; e += blockDim.x) {
+      const int cc = e / ldsCols, u = e - cc * ldsCols;
+      const int wb = u / JBP, jj = u - wb * JBP;
+      const int col = jg0 + wb * JB + jj;
+      S v = S(0);
+      if (cc < kc && jj < JB && col < M) v = stage_val(kb[(size_t)(c0 + cc) * M + col]);
+      kt[e] = v;
+    }
+    __syncthreads();
+
+    const S* kw = kt + wave * JBP;
+    for (int cc = 0; cc < kc; cc += CK) {
+      const int cg = c0 + cc;
+      if constexpr (std::is_same<T, f16s>::value) {
+        // 8 query halves as 4 packed registers.
+        uint32_t qh[4];
+        if (vecq) {
+          uint4 v = *reinterpret_cast<const uint4*>(qrow + cg);
+          qh[0] = v.x; qh[1] = v.y; qh[2] = v.z; qh[3] = v.w;
+        } else {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            uint32_t lo = (cg + 2 * p < C) ? qrow[cg + 2 * p].bits : 0u;
+            uint32_t hi = (cg + 2 * p + 1 < C) ? qrow[cg + 2 * p + 1].bits : 0u;
+            qh[p] = lo | (hi << 16);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < CK; ++u) {
+          uint32_t kwv[JBP / 2];
+          const uint4* kr = reinterpret_cast<const uint4*>(kw + (cc + u) * ldsCols);
+#pragma unroll
+          for (int t = 0; t < JBP / 8; ++t) {
+            uint4 v = kr[t];
+            kwv[4 * t] = v.x; kwv[4 * t + 1] = v.y; kwv[4 * t + 2] = v.z; kwv[4 * t + 3] = v.w;
+          }
+          const uint32_t qp = qh[u >> 1];
+#pragma unroll
+          for (int j = 0; j < JB; ++j) {
+            const uint32_t kp = kwv[j >> 1];
+            float d;
+            if (u & 1) d = (j & 1) ? mix_sub_hh<1, 1>(qp, kp) : mix_sub_hh<1, 0>(qp, kp);
+            else       d = (j & 1) ? mix_sub_hh<0, 1>(qp, kp) : mix_sub_hh<0, 0>(qp, kp);
+            acc[j] += fabsf(d);
+          }
+        }
+      } else {
+        A qf[CK];
+        if (vecq) {
+          if constexpr (std::is_same<T, bf16s>::value) {
+            uint4 v = *reinterpret_cast<const uint4*>(qrow + cg);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              qf[2 * p] = __builtin_bit_cast(float, w[p] << 16);
+              qf[2 * p + 1] = __builtin_bit_cast(float, w[p] & 0xffff0000u);
+            }
+          } else {
+            const T* src = qrow + cg;
+#pragma unroll
+            for (int p = 0; p < CK; ++p) qf[p] = to_acc(src[p]);
+          }
+        } else {
+#pragma unroll
+          for (int p = 0; p < CK; ++p) qf[p] = (cg + p < C) ? to_acc(qrow[cg + p]) : A(0);
+        }
+#pragma unroll
+        for (int u = 0; u < CK; ++u) {
+          const S* kr = kw + (cc + u) * ldsCols;
+          S kv[JBP];
+#pragma unroll
+          for (int t = 0; t < JBP; ++t) kv[t] = kr[t];
+          const A qv = qf[u];
+#pragma unroll
+          for (int j = 0; j < JB; ++j) {
+            acc[j] += fabs(qv - (A)kv[j]);
+          }
+        }
+      }
+    }
+  }
+
+  // Stage the 64 x colsPerGroup tile, then store it row-contiguously.
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < JB; ++j) ot[lane * colsPerGroup + wave * JB + j] = from_acc<T>(acc[j]);
+  __syncthreads();
+  const int colsValid = min(colsPerGroup, M - jg0);
+  const int rowsValid = min(64, N - row0);
+  T* ob = out + ((size_t)bh * N + row0) * M + jg0;
+  if (colsPerGroup == M) {
+    const int total = rowsValid * M;  // whole rows: one contiguous range
+    for (int e = threadIdx.x; e < total; e += blockDim.x) ob[e] = ot[e];
+  } else {
+    for (int r = wave; r < rowsValid; r += W)
+      for (int cidx = lane; cidx < colsValid; cidx += 64)
+        ob[(size_t)r * M + cidx] = ot[r * colsPerGroup + cidx];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward.
+// ---------------------------------------------------------------------------
+// sgn(q - k) with sgn(0) = 0. For fp16 inputs both operands are pre-scaled by
+// 2^24, which makes every non-zero difference at least 1 in magnitude, so a
+// clamp to [-1, 1] is the exact sign. For fp32/bf16 the difference is first
+// scaled by 2^200 (ldexp; overflow to +-inf is fine) for the same effect.
+template <typename T> struct SignOps {
+  static __device__ __forceinline__ float scale(float v) { return v; }
+  static __device__ __forceinline__ float sgn(float d) {
+    return __builtin_amdgcn_fmed3f(ldexpf(d, 200), -1.0f, 1.0f);
+  }
+};
+template <> struct SignOps<f16s> {
+  static __device__ __forceinline__ float scale(float v) { return v * 16777216.0f; }
+  static __device__ __forceinline__ float sgn(float d) {
+    return __builtin_amdgcn_fmed3f(d, -1.0f, 1.0f);
+  }
+};
+template <> struct SignOps<double> {
+  static __device__ __forceinline__ double scale(double v) { return v; }
+  static __device__ __forceinline__ double sgn(double d) {
+    return (double)((d > 0.0) - (d < 0.0));
+  }
+};
+
+constexpr int kBwdRB = 8;  // grad_output rows staged per LDS batch
+
+template <typename T, int JB, bool DQ, bool DK>
+__global__ void __launch_bounds__(512)
+laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
+                   const T* __restrict__ key, T* __restrict__ dq, T* __restrict__ dk,
+                   typename AccOf<T>::type* __restrict__ partial, unsigned* __restrict__ counters,
+                   int N, int M, int C, int rowsPerWave) {
+  using A = typename AccOf<T>::type;
+  using SO = SignOps<T>;
+  constexpr int GV = 16 / (int)sizeof(A);
+  constexpr int JBP = round_up(JB, GV);
+
+  const int W = blockDim.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.z;
+  const int cb = blockIdx.y;
+  const int x = blockIdx.x;
+  const int nx = gridDim.x;
+  const int slice = bh * gridDim.y + cb;
+  const int c = cb * 64 + lane;
+  const bool cval = c < C;
+  const int rowBeg = (x * W + wave) * rowsPerWave;
+  const int rowEnd = min(N, rowBeg + rowsPerWave);
+  const bool multiJ = M > JB;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  A* gsm = reinterpret_cast<A*>(smem);                 // [W][kBwdRB][JBP]
+  A* red = gsm + (size_t)W * kBwdRB * JBP;             // [JB][64]        (DK)
+  A* dqp = red + (DK ? JB * 64 : 0);                   // [W][rowsPerWave][64] (DQ && multiJ)
+
+  const T* qb = query + (size_t)bh * N * C;
+  const T* gb = gout + (size_t)bh * N * M;
+  const T* kb = key + (size_t)bh * C * M;
+  A* gw = gsm + (size_t)wave * kBwdRB * JBP;
+
+  for (int jb0 = 0; jb0 < M; jb0 += JB) {
+    const bool lastJ = jb0 + JB >= M;
+    A kreg[JB];
+    A dka[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int col = jb0 + j;
+      kreg[j] = (cval && col < M) ? SO::scale(to_acc(kb[(size_t)c * M + col])) : A(0);
+      dka[j] = A(0);
+    }
+
+    for (int rb = rowBeg; rb < rowEnd; rb += kBwdRB) {
+      const int nr = min(kBwdRB, rowEnd - rb);
+      for (int e = lane; e < kBwdRB * JBP; e += 64) {
+        const int r = e / JBP, jj = e - r * JBP;
+        const int col = jb0 + jj;
+        A v = A(0);
+        if (r < nr && jj < JB && col < M) v = to_acc(gb[(size_t)(rb + r) * M + col]);
+        gw[e] = v;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      for (int r = 0; r < nr; ++r) {
+        const int i = rb + r;
+        const A qv = cval ? SO::scale(to_acc(qb[(size_t)i * C + c])) : A(0);
+        A dqa = A(0);
+        if (DQ && multiJ && jb0 > 0) dqa = dqp[((size_t)wave * rowsPerWave + (i - rowBeg)) * 64 + lane];
+        const A* gr = gw + r * JBP;
+#pragma unroll
+        for (int j0 = 0; j0 < JBP; j0 += GV) {
+          A gv[GV];
+#pragma unroll
+          for (int t = 0; t < GV; ++t) gv[t] = gr[j0 + t];
+#pragma unroll
+          for (int t = 0; t < GV; ++t) {
+            const int j = j0 + t;
+            if (j < JB) {
+              const A s = SO::sgn(qv - kreg[j]);
+              if (DQ) dqa = fma(s, gv[t], dqa);
+              if (DK) dka[j] = fma(s, -gv[t], dka[j]);
+            }
+          }
+        }
+        if (DQ) {
+          if (lastJ) {
+            if (cval) dq[((size_t)bh * N + i) * C + c] = from_acc<T>(dqa);
+          } else {
+            dqp[((size_t)wave * rowsPerWave + (i - rowBeg)) * 64 + lane] = dqa;
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    if (DK) {
+      // Fold the waves' partial sums in wave order (deterministic).
+      for (int w = 0; w < W; ++w) {
+        if (wave == w) {
+#pragma unroll
+          for (int j = 0; j < JB; ++j)
+            red[j * 64 + lane] = (w == 0 ? A(0) : red[j * 64 + lane]) + dka[j];
+        }
+        __syncthreads();
+      }
+      // partial[slice][x][c_local][M]
+      A* pb = partial + ((size_t)slice * nx + x) * 64 * M;
+      for (int t = threadIdx.x; t < 64 * JB; t += blockDim.x) {
+        const int cl = t / JB, j = t - cl * JB;
+        const int col = jb0 + j;
+        if (col < M) pb[(size_t)cl * M + col] = red[j * 64 + cl];
+      }
+      __syncthreads();
+    }
+  }
+
+  if (DK) {
+    // The last workgroup of the slice folds all partials in workgroup order.
+    __shared__ int isLast;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = atomicAdd(&counters[slice], 1u);
+      isLast = (prev == (unsigned)(nx - 1));
+    }
+    __syncthreads();
+    if (isLast) {
+      __threadfence();
+      const A* pb = partial + (size_t)slice * nx * 64 * M;
+      for (int t = threadIdx.x; t < 64 * M; t += blockDim.x) {
+        const int cl = t / M, j = t - cl * M;
+        const int cc = cb * 64 + cl;
+        if (cc < C) {
+          A s = A(0);
+          for (int x2 = 0; x2 < nx; ++x2) s += pb[(size_t)x2 * 64 * M + t];
+          dk[((size_t)bh * C + cc) * M + j] = from_acc<T>(s);
+        }
+      }
+      if (threadIdx.x == 0) atomicExch(&counters[slice], 0u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Legacy reduce forward: one workgroup of bd = min(C, 256) threads per output,
+// arithmetic in the element type, halving-tree fold (reference :399-447).
+// ---------------------------------------------------------------------------
+template <typename T> struct NativeOf { using type = float; };
+template <> struct NativeOf<f16s> { using type = _Float16; };
+template <> struct NativeOf<double> { using type = double; };
+
+template <typename T> __device__ __forceinline__ typename NativeOf<T>::type to_native(T v);
+template <> __device__ __forceinline__ float to_native<float>(float v) { return v; }
+template <> __device__ __forceinline__ double to_native<double>(double v) { return v; }
+template <> __device__ __forceinline__ _Float16 to_native<f16s>(f16s v) {
+  return __builtin_bit_cast(_Float16, v.bits);
+}
+template <> __device__ __forceinline__ float to_native<bf16s>(bf16s v) { return to_acc(v); }
+
+// One rounding to the element type after each native operation (bf16 is
+// emulated in fp32 and rounded back; fp32 has enough precision for that to
+// equal a direct bf16 operation).
+template <typename T> __device__ __forceinline__ typename NativeOf<T>::type round_native(typename NativeOf<T>::type v) { return v; }
+template <> __device__ __forceinline__ float round_native<bf16s>(float v) { return to_acc(from_acc<bf16s>(v)); }
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+laplace_reduce_fwd_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out,
+                          int64_t total, int N, int M, int C) {
+  using Nt = typename NativeOf<T>::type;
+  __shared__ Nt sdata[256];
+  const int bd = blockDim.x;
+  for (int64_t idx = blockIdx.x; idx < total; idx += gridDim.x) {
+    const int64_t bh = idx / ((int64_t)N * M);
+    const int64_t rem = idx - bh * N * M;
+    const int p = (int)(rem / M), qj = (int)(rem - (int64_t)p * M);
+    const T* qr = query + (bh * N + p) * C;
+    const T* kc = key + bh * C * M + qj;
+    Nt s = Nt(0);
+    for (int c = threadIdx.x; c < C; c += bd) {
+      Nt diff = round_native<T>(to_native(qr[c]) - to_native(kc[(int64_t)c * M]));
+      s = round_native<T>(s + (diff >= Nt(0) ? diff : -diff));
+    }
+    sdata[threadIdx.x] = s;
+    __syncthreads();
+    for (int stride = bd / 2; stride > 0; stride >>= 1) {
+      if ((int)threadIdx.x < stride) sdata[threadIdx.x] = round_native<T>(sdata[threadIdx.x] + sdata[threadIdx.x + stride]);
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      if constexpr (std::is_same<T, f16s>::value) out[idx] = f16s{__builtin_bit_cast(uint16_t, sdata[0])};
+      else if constexpr (std::is_same<T, bf16s>::value) out[idx] = from_acc<bf16s>(sdata[0]);
+      else out[idx] = sdata[0];
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Dims {
+  int64_t B, H, N, M, C;
+  int64_t BH() const { return B * H; }
+};
+
+int check_dims(const Dims& d, const char* who) {
+  if (d.B < 0 || d.H < 0 || d.N < 0 || d.M < 0 || d.C < 0)
+    return fail(LFAMD_ERR_ARG, "%s: negative size", who);
+  if (d.N > INT32_MAX / 2 || d.M > INT32_MAX / 2 || d.C > INT32_MAX / 2 || d.BH() > 65535)
+    return fail(LFAMD_ERR_UNSUPPORTED, "%s: sizes too large (B*H must be <= 65535)", who);
+  return LFAMD_OK;
+}
+
+bool empty(const Dims& d) { return d.BH() == 0 || d.N == 0 || d.M == 0; }
+
+// ---- forward ----
+template <typename T> constexpr int stage_bytes() { return (int)sizeof(typename StageOf<T>::type); }
+
+template <typename T, int JB>
+int launch_fwd_jb(const T* q, const T* k, T* o, const Dims& d, hipStream_t st) {
+  constexpr int SV = 16 / stage_bytes<T>();
+  constexpr int JBP = round_up(JB, SV);
+  const int M = (int)d.M, N = (int)d.N, C = (int)d.C;
+  const int ldsBudget = 64 * 1024;
+  int W = std::min(16, ceil_div(M, JB));
+  auto lds = [&](int w) {
+    return (size_t)kFwdKC * w * JBP * stage_bytes<T>() + (size_t)64 * w * JB * sizeof(T);
+  };
+  while (W > 1 && lds(W) > (size_t)ldsBudget) --W;
+  const int cols = W * JB;
+  dim3 grid(ceil_div(N, 64), ceil_div(M, cols), (unsigned)d.BH());
+  dim3 block(64 * W);
+  constexpr int CK = QChunk<T>::value;
+  const int vecq = (C % CK == 0) && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
+  hipLaunchKernelGGL((laplace_fwd_kernel<T, JB>), grid, block, lds(W), st, q, k, o, N, M, C, cols, vecq);
+  return check_launch("laplace forward");
+}
+
+// Column block: the candidate with the least padding, ties to the larger block.
+int pick_fwd_jb(int64_t M) {
+  const int cands[4] = {7, 8, 16, 32};
+  int best = 32;
+  int64_t bestPad = INT64_MAX;
+  for (int jb : cands) {
+    const int64_t pad = ceil_div((int)M, jb) * (int64_t)jb - M;
+    if (pad < bestPad || (pad == bestPad && jb > best)) { bestPad = pad; best = jb; }
+  }
+  return best;
+}
+
+template <typename T>
+int launch_fwd(const void* q, const void* k, void* o, const Dims& d, hipStream_t st) {
+  const T* qq = static_cast<const T*>(q);
+  const T* kk = static_cast<const T*>(k);
+  T* oo = static_cast<T*>(o);
+  switch (pick_fwd_jb(d.M)) {
+    case 7: return launch_fwd_jb<T, 7>(qq, kk, oo, d, st);
+    case 8: return launch_fwd_jb<T, 8>(qq, kk, oo, d, st);
+    case 16: return launch_fwd_jb<T, 16>(qq, kk, oo, d, st);
+    default: return launch_fwd_jb<T, 32>(qq, kk, oo, d, st);
+  }
+}
+
+// ---- backward ----
+struct BwdPlan {
+  int JB;           // key columns per register block
+  int W;            // waves per workgroup
+  int nx;           // workgroups per (bh, channel block) slice
+  int rowsPerWave;
+  int ncb;          // channel blocks of 64
+  size_t lds;
+  size_t partialElems;
+};
+
+int pick_bwd_jb(int64_t M) {
+  if (M <= 16) return 16;
+  if (M <= 32) return 32;
+  if (M == 49) return 49;
+  return 64;
+}
+
+BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes) {
+  BwdPlan p{};
+  p.JB = pick_bwd_jb(d.M);
+  p.ncb = ceil_div((int)d.C, 64);
+  const int GV = 16 / (int)accBytes;
+  const int JBP = round_up(p.JB, GV);
+  const bool multiJ = d.M > p.JB;
+  const int64_t slices = d.BH() * p.ncb;
+  const int N = (int)std::max<int64_t>(d.N, 1);
+  // One round of resident waves: 2 per SIMD (the kernel may use up to 256
+  // registers), at least 8 rows per wave.
+  const int target = 8 * num_cus();
+  int64_t wps = std::max<int64_t>(1, ceil_div(target, (int)std::min<int64_t>(slices, target)));
+  wps = std::min<int64_t>(wps, ceil_div(N, 8));
+  int rows = ceil_div(N, (int)wps);
+  if (dq && multiJ) rows = std::min(rows, 64);
+  wps = ceil_div(N, rows);
+  const size_t budget = 96 * 1024;
+  auto lds = [&](int w) {
+    size_t b = (size_t)w * kBwdRB * JBP * accBytes;
+    if (dkey) b += (size_t)p.JB * 64 * accBytes;
+    if (dq && multiJ) b += (size_t)w * rows * 64 * accBytes;
+    return b;
+  };
+  int W = (int)std::min<int64_t>(8, wps);
+  while (W > 1 && lds(W) > budget) --W;
+  p.W = W;
+  p.nx = ceil_div((int)wps, W);
+  p.rowsPerWave = ceil_div(N, p.nx * W);
+  if (dq && multiJ) p.rowsPerWave = std::min(p.rowsPerWave, rows);
+  p.lds = lds(W);
+  p.partialElems = dkey ? (size_t)slices * p.nx * 64 * (size_t)d.M : 0;
+  return p;
+}
+
+template <typename T, int JB, bool DQ, bool DK>
+int launch_bwd_jb(const T* g, const T* q, const T* k, T* dq, T* dk, void* ws, unsigned* counters,
+                  const Dims& d, const BwdPlan& p, hipStream_t st) {
+  using A = typename AccOf<T>::type;
+  dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
+  dim3 block(64 * p.W);
+  hipLaunchKernelGGL((laplace_bwd_kernel<T, JB, DQ, DK>), grid, block, p.lds, st, g, q, k, dq, dk,
+                     static_cast<A*>(ws), counters, (int)d.N, (int)d.M, (int)d.C, p.rowsPerWave);
+  return check_launch("laplace backward");
+}
+
+template <typename T, bool DQ, bool DK>
+int launch_bwd_t(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws,
+                 unsigned* counters, const Dims& d, const BwdPlan& p, hipStream_t st) {
+  auto G = static_cast<const T*>(g);
+  auto Q = static_cast<const T*>(q);
+  auto K = static_cast<const T*>(k);
+  auto DQp = static_cast<T*>(dq);
+  auto DKp = static_cast<T*>(dk);
+  switch (p.JB) {
+    case 16: return launch_bwd_jb<T, 16, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
+    case 32: return launch_bwd_jb<T, 32, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
+    case 49: return launch_bwd_jb<T, 49, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
+    default: return launch_bwd_jb<T, 64, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
+  }
+}
+
+template <bool DQ, bool DK>
+int launch_bwd(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws,
+               unsigned* counters, const Dims& d, const BwdPlan& p, hipStream_t st) {
+  switch (dtype) {
+    case LFAMD_F32: return launch_bwd_t<float, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
+    case LFAMD_F16: return launch_bwd_t<f16s, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
+    case LFAMD_BF16: return launch_bwd_t<bf16s, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
+    default: return launch_bwd_t<double, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
+  }
+}
+
+// Fills `n` elements of `p` with zero (used when the reduction length is 0).
+template <typename T>
+__global__ void fill_zero_kernel(T* __restrict__ p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = T{};
+}
+
+int zero_fill(void* p, int64_t bytes, hipStream_t st) {
+  if (bytes <= 0) return LFAMD_OK;
+  const int64_t words = bytes / 2;  // every element type is a multiple of 2 bytes
+  const int blocks = (int)std::min<int64_t>(1024, (words + 255) / 256);
+  hipLaunchKernelGGL(fill_zero_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, static_cast<uint16_t*>(p), words);
+  return check_launch("zero fill");
+}
+
+int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk,
+               const Dims& d, void* ws, size_t wsBytes, void* stream, bool doDq, bool doDk,
+               const char* who) {
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dtype);
+  int s = check_dims(d, who);
+  if (s) return s;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t es = dtype_size(dtype);
+  if (d.BH() == 0 || d.C == 0) return ok();
+  if (d.M == 0 || d.N == 0) {
+    // Empty reduction: the gradients are zero (the output is empty when N or M is 0).
+    if (doDq && (s = zero_fill(dq, d.BH() * d.N * d.C * (int64_t)es, st))) return s;
+    if (doDk && (s = zero_fill(dk, d.BH() * d.C * d.M * (int64_t)es, st))) return s;
+    return ok();
+  }
+  if (!g || !q || !k || (doDq && !dq) || (doDk && !dk)) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
+  const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
+  const BwdPlan p = plan_bwd(d, doDq, doDk, acc);
+  unsigned* counters = nullptr;
+  if (doDk) {
+    const size_t need = p.partialElems * acc;
+    if (!ws || wsBytes < need)
+      return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, need, wsBytes);
+    counters = stream_counters(st, (size_t)d.BH() * p.ncb);
+    if (!counters) return LFAMD_ERR_HIP;
+  }
+  if (doDq && doDk) return launch_bwd<true, true>(dtype, g, q, k, dq, dk, ws, counters, d, p, st);
+  if (doDq) return launch_bwd<true, false>(dtype, g, q, k, dq, dk, ws, counters, d, p, st);
+  return launch_bwd<false, true>(dtype, g, q, k, dq, dk, ws, counters, d, p, st);
+}
+
+}  // namespace
+}  // namespace lfamd
+
+using namespace lfamd;
+
+extern "C" {
+
+int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* output,
+                          int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                          int64_t channels, void* stream) {
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "laplace forward: unsupported dtype %d", dtype);
+  const Dims d{batch, heads, q_len, k_len, channels};
+  int s = check_dims(d, "laplace forward");
+  if (s) return s;
+  if (empty(d)) return ok();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d.C == 0) return zero_fill(output, d.BH() * d.N * d.M * (int64_t)dtype_size(dtype), st);
+  if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace forward: null pointer");
+  switch (dtype) {
+    case LFAMD_F32: return launch_fwd<float>(query, key, output, d, st);
+    case LFAMD_F16: return launch_fwd<f16s>(query, key, output, d, st);
+    case LFAMD_BF16: return launch_fwd<bf16s>(query, key, output, d, st);
+    default: return launch_fwd<double>(query, key, output, d, st);
+  }
+}
+
+int lfamd_laplace_backward_query(int dtype, const void* grad_output, const void* query,
+                                 const void* key, void* grad_query, int64_t batch,
+                                 int64_t heads, int64_t q_len, int64_t k_len,
+                                 int64_t channels, void* stream) {
+  return bwd_common(dtype, grad_output, query, key, grad_query, nullptr,
+                    Dims{batch, heads, q_len, k_len, channels}, nullptr, 0, stream, true, false,
+                    "laplace backward_query");
+}
+
+size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t heads,
+                                             int64_t q_len, int64_t k_len, int64_t channels) {
+  const Dims d{batch, heads, q_len, k_len, channels};
+  if (!valid_dtype(dtype) || check_dims(d, "workspace") || d.BH() == 0 || d.N == 0 || d.M == 0 || d.C == 0)
+    return 0;
+  const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
+  return plan_bwd(d, true, true, acc).partialElems * acc;
+}
+
+int lfamd_laplace_backward_key(int dtype, const void* grad_output, const void* query,
+                               const void* key, void* grad_key, int64_t batch,
+                               int64_t heads, int64_t q_len, int64_t k_len,
+                               int64_t channels, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return bwd_common(dtype, grad_output, query, key, nullptr, grad_key,
+                    Dims{batch, heads, q_len, k_len, channels}, workspace, workspace_bytes, stream,
+                    false, true, "laplace backward_key");
+}
+
+int lfamd_laplace_backward(int dtype, const void* grad_output, const void* query,
+                           const void* key, void* grad_query, void* grad_key,
+                           int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                           int64_t channels, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return bwd_common(dtype, grad_output, query, key, grad_query, grad_key,
+                    Dims{batch, heads, q_len, k_len, channels}, workspace, workspace_bytes, stream,
+                    true, true, "laplace backward");
+}
+
+int lfamd_laplace_reduce_forward(int dtype, const void* query, const void* key,
+                                 void* output, int64_t batch, int64_t heads,
+                                 int64_t q_len, int64_t k_len, int64_t channels,
+                                 void* stream) {
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "laplace reduce_forward: unsupported dtype %d", dtype);
+  const Dims d{batch, heads, q_len, k_len, channels};
+  int s = check_dims(d, "laplace reduce_forward");
+  if (s) return s;
+  if (empty(d)) return ok();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d.C == 0) return zero_fill(output, d.BH() * d.N * d.M * (int64_t)dtype_size(dtype), st);
+  if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace reduce_forward: null pointer");
+  const int64_t total = d.BH() * d.N * d.M;
+  const int bd = (int)std::min<int64_t>(d.C, 256);
+  const unsigned blocks = (unsigned)std::min<int64_t>(total, 1 << 20);
+#define LFAMD_REDUCE(T)                                                                        \
+  hipLaunchKernelGGL(laplace_reduce_fwd_kernel<T>, dim3(blocks), dim3(bd), 0, st,              \
+                     static_cast<const T*>(query), static_cast<const T*>(key), static_cast<T*>(output), \
+                     total, (int)d.N, (int)d.M, (int)d.C)
+  switch (dtype) {
+    case LFAMD_F32: LFAMD_REDUCE(float); break;
+    case LFAMD_F16: LFAMD_REDUCE(f16s); break;
+    case LFAMD_BF16: LFAMD_REDUCE(bf16s); break;
+    default: LFAMD_REDUCE(double); break;
+  }
+#undef LFAMD_REDUCE
+  return check_launch("laplace reduce_forward");
+}
+
+}  // extern "C"

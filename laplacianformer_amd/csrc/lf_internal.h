@@ -1,0 +1,38 @@
+// Host-side internals shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/laplacianformer_amd.h"
+
+namespace lfamd {
+
+// Records a message for lfamd_last_error() on the calling thread and returns `status`.
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Clears the calling thread's error message and returns LFAMD_OK.
+int ok();
+
+// Turns a pending launch error into LFAMD_ERR_HIP.
+int check_launch(const char* what);
+
+// Per-(device, stream) array of at least `n` zeroed uint32 counters used by the
+// last-workgroup reductions. Every kernel that takes a counter back to zero
+// before it exits, so the array stays zero between calls on one stream.
+// Returns nullptr (and records an error) on allocation failure.
+unsigned* stream_counters(hipStream_t stream, size_t n);
+
+// Max dynamic LDS bytes per workgroup on the current device (cached per device).
+int max_lds_bytes();
+
+// Compute units of the current device (cached per device; 256 if unknown).
+int num_cus();
+
+inline bool valid_dtype(int dt) {
+  return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;
+}
+inline size_t dtype_size(int dt) { return dt == LFAMD_F64 ? 8 : (dt == LFAMD_F32 ? 4 : 2); }
+
+}  // namespace lfamd

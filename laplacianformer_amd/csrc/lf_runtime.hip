@@ -1,0 +1,128 @@
+// Runtime plumbing of the C ABI: status strings, per-thread error text, the
+// per-(device, stream) counter arrays of the last-workgroup reductions, and the
+// HIP runtime version probe.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+#include <vector>
+
+#include "lf_internal.h"
+
+namespace lfamd {
+
+static thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return LFAMD_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LFAMD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+namespace {
+struct CounterBlock {
+  unsigned* ptr = nullptr;
+  size_t n = 0;
+};
+std::mutex g_counter_mu;
+std::map<std::pair<int, hipStream_t>, CounterBlock> g_counters;
+std::vector<unsigned*> g_retired;  // superseded blocks; queued kernels may still use them
+}  // namespace
+
+unsigned* stream_counters(hipStream_t stream, size_t n) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    fail(LFAMD_ERR_HIP, "hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_counter_mu);
+  CounterBlock& b = g_counters[std::make_pair(dev, stream)];
+  if (b.n >= n) return b.ptr;
+  size_t want = n < 4096 ? 4096 : n * 2;
+  unsigned* p = nullptr;
+  if (hipMalloc(&p, want * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(p, 0, want * sizeof(unsigned)) != hipSuccess) {
+    fail(LFAMD_ERR_HIP, "cannot allocate %zu reduction counters", want);
+    return nullptr;
+  }
+  if (b.ptr) g_retired.push_back(b.ptr);
+  b.ptr = p;
+  b.n = want;
+  return p;
+}
+
+int max_lds_bytes() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 65536;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  // The opt-in limit (what hipFuncSetAttribute may raise a kernel to) if the
+  // runtime reports one, else the default per-workgroup limit.
+  int v = 0, optin = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+    v = 65536;
+  if (hipDeviceGetAttribute(&optin, hipDeviceAttributeSharedMemPerBlockOptin, dev) == hipSuccess && optin > v)
+    v = optin;
+  cache[dev] = v;
+  return v;
+}
+
+int num_cus() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cache[dev] = v;
+  return v;
+}
+
+}  // namespace lfamd
+
+extern "C" {
+
+int lfamd_runtime_version(void) {
+  int v = 0;
+  if (hipRuntimeGetVersion(&v) != hipSuccess) return 0;
+  // hipRuntimeGetVersion encodes major*10000000 + minor*100000 + patch.
+  int major = v / 10000000, minor = (v / 100000) % 100;
+  return major * 100 + minor;
+}
+
+const char* lfamd_status_string(int status) {
+  switch (status) {
+    case LFAMD_OK: return "ok";
+    case LFAMD_ERR_ARG: return "invalid argument";
+    case LFAMD_ERR_DTYPE: return "unsupported element type";
+    case LFAMD_ERR_UNSUPPORTED: return "size outside the supported envelope";
+    case LFAMD_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+const char* lfamd_last_error(void) { return lfamd::g_last_error; }
+
+}  // extern "C"

@@ -1,0 +1,461 @@
+// NewtonInverse on gfx950: batched Newton-Schulz inverse with the matrices kept
+// in LDS for all iterations, products on the fp32 matrix cores.
+//
+// Reference semantics (src/NewtonInverse_cuda_kernel.cu):
+//   P = f32(mat) + 0.01 I                                       (:169, :320)
+//   alpha = 1.8 / (max_i sum_j P_ij)^2, signed row sums          (:82-120)
+//   V0 = alpha P; iters x V <- 2V - V(PV)   [3-buffer, n <= 112] (:181-248)
+//                          V <- 2V - (VP)V  [2-buffer, n = 128]  (:381-457)
+//   grad_mat = -(V^T G) V^T                                     (:469-573)
+// Matrices are zero-padded to NP = 16*ceil(n/16) (the reference's N_MAX
+// buckets, :677-688); the padding stays exactly zero through the iteration.
+//
+// Mapping: one workgroup per matrix, NP/16 waves; wave w owns output rows
+// [16w, 16w+16) and all NP/16 column tiles, one v_mfma_f32_16x16x4_f32
+// accumulator (4 VGPRs) per 16x16 tile. MFMA 16x16x4 operand layout (wave64):
+//   A[i][k]: lane = i + 16k     B[k][j]: lane = j + 16k
+//   D[i][j]: lane = j + 16*(i/4), register i%4.
+#include <algorithm>
+
+#include "lf_common.h"
+#include "lf_internal.h"
+
+namespace lfamd {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int NP> struct NsLayout {
+  static constexpr int NT = NP / 16;       // tiles per dimension = waves per workgroup
+  static constexpr int LS = NP + 4;        // LDS row stride (floats)
+  static constexpr int ELEMS = NP * LS;
+  static constexpr int THREADS = NT * 64;
+};
+
+// acc[t] = X(rows of this wave) * Y(:, tile t), X and Y row-major in LDS.
+// TRANS_X: X is read transposed (X[i][k] := Xs[k][i]); TRANS_Y likewise.
+template <int NP, bool TRANS_X, bool TRANS_Y>
+__device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, const float* __restrict__ Ys,
+                                              int wave, int lane, v4f (&acc)[NP / 16]) {
+  using L = NsLayout<NP>;
+  const int li = lane & 15, lk = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < L::NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int k0 = 0; k0 < NP; k0 += 4) {
+    const int k = k0 + lk;
+    const int i = 16 * wave + li;
+    const float a = TRANS_X ? Xs[k * L::LS + i] : Xs[i * L::LS + k];
+#pragma unroll
+    for (int t = 0; t < L::NT; ++t) {
+      const int j = 16 * t + li;
+      const float b = TRANS_Y ? Ys[j * L::LS + k] : Ys[k * L::LS + j];
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[t], 0, 0, 0);
+    }
+  }
+}
+
+// Element (r) of tile t held by this lane: row 16*wave + 4*(lane/16) + r, col 16t + lane%16.
+template <int NP>
+__device__ __forceinline__ void store_strip(float* __restrict__ Ds, int wave, int lane, const v4f (&acc)[NP / 16]) {
+  using L = NsLayout<NP>;
+#pragma unroll
+  for (int t = 0; t < L::NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      Ds[(16 * wave + 4 * (lane >> 4) + r) * L::LS + 16 * t + (lane & 15)] = acc[t][r];
+}
+
+// V <- 2V - U on this wave's strip.
+template <int NP>
+__device__ __forceinline__ void update_strip(float* __restrict__ Vs, int wave, int lane, const v4f (&acc)[NP / 16]) {
+  using L = NsLayout<NP>;
+#pragma unroll
+  for (int t = 0; t < L::NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* p = &Vs[(16 * wave + 4 * (lane >> 4) + r) * L::LS + 16 * t + (lane & 15)];
+      *p = 2.0f * (*p) - acc[t][r];
+    }
+}
+
+// P = f32(mat) + 0.01 I on the live n x n block; zero padding elsewhere when `pad`.
+template <typename T, int NP>
+__device__ __forceinline__ void load_P(float* __restrict__ Ps, const T* __restrict__ M, int n, bool pad) {
+  using L = NsLayout<NP>;
+  if (pad)
+    for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Ps[e] = 0.f;
+  if (pad) __syncthreads();
+  for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
+    const int i = e / n, j = e - i * n;
+    Ps[i * L::LS + j] = to_acc(M[e]) + (i == j ? 0.01f : 0.f);
+  }
+}
+
+// alpha = 1.8 / (max_i sum_j P_ij)^2; row sums in ascending j, one thread per row.
+template <int NP>
+__device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int n, float* __restrict__ red) {
+  using L = NsLayout<NP>;
+  const int tid = threadIdx.x;
+  float row = -1e30f;
+  if (tid < n) {
+    float s = 0.f;
+    for (int j = 0; j < n; ++j) s += Ps[tid * L::LS + j];
+    row = s;
+  }
+  for (int off = 32; off > 0; off >>= 1) row = fmaxf(row, __shfl_xor(row, off));
+  if ((tid & 63) == 0) red[tid >> 6] = row;
+  __syncthreads();
+  float m = red[0];
+  for (int w = 1; w < L::NT; ++w) m = fmaxf(m, red[w]);
+  return 1.8f / (m * m);
+}
+
+template <typename T, int NP, bool THREE_BUF>
+__global__ void __launch_bounds__(NP * 4)
+newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
+  using L = NsLayout<NP>;
+  extern __shared__ __align__(16) float nsm[];
+  __shared__ float red[8];
+  float* Ps = nsm;                 // P (2-buffer: P, then W = VP)
+  float* Vs = nsm + L::ELEMS;      // V
+  float* Ts = nsm + 2 * L::ELEMS;  // T = PV (3-buffer only)
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const T* Mg = mat + (size_t)blockIdx.x * n * n;
+  T* Og = out + (size_t)blockIdx.x * n * n;
+  const bool pad = n < NP;
+
+  if (pad)
+    for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = 0.f;
+  load_P<T, NP>(Ps, Mg, n, pad);
+  __syncthreads();
+  const float alpha = compute_alpha<NP>(Ps, n, red);
+  for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = Ps[e] * alpha;
+  __syncthreads();
+
+  v4f acc[L::NT];
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (THREE_BUF) {
+      mfma_rowstrip<NP, false, false>(Ps, Vs, wave, lane, acc);  // T = P V
+      store_strip<NP>(Ts, wave, lane, acc);
+      __syncthreads();
+      mfma_rowstrip<NP, false, false>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
+      update_strip<NP>(Vs, wave, lane, acc);                      // V = 2V - U
+      __syncthreads();
+    } else {
+      mfma_rowstrip<NP, false, false>(Vs, Ps, wave, lane, acc);  // W = V P
+      __syncthreads();                                            // P reads done
+      store_strip<NP>(Ps, wave, lane, acc);
+      __syncthreads();
+      mfma_rowstrip<NP, false, false>(Ps, Vs, wave, lane, acc);  // U = W V
+      __syncthreads();                                            // V reads done
+      update_strip<NP>(Vs, wave, lane, acc);
+      if (it + 1 < iters) load_P<T, NP>(Ps, Mg, n, false);        // padding of slot P is still zero
+      __syncthreads();
+    }
+  }
+  for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
+    const int i = e / n, j = e - i * n;
+    Og[e] = from_acc<T>(Vs[i * L::LS + j]);
+  }
+}
+
+template <typename T, int NP>
+__global__ void __launch_bounds__(NP * 4)
+newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __restrict__ gmat, int n) {
+  using L = NsLayout<NP>;
+  extern __shared__ __align__(16) float nsm[];
+  float* Vs = nsm;
+  float* Gs = nsm + L::ELEMS;  // G, then S = V^T G
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const size_t off = (size_t)blockIdx.x * n * n;
+  if (n < NP)
+    for (int e = threadIdx.x; e < 2 * L::ELEMS; e += L::THREADS) nsm[e] = 0.f;
+  __syncthreads();
+  for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
+    const int i = e / n, j = e - i * n;
+    Vs[i * L::LS + j] = to_acc(inv[off + e]);
+    Gs[i * L::LS + j] = to_acc(gout[off + e]);
+  }
+  __syncthreads();
+  v4f acc[L::NT];
+  mfma_rowstrip<NP, true, false>(Vs, Gs, wave, lane, acc);  // S = V^T G
+  __syncthreads();
+  store_strip<NP>(Gs, wave, lane, acc);
+  __syncthreads();
+  mfma_rowstrip<NP, false, true>(Gs, Vs, wave, lane, acc);  // R = S V^T
+#pragma unroll
+  for (int t = 0; t < L::NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * wave + 4 * (lane >> 4) + r, j = 16 * t + (lane & 15);
+      if (i < n && j < n) gmat[off + (size_t)i * n + j] = from_acc<T>(-acc[t][r]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp64: VALU products, 2-buffer (VP)V order, one workgroup of 256 threads per
+// matrix. Slot A holds P, then W = VP; P is reloaded each iteration.
+// ---------------------------------------------------------------------------
+constexpr int kF64Threads = 256;
+
+__device__ __forceinline__ void f64_matmul(const double* X, const double* Y, int np, int ls,
+                                           bool transX, bool transY, double* outv, int perThread) {
+  for (int q = 0; q < perThread; ++q) {
+    const int e = threadIdx.x + q * kF64Threads;
+    double s = 0.0;
+    if (e < np * np) {
+      const int i = e / np, j = e - i * np;
+      for (int k = 0; k < np; ++k) {
+        const double x = transX ? X[k * ls + i] : X[i * ls + k];
+        const double y = transY ? Y[j * ls + k] : Y[k * ls + j];
+        s = fma(x, y, s);
+      }
+    }
+    outv[q] = s;
+  }
+}
+
+constexpr int kF64MaxPer = 37;  // ceil(96*96 / 256)
+
+__global__ void __launch_bounds__(kF64Threads)
+newton_fwd_f64_kernel(const double* __restrict__ mat, double* __restrict__ out, int n, int np, int iters) {
+  extern __shared__ __align__(16) double dsm[];
+  __shared__ double redd[kF64Threads / 64];
+  const int ls = np + 1, elems = np * ls;
+  double* As = dsm;
+  double* Vs = dsm + elems;
+  const double* Mg = mat + (size_t)blockIdx.x * n * n;
+  double* Og = out + (size_t)blockIdx.x * n * n;
+  const int per = (np * np + kF64Threads - 1) / kF64Threads;
+  auto loadP = [&]() {
+    for (int e = threadIdx.x; e < n * n; e += kF64Threads) {
+      const int i = e / n, j = e - i * n;
+      As[i * ls + j] = Mg[e] + (i == j ? 0.01 : 0.0);
+    }
+  };
+  for (int e = threadIdx.x; e < 2 * elems; e += kF64Threads) dsm[e] = 0.0;
+  __syncthreads();
+  loadP();
+  __syncthreads();
+  double row = -1e300;
+  if ((int)threadIdx.x < n) {
+    double s = 0.0;
+    for (int j = 0; j < n; ++j) s += As[threadIdx.x * ls + j];
+    row = s;
+  }
+  for (int o = 32; o > 0; o >>= 1) row = fmax(row, __shfl_xor(row, o));
+  if ((threadIdx.x & 63) == 0) redd[threadIdx.x >> 6] = row;
+  __syncthreads();
+  double m = redd[0];
+  for (int w = 1; w < kF64Threads / 64; ++w) m = fmax(m, redd[w]);
+  const double alpha = 1.8 / (m * m);
+  for (int e = threadIdx.x; e < elems; e += kF64Threads) Vs[e] = As[e] * alpha;
+  __syncthreads();
+  double tmp[kF64MaxPer];
+  for (int it = 0; it < iters; ++it) {
+    f64_matmul(Vs, As, np, ls, false, false, tmp, per);  // W = V P
+    __syncthreads();
+    for (int q = 0; q < per; ++q) {
+      const int e = threadIdx.x + q * kF64Threads;
+      if (e < np * np) As[(e / np) * ls + e % np] = tmp[q];
+    }
+    __syncthreads();
+    f64_matmul(As, Vs, np, ls, false, false, tmp, per);  // U = W V
+    __syncthreads();
+    for (int q = 0; q < per; ++q) {
+      const int e = threadIdx.x + q * kF64Threads;
+      if (e < np * np) {
+        double* p = &Vs[(e / np) * ls + e % np];
+        *p = 2.0 * (*p) - tmp[q];
+      }
+    }
+    // Restore P in slot A (padding rows/cols of W are zero already).
+    if (it + 1 < iters) loadP();
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < n * n; e += kF64Threads) Og[e] = Vs[(e / n) * ls + e % n];
+}
+
+__global__ void __launch_bounds__(kF64Threads)
+newton_bwd_f64_kernel(const double* __restrict__ gout, const double* __restrict__ inv,
+                      double* __restrict__ gmat, int n, int np) {
+  extern __shared__ __align__(16) double dsm[];
+  const int ls = np + 1, elems = np * ls;
+  double* Vs = dsm;
+  double* Gs = dsm + elems;
+  const size_t off = (size_t)blockIdx.x * n * n;
+  const int per = (np * np + kF64Threads - 1) / kF64Threads;
+  for (int e = threadIdx.x; e < 2 * elems; e += kF64Threads) dsm[e] = 0.0;
+  __syncthreads();
+  for (int e = threadIdx.x; e < n * n; e += kF64Threads) {
+    Vs[(e / n) * ls + e % n] = inv[off + e];
+    Gs[(e / n) * ls + e % n] = gout[off + e];
+  }
+  __syncthreads();
+  double tmp[kF64MaxPer];
+  f64_matmul(Vs, Gs, np, ls, true, false, tmp, per);  // S = V^T G
+  __syncthreads();
+  for (int q = 0; q < per; ++q) {
+    const int e = threadIdx.x + q * kF64Threads;
+    if (e < np * np) Gs[(e / np) * ls + e % np] = tmp[q];
+  }
+  __syncthreads();
+  f64_matmul(Gs, Vs, np, ls, false, true, tmp, per);  // R = S V^T
+  for (int q = 0; q < per; ++q) {
+    const int e = threadIdx.x + q * kF64Threads;
+    if (e < np * np) {
+      const int i = e / np, j = e - i * np;
+      if (i < n && j < n) gmat[off + (size_t)i * n + j] = -tmp[q];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kMaxN = 128;
+constexpr int kF64MaxN = 96;  // two fp64 96x97 buffers fill most of gfx950's 160 KB LDS
+
+int bucket(int64_t n) { return (int)((n + 15) / 16) * 16; }
+
+template <int NP> constexpr size_t fwd_lds(bool three) { return (three ? 3 : 2) * (size_t)NsLayout<NP>::ELEMS * 4; }
+
+template <typename Kern>
+int set_lds(Kern k, size_t bytes) {
+  if (bytes > (size_t)max_lds_bytes())
+    return fail(LFAMD_ERR_UNSUPPORTED, "NewtonInverse needs %zu bytes of LDS, device allows %d", bytes, max_lds_bytes());
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
+    return fail(LFAMD_ERR_HIP, "hipFuncSetAttribute failed");
+  return LFAMD_OK;
+}
+
+template <typename T, int NP>
+int fwd_np(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
+  // Mirrors the reference's buffer choice: 3 buffers unless they do not fit.
+  const bool three = NP < 128 && fwd_lds<NP>(true) <= (size_t)max_lds_bytes();
+  if (three) {
+    auto k = newton_fwd_kernel<T, NP, true>;
+    int s = set_lds(k, fwd_lds<NP>(true));
+    if (s) return s;
+    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4), fwd_lds<NP>(true), st, m, o, n, iters);
+  } else {
+    auto k = newton_fwd_kernel<T, NP, false>;
+    int s = set_lds(k, fwd_lds<NP>(false));
+    if (s) return s;
+    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4), fwd_lds<NP>(false), st, m, o, n, iters);
+  }
+  return check_launch("newton forward");
+}
+
+template <typename T, int NP>
+int bwd_np(const T* g, const T* v, T* o, int64_t bh, int n, hipStream_t st) {
+  auto k = newton_bwd_kernel<T, NP>;
+  const size_t lds = 2 * (size_t)NsLayout<NP>::ELEMS * 4;
+  int s = set_lds(k, lds);
+  if (s) return s;
+  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4), lds, st, g, v, o, n);
+  return check_launch("newton backward");
+}
+
+template <typename T>
+int fwd_t(const void* m, void* o, int64_t bh, int n, int iters, hipStream_t st) {
+  auto M = static_cast<const T*>(m);
+  auto O = static_cast<T*>(o);
+  switch (bucket(n)) {
+    case 16: return fwd_np<T, 16>(M, O, bh, n, iters, st);
+    case 32: return fwd_np<T, 32>(M, O, bh, n, iters, st);
+    case 48: return fwd_np<T, 48>(M, O, bh, n, iters, st);
+    case 64: return fwd_np<T, 64>(M, O, bh, n, iters, st);
+    case 80: return fwd_np<T, 80>(M, O, bh, n, iters, st);
+    case 96: return fwd_np<T, 96>(M, O, bh, n, iters, st);
+    case 112: return fwd_np<T, 112>(M, O, bh, n, iters, st);
+    default: return fwd_np<T, 128>(M, O, bh, n, iters, st);
+  }
+}
+
+template <typename T>
+int bwd_t(const void* g, const void* v, void* o, int64_t bh, int n, hipStream_t st) {
+  auto G = static_cast<const T*>(g);
+  auto V = static_cast<const T*>(v);
+  auto O = static_cast<T*>(o);
+  switch (bucket(n)) {
+    case 16: return bwd_np<T, 16>(G, V, O, bh, n, st);
+    case 32: return bwd_np<T, 32>(G, V, O, bh, n, st);
+    case 48: return bwd_np<T, 48>(G, V, O, bh, n, st);
+    case 64: return bwd_np<T, 64>(G, V, O, bh, n, st);
+    case 80: return bwd_np<T, 80>(G, V, O, bh, n, st);
+    case 96: return bwd_np<T, 96>(G, V, O, bh, n, st);
+    case 112: return bwd_np<T, 112>(G, V, O, bh, n, st);
+    default: return bwd_np<T, 128>(G, V, O, bh, n, st);
+  }
+}
+
+int check_common(int dtype, int64_t bh, int64_t n, const char* who) {
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dtype);
+  if (bh < 0 || n < 0) return fail(LFAMD_ERR_ARG, "%s: negative size", who);
+  if (n < 1 || n > kMaxN)
+    return fail(LFAMD_ERR_UNSUPPORTED, "NewtonInverse: N=%lld is not supported on this device (insufficient smem or out of range)", (long long)n);
+  if (bh > INT32_MAX) return fail(LFAMD_ERR_UNSUPPORTED, "%s: too many matrices", who);
+  if (dtype == LFAMD_F64 && n > kF64MaxN)
+    return fail(LFAMD_ERR_UNSUPPORTED, "NewtonInverse: fp64 N=%lld needs more LDS than this device allows (fp64 limit %d)", (long long)n, kF64MaxN);
+  return LFAMD_OK;
+}
+
+}  // namespace
+}  // namespace lfamd
+
+using namespace lfamd;
+
+extern "C" {
+
+int lfamd_newton_is_supported(int64_t n) { return n >= 1 && n <= kMaxN ? 1 : 0; }
+
+int lfamd_newton_forward(int dtype, const void* mat, void* output, int64_t batch_heads,
+                         int64_t n, int iters, void* stream) {
+  int s = check_common(dtype, batch_heads, n, "newton forward");
+  if (s) return s;
+  if (batch_heads == 0) return ok();
+  if (!mat || !output) return fail(LFAMD_ERR_ARG, "newton forward: null pointer");
+  if (iters < 0) iters = 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LFAMD_F32: return fwd_t<float>(mat, output, batch_heads, (int)n, iters, st);
+    case LFAMD_F16: return fwd_t<f16s>(mat, output, batch_heads, (int)n, iters, st);
+    case LFAMD_BF16: return fwd_t<bf16s>(mat, output, batch_heads, (int)n, iters, st);
+    default: {
+      const int np = bucket(n);
+      const size_t lds = 2 * (size_t)np * (np + 1) * 8;
+      if ((s = set_lds(newton_fwd_f64_kernel, lds))) return s;
+      hipLaunchKernelGGL(newton_fwd_f64_kernel, dim3((unsigned)batch_heads), dim3(kF64Threads), lds, st,
+                         static_cast<const double*>(mat), static_cast<double*>(output), (int)n, np, iters);
+      return check_launch("newton forward fp64");
+    }
+  }
+}
+
+int lfamd_newton_backward(int dtype, const void* grad_output, const void* inverse,
+                          void* grad_mat, int64_t batch_heads, int64_t n, void* stream) {
+  int s = check_common(dtype, batch_heads, n, "newton backward");
+  if (s) return s;
+  if (batch_heads == 0) return ok();
+  if (!grad_output || !inverse || !grad_mat) return fail(LFAMD_ERR_ARG, "newton backward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LFAMD_F32: return bwd_t<float>(grad_output, inverse, grad_mat, batch_heads, (int)n, st);
+    case LFAMD_F16: return bwd_t<f16s>(grad_output, inverse, grad_mat, batch_heads, (int)n, st);
+    case LFAMD_BF16: return bwd_t<bf16s>(grad_output, inverse, grad_mat, batch_heads, (int)n, st);
+    default: {
+      const int np = bucket(n);
+      const size_t lds = 2 * (size_t)np * (np + 1) * 8;
+      if ((s = set_lds(newton_bwd_f64_kernel, lds))) return s;
+      hipLaunchKernelGGL(newton_bwd_f64_kernel, dim3((unsigned)batch_heads), dim3(kF64Threads), lds, st,
+                         static_cast<const double*>(grad_output), static_cast<const double*>(inverse),
+                         static_cast<double*>(grad_mat), (int)n, np);
+      return check_launch("newton backward fp64");
+    }
+  }
+}
+
+}  // extern "C"

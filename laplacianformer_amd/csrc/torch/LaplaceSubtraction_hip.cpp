@@ -1,0 +1,121 @@
+// Host adapters of LaplaceSubtraction: reference input contract, then the C ABI
+// of include/laplacianformer_amd.h on the tensor's device and current stream.
+//
+// Mirrors src/LaplaceSubtraction_cuda.cu:12-116 (shape_check and size
+// extraction: B=q.size(0), H=q.size(1), N=q.size(2), M=k.size(3), C=q.size(3)).
+// Stricter than the reference: output / gradient tensors are also checked for
+// shape, dtype and device (the reference writes through them unchecked), and a
+// non-contiguous grad_output is made contiguous instead of being read raw.
+#include "LaplaceSubtraction.h"
+
+#include "torch_common.h"
+
+namespace laplace {
+
+void shape_check(const at::Tensor& query, const at::Tensor& key) {
+  TORCH_CHECK(query.ndimension() == 4,
+              "4D weight tensor (batch size, head number, sequence length, channel) expected, but got: ",
+              query.ndimension());
+  TORCH_CHECK(key.ndimension() == 4,
+              "4D weight tensor (batch size, head number, sequence length, channel) expected, but got: ",
+              key.ndimension());
+  TORCH_CHECK(query.is_contiguous(), "query tensor has to be contiguous");
+  TORCH_CHECK(key.is_contiguous(), "key tensor has to be contiguous");
+  TORCH_CHECK(query.size(0) == key.size(0) && query.size(1) == key.size(1) && query.size(3) == key.size(2),
+              "query and key must match their size");
+}
+
+namespace {
+
+struct Sizes {
+  int64_t B, H, N, M, C;
+};
+
+Sizes sizes_of(const at::Tensor& query, const at::Tensor& key) {
+  return Sizes{query.size(0), query.size(1), query.size(2), key.size(3), query.size(3)};
+}
+
+void check_out(const at::Tensor& ref, const at::Tensor& t, at::IntArrayRef shape, const char* name) {
+  detail::same_type(ref, t, name);
+  TORCH_CHECK(t.sizes() == shape, name, " must have shape ", shape, " but has ", t.sizes());
+  TORCH_CHECK(t.is_contiguous(), name, " has to be contiguous");
+}
+
+}  // namespace
+
+void LaplaceSubtraction_forward_cuda(const at::Tensor query, const at::Tensor key, at::Tensor output) {
+  shape_check(query, key);
+  const int dt = detail::abi_dtype(query, "laplace_forward_tiled");
+  detail::same_type(query, key, "key");
+  const Sizes s = sizes_of(query, key);
+  check_out(query, output, {s.B, s.H, s.N, s.M}, "output");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  detail::check_status(lfamd_laplace_forward(dt, query.data_ptr(), key.data_ptr(), output.data_ptr(), s.B,
+                                             s.H, s.N, s.M, s.C, detail::stream_of(query)));
+}
+
+void LaplaceSubtraction_backward_query_cuda(const at::Tensor gradOutput, const at::Tensor query,
+                                            const at::Tensor key, at::Tensor gradQuery) {
+  shape_check(query, key);
+  const int dt = detail::abi_dtype(query, "laplace_backward_query_tiled");
+  detail::same_type(query, key, "key");
+  const Sizes s = sizes_of(query, key);
+  check_out(query, gradQuery, {s.B, s.H, s.N, s.C}, "gradQuery");
+  detail::same_type(query, gradOutput, "gradOutput");
+  TORCH_CHECK(gradOutput.sizes() == at::IntArrayRef({s.B, s.H, s.N, s.M}), "gradOutput must have shape [B,H,N,M]");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  const at::Tensor g = gradOutput.contiguous();
+  detail::check_status(lfamd_laplace_backward_query(dt, g.data_ptr(), query.data_ptr(), key.data_ptr(),
+                                                    gradQuery.data_ptr(), s.B, s.H, s.N, s.M, s.C,
+                                                    detail::stream_of(query)));
+}
+
+namespace {
+void backward_impl(const at::Tensor& gradOutput, const at::Tensor& query, const at::Tensor& key,
+                   at::Tensor* gradQuery, at::Tensor* gradKey, const char* op) {
+  shape_check(query, key);
+  const int dt = detail::abi_dtype(query, op);
+  detail::same_type(query, key, "key");
+  const Sizes s = sizes_of(query, key);
+  if (gradQuery) check_out(query, *gradQuery, {s.B, s.H, s.N, s.C}, "gradQuery");
+  check_out(query, *gradKey, {s.B, s.H, s.C, s.M}, "gradKey");
+  detail::same_type(query, gradOutput, "gradOutput");
+  TORCH_CHECK(gradOutput.sizes() == at::IntArrayRef({s.B, s.H, s.N, s.M}), "gradOutput must have shape [B,H,N,M]");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  const at::Tensor g = gradOutput.contiguous();
+  const size_t ws_bytes = lfamd_laplace_backward_workspace_size(dt, s.B, s.H, s.N, s.M, s.C);
+  at::Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, query.options().dtype(at::kByte));
+  void* stream = detail::stream_of(query);
+  if (gradQuery)
+    detail::check_status(lfamd_laplace_backward(dt, g.data_ptr(), query.data_ptr(), key.data_ptr(),
+                                                gradQuery->data_ptr(), gradKey->data_ptr(), s.B, s.H, s.N,
+                                                s.M, s.C, ws.data_ptr(), ws_bytes, stream));
+  else
+    detail::check_status(lfamd_laplace_backward_key(dt, g.data_ptr(), query.data_ptr(), key.data_ptr(),
+                                                    gradKey->data_ptr(), s.B, s.H, s.N, s.M, s.C,
+                                                    ws.data_ptr(), ws_bytes, stream));
+}
+}  // namespace
+
+void LaplaceSubtraction_backward_key_cuda(const at::Tensor gradOutput, const at::Tensor query,
+                                          const at::Tensor key, at::Tensor gradKey) {
+  backward_impl(gradOutput, query, key, nullptr, &gradKey, "laplace_backward_key_tiled");
+}
+
+void LaplaceSubtraction_backward_cuda(const at::Tensor gradOutput, const at::Tensor query, const at::Tensor key,
+                                      at::Tensor gradQuery, at::Tensor gradKey) {
+  backward_impl(gradOutput, query, key, &gradQuery, &gradKey, "laplace_backward_fused");
+}
+
+void LaplaceSubtraction_reduce_forward_cuda(const at::Tensor query, const at::Tensor key, at::Tensor output) {
+  shape_check(query, key);
+  const int dt = detail::abi_dtype(query, "subtraction_reduce_laplace_forward_cuda");
+  detail::same_type(query, key, "key");
+  const Sizes s = sizes_of(query, key);
+  check_out(query, output, {s.B, s.H, s.N, s.M}, "output");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  detail::check_status(lfamd_laplace_reduce_forward(dt, query.data_ptr(), key.data_ptr(), output.data_ptr(),
+                                                    s.B, s.H, s.N, s.M, s.C, detail::stream_of(query)));
+}
+
+}  // namespace laplace

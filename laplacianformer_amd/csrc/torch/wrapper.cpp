@@ -1,0 +1,57 @@
+// pybind11 module of the MI355X build. Same module name and the same ten
+// exports as the reference module (src/wrapper.cpp:73-99), plus the fused
+// backward LaplaceSubtraction_backward.
+#include <torch/extension.h>
+
+#include <sstream>
+#include <string>
+
+#include "../../../include/laplacianformer_amd.h"
+#include "LaplaceSubtraction.h"
+#include "NewtonInverse.h"
+
+namespace laplace {
+
+// HIP runtime version as major*100 + minor (reference src/cuda_version.cu:16-20).
+int get_cudart_version() { return lfamd_runtime_version(); }
+
+// "HIP " followed by the version printed the way the reference prints it
+// (src/wrapper.cpp:14-37: v/1000 "." v/10%100 ["." v%10]).
+std::string get_cuda_version() {
+  std::ostringstream oss;
+  oss << "HIP ";
+  const int v = get_cudart_version();
+  oss << (v / 1000) << "." << (v / 10 % 100);
+  if (v % 10 != 0) oss << "." << (v % 10);
+  return oss.str();
+}
+
+// True only for a CUDA build (reference src/wrapper.cpp:39-45): false here.
+bool has_cuda() { return false; }
+
+std::string get_compiler_version() {
+  std::ostringstream ss;
+#if defined(__clang_major__)
+  ss << "clang " << __clang_major__ << "." << __clang_minor__ << "." << __clang_patchlevel__;
+#elif defined(__GNUC__)
+  ss << "GCC " << __GNUC__ << "." << __GNUC_MINOR__;
+#endif
+  return ss.str();
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("get_compiler_version", &get_compiler_version, "get_compiler_version");
+  m.def("get_cuda_version", &get_cuda_version, "get_cuda_version");
+  m.def("has_cuda", &has_cuda, "has_cuda");
+  m.def("LaplaceSubtraction_forward", &LaplaceSubtraction_forward, "LaplaceSubtraction_forward");
+  m.def("LaplaceSubtraction_backward_query", &LaplaceSubtraction_backward_query, "LaplaceSubtraction_backward_query");
+  m.def("LaplaceSubtraction_backward_key", &LaplaceSubtraction_backward_key, "LaplaceSubtraction_backward_key");
+  m.def("LaplaceSubtraction_reduce_forward", &LaplaceSubtraction_reduce_forward, "LaplaceSubtraction_reduce_forward");
+  m.def("NewtonInverse_forward", &NewtonInverse_forward, "NewtonInverse_forward (mat, output, iter)");
+  m.def("NewtonInverse_backward", &NewtonInverse_backward, "NewtonInverse_backward (grad_output, inverse, grad_mat)");
+  m.def("NewtonInverse_is_supported", &NewtonInverse_is_supported, "NewtonInverse_is_supported (N)");
+  m.def("LaplaceSubtraction_backward", &LaplaceSubtraction_backward,
+        "LaplaceSubtraction_backward (gradOutput, query, key, gradQuery, gradKey): fused dq+dk");
+}
+
+}  // namespace laplace

@@ -1,0 +1,81 @@
+"""Autograd wrappers over the drop-in extension.
+
+The reference ships the raw out-parameter ops only (its autograd glue is not in
+the repository); these Functions pair forward with backward the way a model
+uses them: LaplaceSubtraction forward (reference src/wrapper.cpp:81-82) with
+the fused dq+dk backward (one pass; equal to backward_query + backward_key,
+src/wrapper.cpp:84-88), and NewtonInverse forward with its -V^T G V^T backward
+(src/wrapper.cpp:93-96).
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import ext
+
+
+class LaplaceSubtractionFunction(torch.autograd.Function):
+    """dist[b,h,i,j] = sum_c |query[b,h,i,c] - key[b,h,c,j]| with key channel-major."""
+
+    @staticmethod
+    def forward(ctx, query: torch.Tensor, key: torch.Tensor) -> torch.Tensor:
+        query = query.contiguous()
+        key = key.contiguous()
+        B, H, N, _ = query.shape
+        M = key.shape[3]
+        out = torch.empty((B, H, N, M), dtype=query.dtype, device=query.device)
+        ext().LaplaceSubtraction_forward(query, key, out)
+        ctx.save_for_backward(query, key)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        query, key = ctx.saved_tensors
+        grad = grad.contiguous()
+        need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dq = torch.empty_like(query) if need_q else None
+        dk = torch.empty_like(key) if need_k else None
+        if need_q and need_k:
+            ext().LaplaceSubtraction_backward(grad, query, key, dq, dk)
+        elif need_q:
+            ext().LaplaceSubtraction_backward_query(grad, query, key, dq)
+        elif need_k:
+            ext().LaplaceSubtraction_backward_key(grad, query, key, dk)
+        return dq, dk
+
+
+class NewtonInverseFunction(torch.autograd.Function):
+    """Newton-Schulz approximate inverse of mat + 0.01 I; backward -V^T G V^T."""
+
+    @staticmethod
+    def forward(ctx, mat: torch.Tensor, iters: int) -> torch.Tensor:
+        mat = mat.contiguous()
+        out = torch.empty_like(mat)
+        ext().NewtonInverse_forward(mat, out, int(iters))
+        ctx.save_for_backward(out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        (inv,) = ctx.saved_tensors
+        dmat = torch.empty_like(inv)
+        ext().NewtonInverse_backward(grad.contiguous(), inv, dmat)
+        return dmat, None
+
+
+def laplace_subtraction(query: torch.Tensor, key: torch.Tensor, key_layout: str = "cm") -> torch.Tensor:
+    """Pairwise L1 distance with autograd.
+
+    ``key_layout="cm"`` takes the reference's channel-major key ``[B,H,C,M]``;
+    ``"mc"`` takes ``[B,H,M,C]`` and transposes it (one copy).
+    """
+    if key_layout == "mc":
+        key = key.transpose(-1, -2)
+    elif key_layout != "cm":
+        raise ValueError("key_layout must be 'cm' or 'mc'")
+    return LaplaceSubtractionFunction.apply(query, key)
+
+
+def newton_inverse(mat: torch.Tensor, iters: int) -> torch.Tensor:
+    """Newton-Schulz inverse with autograd; mat is ``[B,H,n,n]``, 1 <= n <= 128."""
+    return NewtonInverseFunction.apply(mat, iters)

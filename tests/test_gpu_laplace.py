@@ -1,0 +1,215 @@
+"""GPU parity of LaplaceSubtraction against the CPU oracle (drop-in module and C ABI)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lfcheck import TORCH_DT, assert_bitwise, assert_l1_close, check_l1, gen, l1_refs
+
+pytestmark = pytest.mark.gpu
+
+# (B, H, N, M, C): reference-config shapes, tile tails, one-element and channel-split cases.
+SHAPES = [
+    (2, 2, 196, 49, 32),
+    (1, 1, 1, 1, 1),
+    (1, 1, 63, 7, 5),
+    (2, 1, 65, 17, 64),
+    (1, 3, 130, 64, 65),
+    (1, 1, 64, 65, 16),
+    (1, 2, 100, 100, 33),
+    (1, 1, 129, 256, 64),
+    (2, 1, 96, 48, 130),
+]
+DTYPES = ["f32", "f16", "bf16", "f64"]
+
+
+def _inputs(B, H, N, M, C, dt, seed, integer=None, scale=1.0):
+    q = gen((B, H, N, C), seed, dt, scale, integer)
+    k = gen((B, H, C, M), seed + 1, dt, scale, integer)
+    g = gen((B, H, N, M), seed + 2, dt, 1.0, 4 if integer else None)
+    return q, k, g
+
+
+def _run(dev, q, k, g):
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    qd, kd, gd = q.to(dev), k.to(dev), g.to(dev)
+    B, H, N, C = q.shape
+    M = k.shape[3]
+    out = torch.empty((B, H, N, M), dtype=q.dtype, device=dev)
+    dq = torch.empty_like(qd)
+    dk = torch.empty_like(kd)
+    dq2 = torch.empty_like(qd)
+    dk2 = torch.empty_like(kd)
+    L.LaplaceSubtraction_forward(qd, kd, out)
+    L.LaplaceSubtraction_backward_query(gd, qd, kd, dq)
+    L.LaplaceSubtraction_backward_key(gd, qd, kd, dk)
+    L.LaplaceSubtraction_backward(gd, qd, kd, dq2, dk2)
+    torch.cuda.synchronize()
+    return out, dq, dk, dq2, dk2
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_laplace_parity(gpu, shape, dt):
+    B, H, N, M, C = shape
+    print(f"laplace parity {shape} {dt}", flush=True)
+    q, k, g = _inputs(B, H, N, M, C, dt, seed=1000 + sum(shape))
+    out, dq, dk, dq2, dk2 = _run(gpu, q, k, g)
+    refs = l1_refs(q, k, g, dt)
+    check_l1(out, dq, dk, refs, dt, "separate ")
+    check_l1(out, dq2, dk2, refs, dt, "fused ")
+    # Forward and dq follow the reference's serial order exactly: bit-identical
+    # to the fp32 (fp64 for double) serial oracle.
+    assert_bitwise(out, oracle.laplace_forward(q, k, dt), dt, "forward bits")
+    if M <= 64:
+        assert_bitwise(dq, oracle.laplace_backward_query(g, q, k, dt), dt, "dq bits")
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_laplace_integer_ties(gpu, dt):
+    """Integer inputs: every sum is exact and ties (sgn(0) = 0) are frequent."""
+    B, H, N, M, C = 2, 2, 150, 49, 64
+    print(f"laplace integer ties {dt}", flush=True)
+    q, k, g = _inputs(B, H, N, M, C, dt, seed=77, integer=3)
+    out, dq, dk, dq2, dk2 = _run(gpu, q, k, g)
+    ties = (q.float()[..., :, None, :] == k.float().transpose(-1, -2)[..., None, :, :]).sum().item()
+    assert ties > 1000
+    for got, ref in ((out, oracle.laplace_forward(q, k, dt)), (dq, oracle.laplace_backward_query(g, q, k, dt)),
+                     (dk, oracle.laplace_backward_key(g, q, k, dt)), (dq2, oracle.laplace_backward_query(g, q, k, dt)),
+                     (dk2, oracle.laplace_backward_key(g, q, k, dt))):
+        assert_bitwise(got, ref, dt, "integer exact")
+
+
+def test_laplace_config2_full(gpu):
+    """B=32 H=1 N=3136 M=49 d=64 fp16, fwd + bwd."""
+    B, H, N, M, C = 32, 1, 3136, 49, 64
+    print("laplace config 2 full", flush=True)
+    q = gen((B, H, N, C), 1002, "f16")
+    k = gen((B, H, M, C), 1003, "f16").transpose(-1, -2).contiguous()
+    g = gen((B, H, N, M), 1004, "f16")
+    out, dq, dk, dq2, dk2 = _run(gpu, q, k, g)
+    refs = l1_refs(q, k, g, "f16")
+    check_l1(out, dq, dk, refs, "f16", "separate ")
+    check_l1(out, dq2, dk2, refs, "f16", "fused ")
+    assert_bitwise(out, oracle.laplace_forward(q, k, "f16"), "f16", "forward bits")
+    assert_bitwise(dq, oracle.laplace_backward_query(g, q, k, "f16"), "f16", "dq bits")
+    # Size-independent identity: sum_i dq[i,c] + sum_j dk[c,j] = 0 (exactly, in real arithmetic).
+    s = dq2.double().sum(dim=2) + dk2.double().sum(dim=3)
+    assert s.abs().max().item() < 0.05 * dq2.double().abs().sum(dim=2).max().item() + 1.0
+
+
+def test_laplace_config4_sampled(gpu):
+    """BASELINE config 4 (bf16, B=16 H=8 N=4096 M=256 d=64): full GPU run, oracle on sampled slices."""
+    B, H, N, M, C = 16, 8, 4096, 256, 64
+    print("laplace config 4 sampled", flush=True)
+    q = gen((B, H, N, C), 1004, "bf16", scale=0.5)
+    k = gen((B, H, M, C), 1005, "bf16", scale=0.5).transpose(-1, -2).contiguous()
+    g = gen((B, H, N, M), 1006, "bf16")
+    out, dq, dk, dq2, dk2 = _run(gpu, q, k, g)
+    for b, h in ((0, 0), (7, 3), (15, 7)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        qs, ks, gs = q[sl], k[sl], g[sl]
+        check_l1(out[sl], dq2[sl], dk2[sl], l1_refs(qs, ks, gs, "bf16"), "bf16", f"slice {b},{h} ")
+        assert_bitwise(out[sl], oracle.laplace_forward(qs, ks, "bf16"), "bf16", "forward bits")
+    assert torch.equal(dq.cpu(), dq2.cpu())
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "f64"])
+def test_reduce_forward(gpu, dt):
+    import laplacianformer_amd as lf
+
+    for (B, H, N, M, C) in ((1, 2, 33, 9, 64), (1, 1, 10, 5, 3), (1, 1, 7, 3, 300)):
+        print(f"reduce forward {dt} {(B, H, N, M, C)}", flush=True)
+        q, k, _ = _inputs(B, H, N, M, C, dt, seed=5 + C)
+        out = torch.empty((B, H, N, M), dtype=q.dtype, device=gpu)
+        lf.ext().LaplaceSubtraction_reduce_forward(q.to(gpu), k.to(gpu), out)
+        ref = oracle.laplace_reduce_forward(q, k, dt)
+        got = out.cpu().numpy()
+        assert np.array_equal(got.astype(np.float64), np.asarray(ref, dtype=np.float64)), (dt, C)
+
+
+def test_empty_and_errors(gpu):
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    q = torch.zeros((1, 1, 0, 8), device=gpu)
+    k = torch.zeros((1, 1, 8, 5), device=gpu)
+    out = torch.empty((1, 1, 0, 5), device=gpu)
+    L.LaplaceSubtraction_forward(q, k, out)
+    # Reduction length zero: gradients are zero.
+    q = torch.randn((1, 1, 4, 8), device=gpu)
+    k0 = torch.zeros((1, 1, 8, 0), device=gpu)
+    g0 = torch.zeros((1, 1, 4, 0), device=gpu)
+    dq = torch.full((1, 1, 4, 8), 7.0, device=gpu)
+    L.LaplaceSubtraction_backward_query(g0, q, k0, dq)
+    assert dq.abs().max().item() == 0
+    with pytest.raises(RuntimeError, match="query and key must match"):
+        L.LaplaceSubtraction_forward(q, torch.zeros((1, 1, 7, 5), device=gpu), torch.empty((1, 1, 4, 5), device=gpu))
+    with pytest.raises(RuntimeError, match="contiguous"):
+        L.LaplaceSubtraction_forward(q.transpose(2, 3), k, torch.empty((1, 1, 8, 5), device=gpu))
+    with pytest.raises(RuntimeError, match="not implemented for 'Int'"):
+        L.LaplaceSubtraction_forward(q.int(), k.int(), torch.empty((1, 1, 4, 5), device=gpu, dtype=torch.int32))
+
+
+def test_capi_direct(gpu):
+    """The C ABI called with raw pointers and an explicit stream matches the oracle."""
+    import laplacianformer_amd as lf
+
+    lib = lf.capi()
+    B, H, N, M, C = 2, 1, 200, 49, 64
+    print("capi direct", flush=True)
+    q, k, g = _inputs(B, H, N, M, C, "f16", seed=31)
+    qd, kd, gd = q.to(gpu), k.to(gpu), g.to(gpu)
+    out = torch.empty((B, H, N, M), dtype=torch.float16, device=gpu)
+    dq = torch.empty_like(qd)
+    dk = torch.empty_like(kd)
+    st = torch.cuda.Stream()
+    dt = lf.dtype_code(torch.float16)
+    ws_bytes = lib.lfamd_laplace_backward_workspace_size(dt, B, H, N, M, C)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=gpu)
+    torch.cuda.synchronize()
+    s = ctypes.c_void_p(st.cuda_stream)
+    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out.data_ptr(), B, H, N, M, C, s))
+    lf.check(lib.lfamd_laplace_backward(dt, gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), dq.data_ptr(),
+                                        dk.data_ptr(), B, H, N, M, C, ws.data_ptr(), ws_bytes, s))
+    st.synchronize()
+    assert_bitwise(out, oracle.laplace_forward(q, k, "f16"), "f16")
+    check_l1(out, dq, dk, l1_refs(q, k, g, "f16"), "f16", "capi ")
+    # Too small a workspace is rejected before anything is launched.
+    rc = lib.lfamd_laplace_backward_key(dt, gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), dk.data_ptr(),
+                                        B, H, N, M, C, ws.data_ptr(), 1, s)
+    assert rc == 1 and b"workspace" in lib.lfamd_last_error()
+
+
+def test_repeat_deterministic(gpu):
+    """Repeated backward calls on one stream give identical bits (fixed reduction order,
+    self-resetting counters)."""
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = 4, 2, 700, 49, 64
+    q, k, g = _inputs(B, H, N, M, C, "f32", seed=9)
+    qd, kd, gd = q.to(gpu), k.to(gpu), g.to(gpu)
+    res = []
+    for _ in range(3):
+        dq = torch.empty_like(qd)
+        dk = torch.empty_like(kd)
+        lf.ext().LaplaceSubtraction_backward(gd, qd, kd, dq, dk)
+        res.append((dq.cpu(), dk.cpu()))
+    torch.cuda.synchronize()
+    for a, b in res[1:]:
+        assert torch.equal(a, res[0][0]) and torch.equal(b, res[0][1])
+
+
+def test_autograd_function(gpu):
+    import laplacianformer_amd as lf
+
+    q, k, g = _inputs(1, 2, 90, 49, 32, "f32", seed=3)
+    qd = q.to(gpu).requires_grad_()
+    kd = k.to(gpu).requires_grad_()
+    out = lf.laplace_subtraction(qd, kd)
+    out.backward(g.to(gpu))
+    check_l1(out, qd.grad, kd.grad, l1_refs(q, k, g, "f32"), "f32", "autograd ")

@@ -1,0 +1,127 @@
+"""GPU parity of NewtonInverse against the CPU oracle and closed forms."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lfcheck import TORCH_DT, assert_newton_close, gen
+
+pytestmark = pytest.mark.gpu
+
+
+def gram(bh, n, d, seed, shift=1e-3, scale=1.0):
+    """A = exp(-L1(k_i, k_j) / sqrt(d)) + shift*I from k ~ N(0, scale^2) (BASELINE config recipe)."""
+    k = gen((1, bh, n, d), seed, "f64", scale=scale)
+    D = oracle.laplace_forward(k, k.transpose(-1, -2).contiguous(), "f64")[0]
+    return np.exp(-D / np.sqrt(d)) + shift * np.eye(n)
+
+
+NS = [1, 5, 16, 17, 32, 48, 49, 64, 65, 80, 96, 100, 112, 113, 128]
+
+
+@pytest.mark.parametrize("n", NS)
+@pytest.mark.parametrize("iters", [0, 1, 10])
+def test_newton_forward_f32(gpu, n, iters):
+    import laplacianformer_amd as lf
+
+    print(f"newton forward n={n} iters={iters}", flush=True)
+    A = torch.from_numpy(gram(6, n, 32, seed=n)).float().reshape(2, 3, n, n)
+    out = torch.empty_like(A, device=gpu)
+    lf.ext().NewtonInverse_forward(A.to(gpu), out, iters)
+    ref = oracle.newton_forward(A, iters, "f32")
+    assert_newton_close(out, ref, "f32", f"n={n} it={iters}")
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f64"])
+@pytest.mark.parametrize("n", [16, 49, 64, 96])
+def test_newton_forward_dtypes(gpu, dt, n):
+    import laplacianformer_amd as lf
+
+    print(f"newton forward {dt} n={n}", flush=True)
+    A = torch.from_numpy(gram(4, n, 64, seed=100 + n)).reshape(2, 2, n, n).to(TORCH_DT[dt])
+    out = torch.empty_like(A, device=gpu)
+    lf.ext().NewtonInverse_forward(A.to(gpu), out, 10)
+    ref = oracle.newton_forward(A, 10, dt)
+    assert_newton_close(out, ref, dt, f"{dt} n={n}", rtol=1e-4 if dt != "f64" else 1e-10)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "f64"])
+@pytest.mark.parametrize("n", [1, 16, 17, 49, 64, 65, 96, 128])
+def test_newton_backward(gpu, dt, n):
+    import laplacianformer_amd as lf
+
+    if dt == "f64" and n > 96:
+        pytest.skip("fp64 envelope is n <= 96")
+    print(f"newton backward {dt} n={n}", flush=True)
+    V = gen((2, 2, n, n), 7 + n, dt, scale=0.3)
+    G = gen((2, 2, n, n), 8 + n, dt)
+    out = torch.empty_like(V, device=gpu)
+    lf.ext().NewtonInverse_backward(G.to(gpu), V.to(gpu), out)
+    ref = oracle.newton_backward(G, V, dt)
+    assert_newton_close(out, ref, dt, f"bwd {dt} n={n}", rtol=1e-5 if dt != "f64" else 1e-12)
+
+
+def test_newton_config3(gpu):
+    """1024 matrices 64x64 fp32, 12 iterations, forward + backward."""
+    import laplacianformer_amd as lf
+
+    print("newton config 3", flush=True)
+    A = torch.from_numpy(gram(1024, 64, 64, seed=1003)).float().reshape(1024, 1, 64, 64)
+    G = gen((1024, 1, 64, 64), 1013, "f32")
+    Ad, Gd = A.to(gpu), G.to(gpu)
+    V = torch.empty_like(Ad)
+    dA = torch.empty_like(Ad)
+    lf.ext().NewtonInverse_forward(Ad, V, 12)
+    lf.ext().NewtonInverse_backward(Gd, V, dA)
+    ref = oracle.newton_forward(A, 12, "f32")
+    assert_newton_close(V, ref, "f32", "cfg3 fwd")
+    assert_newton_close(dA, oracle.newton_backward(G, V.cpu(), "f32"), "f32", "cfg3 bwd", rtol=1e-5)
+    # Residual ||P X - I||_F matches the oracle's within 1e-4 * sqrt(n).
+    P = A.double() + 0.01 * torch.eye(64, dtype=torch.float64)
+    r_gpu = torch.linalg.matrix_norm(P @ V.cpu().double() - torch.eye(64, dtype=torch.float64))
+    r_ref = torch.linalg.matrix_norm(P @ torch.from_numpy(ref).double() - torch.eye(64, dtype=torch.float64))
+    assert (r_gpu - r_ref).abs().max().item() <= 1e-4 * 8
+
+
+def test_newton_closed_forms(gpu):
+    """Diagonal A = c I: X_k = (1 - (-0.8)^(2^k)) / mu * I with mu = c + 0.01; and iter = 0 gives alpha P."""
+    import laplacianformer_amd as lf
+
+    for n, c in ((16, 0.5), (49, 2.0), (128, 0.09)):
+        mu = c + 0.01
+        A = (c * torch.eye(n)).reshape(1, 1, n, n).repeat(2, 1, 1, 1)
+        for k in (0, 1, 3, 6):
+            out = torch.empty_like(A, device=gpu)
+            lf.ext().NewtonInverse_forward(A.to(gpu), out, k)
+            expect = (1 - (-0.8) ** (2 ** k)) / mu
+            d = torch.diagonal(out.cpu().double(), dim1=-2, dim2=-1)
+            assert torch.allclose(d, torch.full_like(d, expect), rtol=2e-6), (n, c, k)
+            off = out.cpu().double() - torch.diag_embed(d)
+            assert off.abs().max().item() == 0.0
+
+
+def test_newton_errors(gpu):
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    A = torch.zeros((1, 1, 129, 129), device=gpu)
+    with pytest.raises(RuntimeError, match="N=129 is not supported"):
+        L.NewtonInverse_forward(A, torch.empty_like(A), 3)
+    with pytest.raises(RuntimeError, match="must be 4D"):
+        L.NewtonInverse_forward(torch.zeros((3, 4, 4), device=gpu), torch.empty((3, 4, 4), device=gpu), 3)
+    with pytest.raises(RuntimeError, match="same shape"):
+        L.NewtonInverse_forward(torch.zeros((1, 1, 4, 4), device=gpu), torch.empty((1, 1, 5, 5), device=gpu), 3)
+    assert L.NewtonInverse_is_supported(128) and not L.NewtonInverse_is_supported(129)
+    assert not L.NewtonInverse_is_supported(0)
+
+
+def test_newton_autograd(gpu):
+    import laplacianformer_amd as lf
+
+    A = torch.from_numpy(gram(2, 49, 32, seed=4)).float().reshape(1, 2, 49, 49)
+    Ad = A.to(gpu).requires_grad_()
+    V = lf.newton_inverse(Ad, 10)
+    G = gen((1, 2, 49, 49), 5, "f32")
+    V.backward(G.to(gpu))
+    assert_newton_close(V, oracle.newton_forward(A, 10), "f32")
+    assert_newton_close(Ad.grad, oracle.newton_backward(G, V.detach().cpu()), "f32", rtol=1e-5)
