@@ -38,6 +38,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU timing (approx)")
     p.add_argument("--only", choices=["laplace", "newton", "all"], default="all")
+    p.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                   help="after timing, run one plain device copy of MIB MiB (HBM counter calibration)")
     return p.parse_args()
 
 
@@ -258,6 +260,13 @@ def main():
         if not lap:
             line.update({"value": tf, "unit": "TFLOP/s", "ms_per_step": ns["wall_ms"],
                          "config": {"workload": line["newton"]["workload"]}})
+    if args.calib_copy:
+        src = torch.empty(args.calib_copy << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        line["calib_copy_bytes"] = args.calib_copy << 20
     line["device"] = {"name": props.name, "cus": props.multi_processor_count,
                       "arch": getattr(props, "gcnArchName", "")}
     if lap and ns and not args.no_cpu:

@@ -70,7 +70,7 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
 
 /* grad_key[b,h,c,j] = -sum_i grad_output[b,h,i,j] * sgn(query[b,h,i,c] - key[b,h,c,j]).
  * Deterministic: per-workgroup fp32 partials in `workspace`, summed in a fixed
- * order by the last workgroup of each (b,h) slice, rounded once.
+ * order by a second small kernel on the same stream, rounded once.
  * Replaces laplace::LaplaceSubtraction_backward_key_cuda
  * (reference include/LaplaceSubtraction.h:22-27, src/LaplaceSubtraction_cuda.cu:86-101,
  *  src/LaplaceSubtraction_cuda_kernel.cu:549-609). */

@@ -16,8 +16,9 @@
 // key column held in registers, the grad_output row broadcast from LDS. dq is a
 // lane-local sum over j; dk is a lane-local sum over the wave's rows, reduced
 // across the workgroup's waves in LDS in a fixed order and across workgroups by
-// the last workgroup of each slice (fixed order again), so results are
-// deterministic.
+// a second small kernel (fixed order again), so results are deterministic. A
+// kernel boundary rather than device-scope fences: with one L2 per XCD, an
+// agent-scope release/acquire writes back / invalidates a whole L2.
 #include <algorithm>
 
 #include "lf_common.h"
@@ -204,15 +205,27 @@ template <> struct SignOps<double> {
 
 constexpr int kBwdRB = 8;  // grad_output rows staged per LDS batch
 
+// grad_output as staged in LDS: raw fp16 bits (consumed by v_fma_mix_f32),
+// otherwise the accumulation type.
+template <typename T> struct GStageOf { using type = typename AccOf<T>::type; };
+template <> struct GStageOf<f16s> { using type = uint16_t; };
+__device__ __forceinline__ float gstage(float v) { return v; }
+__device__ __forceinline__ double gstage(double v) { return v; }
+__device__ __forceinline__ float gstage(bf16s v) { return to_acc(v); }
+__device__ __forceinline__ uint16_t gstage(f16s v) { return v.bits; }
+
+template <typename T> constexpr int gstage_vec() { return 16 / (int)sizeof(typename GStageOf<T>::type); }
+
 template <typename T, int JB, bool DQ, bool DK>
 __global__ void __launch_bounds__(512)
 laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
                    const T* __restrict__ key, T* __restrict__ dq, T* __restrict__ dk,
-                   typename AccOf<T>::type* __restrict__ partial, unsigned* __restrict__ counters,
-                   int N, int M, int C, int rowsPerWave) {
+                   typename AccOf<T>::type* __restrict__ partial, int N, int M, int C, int rowsPerWave) {
   using A = typename AccOf<T>::type;
   using SO = SignOps<T>;
-  constexpr int GV = 16 / (int)sizeof(A);
+  using GS = typename GStageOf<T>::type;
+  constexpr bool kHalfG = std::is_same<T, f16s>::value;
+  constexpr int GV = gstage_vec<T>();
   constexpr int JBP = round_up(JB, GV);
 
   const int W = blockDim.x >> 6;
@@ -230,57 +243,112 @@ laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
   const bool multiJ = M > JB;
 
   extern __shared__ __align__(16) unsigned char smem[];
-  A* gsm = reinterpret_cast<A*>(smem);                 // [W][kBwdRB][JBP]
-  A* red = gsm + (size_t)W * kBwdRB * JBP;             // [JB][64]        (DK)
+  GS* gsm = reinterpret_cast<GS*>(smem);               // [W][kBwdRB][JBP]  grad_output rows
+  A* qsm = reinterpret_cast<A*>(gsm + (size_t)W * kBwdRB * JBP);  // [W][kBwdRB][64] scaled query values
+  A* ksm = qsm + (size_t)W * kBwdRB * 64;              // [JB][64]          scaled key tile
+  A* red = ksm + JB * 64;                              // [JB][64]          (DK)
   A* dqp = red + (DK ? JB * 64 : 0);                   // [W][rowsPerWave][64] (DQ && multiJ)
 
   const T* qb = query + (size_t)bh * N * C;
   const T* gb = gout + (size_t)bh * N * M;
   const T* kb = key + (size_t)bh * C * M;
-  A* gw = gsm + (size_t)wave * kBwdRB * JBP;
+  GS* gw = gsm + (size_t)wave * kBwdRB * JBP;
+  A* qw = qsm + (size_t)wave * kBwdRB * 64;
 
   for (int jb0 = 0; jb0 < M; jb0 += JB) {
     const bool lastJ = jb0 + JB >= M;
+    // Key tile [64 channels][JB columns] staged through LDS with coalesced loads,
+    // then each lane keeps its channel's JB scaled values in registers.
+    __syncthreads();  // previous j-block's readers of ksm are done
+    for (int t = threadIdx.x; t < 64 * JB; t += blockDim.x) {
+      const int cl = t / JB, j = t - cl * JB;
+      const int cc = cb * 64 + cl, col = jb0 + j;
+      ksm[j * 64 + cl] = (cc < C && col < M) ? SO::scale(to_acc(kb[(size_t)cc * M + col])) : A(0);
+    }
+    __syncthreads();
     A kreg[JB];
     A dka[JB];
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
-      const int col = jb0 + j;
-      kreg[j] = (cval && col < M) ? SO::scale(to_acc(kb[(size_t)c * M + col])) : A(0);
+      kreg[j] = ksm[j * 64 + lane];
       dka[j] = A(0);
     }
 
-    for (int rb = rowBeg; rb < rowEnd; rb += kBwdRB) {
+    // Software pipeline: the next batch's grad_output elements and query values
+    // are loaded into registers while the current batch is computed from LDS.
+    constexpr int NSTG = ceil_div(kBwdRB * JBP, 64);
+    T gpre[NSTG];
+    T qpre[kBwdRB];
+    auto fetch = [&](int rb) {
       const int nr = min(kBwdRB, rowEnd - rb);
-      for (int e = lane; e < kBwdRB * JBP; e += 64) {
+#pragma unroll
+      for (int s = 0; s < NSTG; ++s) {
+        const int e = lane + 64 * s;
         const int r = e / JBP, jj = e - r * JBP;
         const int col = jb0 + jj;
-        A v = A(0);
-        if (r < nr && jj < JB && col < M) v = to_acc(gb[(size_t)(rb + r) * M + col]);
-        gw[e] = v;
+        gpre[s] = (r < nr && jj < JB && col < M) ? gb[(size_t)(rb + r) * M + col] : T{};
       }
+#pragma unroll
+      for (int r = 0; r < kBwdRB; ++r) qpre[r] = (r < nr && cval) ? qb[(size_t)(rb + r) * C + c] : T{};
+    };
+    if (rowBeg < rowEnd) fetch(rowBeg);
+
+    for (int rb = rowBeg; rb < rowEnd; rb += kBwdRB) {
+      const int nr = min(kBwdRB, rowEnd - rb);
+#pragma unroll
+      for (int s = 0; s < NSTG; ++s) {
+        const int e = lane + 64 * s;
+        if (e < kBwdRB * JBP) gw[e] = gstage(gpre[s]);
+      }
+#pragma unroll
+      for (int r = 0; r < kBwdRB; ++r) qw[r * 64 + lane] = SO::scale(to_acc(qpre[r]));
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (rb + kBwdRB < rowEnd) fetch(rb + kBwdRB);
 
       for (int r = 0; r < nr; ++r) {
         const int i = rb + r;
-        const A qv = cval ? SO::scale(to_acc(qb[(size_t)i * C + c])) : A(0);
+        const A qv = qw[r * 64 + lane];
         A dqa = A(0);
         if (DQ && multiJ && jb0 > 0) dqa = dqp[((size_t)wave * rowsPerWave + (i - rowBeg)) * 64 + lane];
-        const A* gr = gw + r * JBP;
+        const GS* gr = gw + r * JBP;
+        if constexpr (kHalfG) {
+          // 8 halves per 16-byte broadcast read; v_fma_mix_f32 widens them in place.
 #pragma unroll
-        for (int j0 = 0; j0 < JBP; j0 += GV) {
-          A gv[GV];
+          for (int j0 = 0; j0 < JBP; j0 += 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(gr + j0);
+            const uint32_t gw4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-          for (int t = 0; t < GV; ++t) gv[t] = gr[j0 + t];
+            for (int t = 0; t < 8; ++t) {
+              const int j = j0 + t;
+              if (j < JB) {
+                const float s = SO::sgn(qv - kreg[j]);
+                const uint32_t gp = gw4[t >> 1];
+                if (t & 1) {
+                  if (DQ) dqa = mix_fma_fh<1>(s, gp, dqa);
+                  if (DK) dka[j] = mix_fms_fh<1>(s, gp, dka[j]);
+                } else {
+                  if (DQ) dqa = mix_fma_fh<0>(s, gp, dqa);
+                  if (DK) dka[j] = mix_fms_fh<0>(s, gp, dka[j]);
+                }
+              }
+            }
+          }
+        } else {
 #pragma unroll
-          for (int t = 0; t < GV; ++t) {
-            const int j = j0 + t;
-            if (j < JB) {
-              const A s = SO::sgn(qv - kreg[j]);
-              if (DQ) dqa = fma(s, gv[t], dqa);
-              if (DK) dka[j] = fma(s, -gv[t], dka[j]);
+          for (int j0 = 0; j0 < JBP; j0 += GV) {
+            A gv[GV];
+#pragma unroll
+            for (int t = 0; t < GV; ++t) gv[t] = gr[j0 + t];
+#pragma unroll
+            for (int t = 0; t < GV; ++t) {
+              const int j = j0 + t;
+              if (j < JB) {
+                const A s = SO::sgn(qv - kreg[j]);
+                if (DQ) dqa = fma(s, gv[t], dqa);
+                if (DK) dka[j] = fma(s, -gv[t], dka[j]);
+              }
             }
           }
         }
@@ -318,31 +386,26 @@ laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
     }
   }
 
-  if (DK) {
-    // The last workgroup of the slice folds all partials in workgroup order.
-    __shared__ int isLast;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const unsigned prev = atomicAdd(&counters[slice], 1u);
-      isLast = (prev == (unsigned)(nx - 1));
-    }
-    __syncthreads();
-    if (isLast) {
-      __threadfence();
-      const A* pb = partial + (size_t)slice * nx * 64 * M;
-      for (int t = threadIdx.x; t < 64 * M; t += blockDim.x) {
-        const int cl = t / M, j = t - cl * M;
-        const int cc = cb * 64 + cl;
-        if (cc < C) {
-          A s = A(0);
-          for (int x2 = 0; x2 < nx; ++x2) s += pb[(size_t)x2 * 64 * M + t];
-          dk[((size_t)bh * C + cc) * M + j] = from_acc<T>(s);
-        }
-      }
-      if (threadIdx.x == 0) atomicExch(&counters[slice], 0u);
-    }
-  }
+}
+
+// grad_key = sum over the workgroups of a slice of their partial sums, in
+// workgroup order (deterministic). One thread per (channel, column).
+template <typename T>
+__global__ void __launch_bounds__(256)
+laplace_dk_reduce_kernel(const typename AccOf<T>::type* __restrict__ partial, T* __restrict__ dk,
+                         int nx, int M, int C) {
+  using A = typename AccOf<T>::type;
+  const int bh = blockIdx.z, cb = blockIdx.y;
+  const int slice = bh * gridDim.y + cb;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 64 * M) return;
+  const int cl = t / M, j = t - cl * M;
+  const int cc = cb * 64 + cl;
+  if (cc >= C) return;
+  const A* pb = partial + (size_t)slice * nx * 64 * M + t;
+  A s = A(0);
+  for (int x = 0; x < nx; ++x) s += pb[(size_t)x * 64 * M];
+  dk[((size_t)bh * C + cc) * M + j] = from_acc<T>(s);
 }
 
 // ---------------------------------------------------------------------------
@@ -486,11 +549,11 @@ int pick_bwd_jb(int64_t M) {
   return 64;
 }
 
-BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes) {
+BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes, size_t gBytes) {
   BwdPlan p{};
   p.JB = pick_bwd_jb(d.M);
   p.ncb = ceil_div((int)d.C, 64);
-  const int GV = 16 / (int)accBytes;
+  const int GV = 16 / (int)gBytes;
   const int JBP = round_up(p.JB, GV);
   const bool multiJ = d.M > p.JB;
   const int64_t slices = d.BH() * p.ncb;
@@ -505,7 +568,7 @@ BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes) {
   wps = ceil_div(N, rows);
   const size_t budget = 96 * 1024;
   auto lds = [&](int w) {
-    size_t b = (size_t)w * kBwdRB * JBP * accBytes;
+    size_t b = (size_t)w * kBwdRB * (JBP * gBytes + 64 * accBytes) + (size_t)p.JB * 64 * accBytes;
     if (dkey) b += (size_t)p.JB * 64 * accBytes;
     if (dq && multiJ) b += (size_t)w * rows * 64 * accBytes;
     return b;
@@ -522,40 +585,45 @@ BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes) {
 }
 
 template <typename T, int JB, bool DQ, bool DK>
-int launch_bwd_jb(const T* g, const T* q, const T* k, T* dq, T* dk, void* ws, unsigned* counters,
-                  const Dims& d, const BwdPlan& p, hipStream_t st) {
+int launch_bwd_jb(const T* g, const T* q, const T* k, T* dq, T* dk, void* ws, const Dims& d,
+                  const BwdPlan& p, hipStream_t st) {
   using A = typename AccOf<T>::type;
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
   dim3 block(64 * p.W);
   hipLaunchKernelGGL((laplace_bwd_kernel<T, JB, DQ, DK>), grid, block, p.lds, st, g, q, k, dq, dk,
-                     static_cast<A*>(ws), counters, (int)d.N, (int)d.M, (int)d.C, p.rowsPerWave);
-  return check_launch("laplace backward");
+                     static_cast<A*>(ws), (int)d.N, (int)d.M, (int)d.C, p.rowsPerWave);
+  int s = check_launch("laplace backward");
+  if (s || !DK) return s;
+  dim3 rgrid(ceil_div(64 * (int)d.M, 256), p.ncb, (unsigned)d.BH());
+  hipLaunchKernelGGL(laplace_dk_reduce_kernel<T>, rgrid, dim3(256), 0, st, static_cast<const A*>(ws), dk,
+                     p.nx, (int)d.M, (int)d.C);
+  return check_launch("laplace backward_key reduction");
 }
 
 template <typename T, bool DQ, bool DK>
 int launch_bwd_t(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws,
-                 unsigned* counters, const Dims& d, const BwdPlan& p, hipStream_t st) {
+                 const Dims& d, const BwdPlan& p, hipStream_t st) {
   auto G = static_cast<const T*>(g);
   auto Q = static_cast<const T*>(q);
   auto K = static_cast<const T*>(k);
   auto DQp = static_cast<T*>(dq);
   auto DKp = static_cast<T*>(dk);
   switch (p.JB) {
-    case 16: return launch_bwd_jb<T, 16, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
-    case 32: return launch_bwd_jb<T, 32, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
-    case 49: return launch_bwd_jb<T, 49, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
-    default: return launch_bwd_jb<T, 64, DQ, DK>(G, Q, K, DQp, DKp, ws, counters, d, p, st);
+    case 16: return launch_bwd_jb<T, 16, DQ, DK>(G, Q, K, DQp, DKp, ws, d, p, st);
+    case 32: return launch_bwd_jb<T, 32, DQ, DK>(G, Q, K, DQp, DKp, ws, d, p, st);
+    case 49: return launch_bwd_jb<T, 49, DQ, DK>(G, Q, K, DQp, DKp, ws, d, p, st);
+    default: return launch_bwd_jb<T, 64, DQ, DK>(G, Q, K, DQp, DKp, ws, d, p, st);
   }
 }
 
 template <bool DQ, bool DK>
 int launch_bwd(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws,
-               unsigned* counters, const Dims& d, const BwdPlan& p, hipStream_t st) {
+               const Dims& d, const BwdPlan& p, hipStream_t st) {
   switch (dtype) {
-    case LFAMD_F32: return launch_bwd_t<float, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
-    case LFAMD_F16: return launch_bwd_t<f16s, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
-    case LFAMD_BF16: return launch_bwd_t<bf16s, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
-    default: return launch_bwd_t<double, DQ, DK>(g, q, k, dq, dk, ws, counters, d, p, st);
+    case LFAMD_F32: return launch_bwd_t<float, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case LFAMD_F16: return launch_bwd_t<f16s, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case LFAMD_BF16: return launch_bwd_t<bf16s, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    default: return launch_bwd_t<double, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
   }
 }
 
@@ -591,18 +659,15 @@ int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq,
   }
   if (!g || !q || !k || (doDq && !dq) || (doDk && !dk)) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
-  const BwdPlan p = plan_bwd(d, doDq, doDk, acc);
-  unsigned* counters = nullptr;
+  const BwdPlan p = plan_bwd(d, doDq, doDk, acc, dtype == LFAMD_F16 ? 2 : acc);
   if (doDk) {
     const size_t need = p.partialElems * acc;
     if (!ws || wsBytes < need)
       return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, need, wsBytes);
-    counters = stream_counters(st, (size_t)d.BH() * p.ncb);
-    if (!counters) return LFAMD_ERR_HIP;
   }
-  if (doDq && doDk) return launch_bwd<true, true>(dtype, g, q, k, dq, dk, ws, counters, d, p, st);
-  if (doDq) return launch_bwd<true, false>(dtype, g, q, k, dq, dk, ws, counters, d, p, st);
-  return launch_bwd<false, true>(dtype, g, q, k, dq, dk, ws, counters, d, p, st);
+  if (doDq && doDk) return launch_bwd<true, true>(dtype, g, q, k, dq, dk, ws, d, p, st);
+  if (doDq) return launch_bwd<true, false>(dtype, g, q, k, dq, dk, ws, d, p, st);
+  return launch_bwd<false, true>(dtype, g, q, k, dq, dk, ws, d, p, st);
 }
 
 }  // namespace
@@ -646,7 +711,7 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
   if (!valid_dtype(dtype) || check_dims(d, "workspace") || d.BH() == 0 || d.N == 0 || d.M == 0 || d.C == 0)
     return 0;
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
-  return plan_bwd(d, true, true, acc).partialElems * acc;
+  return plan_bwd(d, true, true, acc, dtype == LFAMD_F16 ? 2 : acc).partialElems * acc;
 }
 
 int lfamd_laplace_backward_key(int dtype, const void* grad_output, const void* query,

@@ -59,6 +59,26 @@ __device__ __forceinline__ float mix_sub_hh(uint32_t a, uint32_t b) {
   return d;
 }
 
+// acc + s * f32(g.half[GS]) and acc - s * f32(g.half[GS]), one rounding each.
+template <int GS>
+__device__ __forceinline__ float mix_fma_fh(float s, uint32_t g, float acc) {
+  float r;
+  if constexpr (GS == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "v"(g), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "v"(g), "v"(acc));
+  return r;
+}
+template <int GS>
+__device__ __forceinline__ float mix_fms_fh(float s, uint32_t g, float acc) {
+  float r;
+  if constexpr (GS == 0)
+    asm("v_fma_mix_f32 %0, %1, -%2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "v"(g), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, -%2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "v"(g), "v"(acc));
+  return r;
+}
+
 // Wave-uniform value hint (moves a VGPR that is known to be uniform to an SGPR).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

@@ -18,12 +18,6 @@ int ok();
 // Turns a pending launch error into LFAMD_ERR_HIP.
 int check_launch(const char* what);
 
-// Per-(device, stream) array of at least `n` zeroed uint32 counters used by the
-// last-workgroup reductions. Every kernel that takes a counter back to zero
-// before it exits, so the array stays zero between calls on one stream.
-// Returns nullptr (and records an error) on allocation failure.
-unsigned* stream_counters(hipStream_t stream, size_t n);
-
 // Max dynamic LDS bytes per workgroup on the current device (cached per device).
 int max_lds_bytes();
 

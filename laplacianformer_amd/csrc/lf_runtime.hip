@@ -1,14 +1,11 @@
-// Runtime plumbing of the C ABI: status strings, per-thread error text, the
-// per-(device, stream) counter arrays of the last-workgroup reductions, and the
-// HIP runtime version probe.
+// Runtime plumbing of the C ABI: status strings, per-thread error text, cached
+// device limits and the HIP runtime version probe.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
 
 #include <map>
 #include <mutex>
-#include <utility>
-#include <vector>
 
 #include "lf_internal.h"
 
@@ -33,38 +30,6 @@ int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(LFAMD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
   return ok();
-}
-
-namespace {
-struct CounterBlock {
-  unsigned* ptr = nullptr;
-  size_t n = 0;
-};
-std::mutex g_counter_mu;
-std::map<std::pair<int, hipStream_t>, CounterBlock> g_counters;
-std::vector<unsigned*> g_retired;  // superseded blocks; queued kernels may still use them
-}  // namespace
-
-unsigned* stream_counters(hipStream_t stream, size_t n) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    fail(LFAMD_ERR_HIP, "hipGetDevice failed");
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lk(g_counter_mu);
-  CounterBlock& b = g_counters[std::make_pair(dev, stream)];
-  if (b.n >= n) return b.ptr;
-  size_t want = n < 4096 ? 4096 : n * 2;
-  unsigned* p = nullptr;
-  if (hipMalloc(&p, want * sizeof(unsigned)) != hipSuccess ||
-      hipMemset(p, 0, want * sizeof(unsigned)) != hipSuccess) {
-    fail(LFAMD_ERR_HIP, "cannot allocate %zu reduction counters", want);
-    return nullptr;
-  }
-  if (b.ptr) g_retired.push_back(b.ptr);
-  b.ptr = p;
-  b.n = want;
-  return p;
 }
 
 int max_lds_bytes() {
