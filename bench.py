@@ -17,7 +17,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import platform
 import sys
 import time
 
@@ -140,58 +139,77 @@ def cpu_baseline(lap, ns, budget):
 
     torch.set_num_threads(os.cpu_count() or 1)
     q, kT, g = lap["inputs"]
-    B = q.shape[0]
     threads = oracle.max_threads()
-    # Time slices until ~budget/2 seconds, at least one.
-    t_used, nb, b = 0.0, 0, 0
-    while b < B and (t_used < budget / 2 or nb == 0):
-        qs, ks, gs = q[b:b + 1], kT[b:b + 1], g[b:b + 1]
+    # Whole config-2 steps (fwd + dq + dk over all slices), repeated until ~budget/2 seconds.
+    t_used, reps = 0.0, 0
+    while t_used < budget / 2 or reps == 0:
         t0 = time.perf_counter()
-        oracle.laplace_forward(qs, ks, "f16")
-        oracle.laplace_backward_query(gs, qs, ks, "f16")
-        oracle.laplace_backward_key(gs, qs, ks, "f16")
+        oracle.laplace_forward(q, kT, "f16")
+        oracle.laplace_backward_query(g, q, kT, "f16")
+        oracle.laplace_backward_key(g, q, kT, "f16")
         t_used += time.perf_counter() - t0
-        nb += 1
-        b += 1
-    trip = lap["T"] * nb / B
-    port_rate = trip / t_used / 1e9
+        reps += 1
+    port_rate = lap["T"] * reps / t_used / 1e9
 
     # PyTorch CPU: cdist p=1 on [B,H,M,d] keys, fp32 (CPU cdist rejects fp16), forward + autograd backward.
-    qf = q[:max(1, nb)].float().requires_grad_()
-    kf = kT[:max(1, nb)].float().transpose(-1, -2).contiguous().requires_grad_()
-    gf = g[:max(1, nb)].float()
-    t0 = time.perf_counter()
-    d = torch.cdist(qf, kf, p=1)
-    d.backward(gf)
-    t_cd = time.perf_counter() - t0
-    cd_rate = lap["T"] * max(1, nb) / B / t_cd / 1e9
+    qf = q.float().requires_grad_()
+    kf = kT.float().transpose(-1, -2).contiguous().requires_grad_()
+    gf = g.float()
+    t_cd, reps_cd = 0.0, 0
+    while t_cd < budget / 4 or reps_cd == 0:
+        t0 = time.perf_counter()
+        d = torch.cdist(qf, kf, p=1)
+        d.backward(gf)
+        t_cd += time.perf_counter() - t0
+        reps_cd += 1
+    cd_rate = lap["T"] * reps_cd / t_cd / 1e9
 
     # Newton: bmm loop with the reference init on a sample of matrices.
     A = ns["A"].double()
     nmat = min(A.shape[0], 256)
     Ab = A[:nmat, 0].float()
     n = Ab.shape[-1]
-    t0 = time.perf_counter()
-    P = Ab + 0.01 * torch.eye(n)
-    alpha = 1.8 / P.sum(-1).max(-1).values ** 2
-    V = alpha[:, None, None] * P
-    for _ in range(ns["iters"]):
-        V = 2 * V - torch.bmm(V, torch.bmm(P, V))
     Gb = ns["G"][:nmat, 0]
-    Vt = V.transpose(1, 2).contiguous()
-    _ = -torch.bmm(torch.bmm(Vt, Gb), Vt)
-    t_ns = time.perf_counter() - t0
-    ns_flops = nmat * (ns["iters"] + 1) * 4 * n ** 3
+    t_ns, reps_ns = 0.0, 0
+    while t_ns < budget / 4 or reps_ns == 0:
+        t0 = time.perf_counter()
+        P = Ab + 0.01 * torch.eye(n)
+        alpha = 1.8 / P.sum(-1).max(-1).values ** 2
+        V = alpha[:, None, None] * P
+        for _ in range(ns["iters"]):
+            V = 2 * V - torch.bmm(V, torch.bmm(P, V))
+        Vt = V.transpose(1, 2).contiguous()
+        _ = -torch.bmm(torch.bmm(Vt, Gb), Vt)
+        t_ns += time.perf_counter() - t0
+        reps_ns += 1
+    ns_flops = nmat * (ns["iters"] + 1) * 4 * n ** 3 * reps_ns
     return {
         "value": port_rate, "unit": "G(i*j*d)/s", "cores": threads, "kind": "port",
-        "sample": f"C oracle (oracle/laplace_oracle.c) fwd + dq + dk on {nb} of {B} (b,h) slices of config 2, "
-                  f"fp32 accumulation in the reference's serial order, {t_used:.2f} s",
+        "sample": f"C oracle (oracle/laplace_oracle.c) on the whole config-2 step (fwd + dq + dk, 32 (b,h) "
+                  f"slices, fp32 accumulation in the reference's serial order) x {reps}, {t_used:.2f} s",
         "torch_cpu_cdist": {"value": cd_rate, "unit": "G(i*j*d)/s", "threads": torch.get_num_threads(),
-                            "sample": f"torch.cdist(p=1) fp32 fwd+bwd on {max(1, nb)} slice(s), {t_cd:.2f} s"},
+                            "sample": f"torch.cdist(p=1) fp32 fwd+bwd on the config-2 step x {reps_cd}, {t_cd:.2f} s"},
         "torch_cpu_newton": {"value": ns_flops / t_ns / 1e12, "unit": "TFLOP/s", "threads": torch.get_num_threads(),
-                             "sample": f"bmm Newton-Schulz fwd+bwd, {nmat} of 1024 matrices, {t_ns:.2f} s"},
-        "host": {"cpu_count": os.cpu_count(), "cpu_model": platform.processor() or _cpu_model()},
+                             "sample": f"bmm Newton-Schulz fwd+bwd (12 it), {nmat} of 1024 config-3 matrices "
+                                       f"x {reps_ns}, {t_ns:.2f} s"},
+        "host": {"cpu_count": os.cpu_count(), "cpu_model": _cpu_model()},
     }
+
+
+def _traffic(kernel_prefix):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary
+    (profiles/hbm_traffic.json, FETCH_SIZE/WRITE_SIZE scaled by a plain-copy calibration)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for name, v in data.get("kernels", {}).items():
+        if name.startswith(kernel_prefix):
+            return {"bytes": v["read_bytes"] + v["write_bytes"], "read_bytes": v["read_bytes"],
+                    "write_bytes": v["write_bytes"], "source": data.get("source")}
+    return None
 
 
 def _cpu_model():
@@ -222,6 +240,7 @@ def main():
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
     if lap:
         T = lap["T"]
+        B_, N_, M_, C_ = 32, 3136, 49, 64
         value = T / (lap["wall_ms"] * 1e-3) / 1e9
         bwd_tflops = L1_FLOPS_BWD * T / (lap["bwd_ms"] * 1e-3) / 1e12
         fwd_tflops = L1_FLOPS_FWD * T / (lap["fwd_ms"] * 1e-3) / 1e12
@@ -231,9 +250,13 @@ def main():
             "config": {"workload": "BASELINE config 2: LaplaceSubtraction forward + fused backward (dq, dk), "
                                    "B=32 H=1 N=3136 M=49 d=64", "storage": "f16", "accumulate": "f32",
                        "global_batch": 32, "seq_len": 3136, "landmarks": 49, "channels": 64},
-            "roofline": {"bound": "valu", "kernel": "laplace_bwd_kernel<f16s,49,dq,dk>",
+            "roofline": {"bound": "valu",
+                         "kernel": "LaplaceSubtraction_backward = laplace_bwd_kernel<f16s,49,dq,dk> + "
+                                   "laplace_dk_reduce_kernel (one launch of the op, HIP events)",
                          "achieved": bwd_tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                         "frac": bwd_tflops / PEAK_FP32_TFLOPS, "traffic": None,
+                         "frac": bwd_tflops / PEAK_FP32_TFLOPS,
+                         "traffic": _traffic("lfamd::laplace_bwd_kernel<lfamd::f16s, 49, true, true>"),
+                         "algorithmic_bytes": 2 * (B_ * N_ * M_ + 2 * B_ * N_ * C_ + 2 * B_ * C_ * M_),
                          "work": f"{L1_FLOPS_BWD} flop per (i,j,d) triple x {T} triples per launch"},
             "kernels": {
                 "laplace_fwd_kernel<f16s,7>": {"ms": lap["fwd_ms"], "tflops": fwd_tflops,

@@ -1,0 +1,66 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol that
+include/*.h declares, and rejects bad arguments before touching the device."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(lfamd_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import laplacianformer_amd as lf
+
+    return lf.capi()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_symbols()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    import laplacianformer_amd._lib as L
+
+    assert sorted(n for n, _, _ in L.CAPI_PROTOTYPES) == names
+
+
+def test_status_strings_and_version(lib):
+    assert lib.lfamd_status_string(0) == b"ok"
+    assert lib.lfamd_status_string(3) == b"size outside the supported envelope"
+    assert lib.lfamd_status_string(99) == b"unknown status"
+    v = lib.lfamd_runtime_version()
+    assert v >= 600, v  # HIP >= 6.0 as major*100 + minor
+
+
+def test_newton_envelope(lib):
+    table = {0: 0, 1: 1, 16: 1, 49: 1, 64: 1, 100: 1, 128: 1, 129: 0, 256: 0, -3: 0}
+    for n, want in table.items():
+        assert lib.lfamd_newton_is_supported(n) == want, n
+
+
+def test_argument_errors_without_device(lib):
+    null = ctypes.c_void_p(0)
+    assert lib.lfamd_laplace_forward(7, null, null, null, 1, 1, 1, 1, 1, null) == 2
+    assert b"dtype" in lib.lfamd_last_error()
+    assert lib.lfamd_laplace_forward(0, null, null, null, -1, 1, 1, 1, 1, null) == 1
+    # Empty problems succeed without launching anything.
+    assert lib.lfamd_laplace_forward(0, null, null, null, 0, 4, 5, 6, 7, null) == 0
+    assert lib.lfamd_laplace_backward(1, null, null, null, null, null, 2, 2, 0, 3, 4, null, 0, null) in (0, 4)
+    assert lib.lfamd_newton_forward(0, null, null, 4, 129, 3, null) == 3
+    assert b"N=129" in lib.lfamd_last_error()
+    assert lib.lfamd_newton_forward(3, null, null, 4, 100, 3, null) == 3  # fp64 envelope is n <= 96
+    assert lib.lfamd_newton_backward(9, null, null, null, 4, 16, null) == 2
+    assert lib.lfamd_laplace_backward_workspace_size(1, 32, 1, 3136, 49, 64) > 0
+    assert lib.lfamd_laplace_backward_workspace_size(1, 0, 1, 3136, 49, 64) == 0

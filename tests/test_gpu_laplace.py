@@ -213,3 +213,31 @@ def test_autograd_function(gpu):
     out = lf.laplace_subtraction(qd, kd)
     out.backward(g.to(gpu))
     check_l1(out, qd.grad, kd.grad, l1_refs(q, k, g, "f32"), "f32", "autograd ")
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "f64"])
+def test_golden_kat(gpu, dt):
+    """Integer known-answer fixture (tests/golden/kat_l1.npz): exact in every type."""
+    import os
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "kat_l1.npz"))
+    q, k, g = (torch.from_numpy(z[n]).to(TORCH_DT[dt]) for n in ("q", "k", "g"))
+    out, dq, dk, dq2, dk2 = _run(gpu, q, k, g)
+    for got, name in ((out, "out"), (dq, "dq"), (dk, "dk"), (dq2, "dq"), (dk2, "dk")):
+        assert np.array_equal(got.cpu().double().numpy(), z[name]), (dt, name)
+
+
+def test_golden_config1(gpu):
+    """BASELINE config 1 fixture (fp64 torch.cdist results) against the fp32 kernels."""
+    import os
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "config1_l1.npz"))
+    q = torch.from_numpy(z["q"])
+    kT = torch.from_numpy(z["k_mc"]).transpose(-1, -2).contiguous()
+    g = torch.from_numpy(z["g"])
+    out, dq, dk, dq2, dk2 = _run(gpu, q, kT, g)
+    ga = np.abs(z["g"].astype(np.float64))
+    assert_l1_close(out, z["out"], "f32", "fixture forward")
+    assert_l1_close(dq2, z["dq"], "f32", "fixture dq", np.broadcast_to(ga.sum(3, keepdims=True), dq2.shape))
+    assert_l1_close(dk2, np.swapaxes(z["dk_mc"], -1, -2), "f32", "fixture dk",
+                    np.broadcast_to(ga.sum(2, keepdims=True), dk2.shape))

@@ -125,3 +125,18 @@ def test_newton_autograd(gpu):
     V.backward(G.to(gpu))
     assert_newton_close(V, oracle.newton_forward(A, 10), "f32")
     assert_newton_close(Ad.grad, oracle.newton_backward(G, V.detach().cpu()), "f32", rtol=1e-5)
+
+
+def test_newton_golden_closed_form(gpu):
+    """tests/golden/newton_closed.npz: eigen closed form of the iteration with the reference init."""
+    import os
+
+    import laplacianformer_amd as lf
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "newton_closed.npz"))
+    for n in (5, 49, 64):
+        A = torch.from_numpy(z[f"A_{n}"]).float().reshape(1, 1, n, n)
+        for it in (0, 1, 4, 10):
+            out = torch.empty_like(A, device=gpu)
+            lf.ext().NewtonInverse_forward(A.to(gpu), out, it)
+            assert_newton_close(out, z[f"X_{n}_{it}"][None, None], "f32", f"closed n={n} it={it}")
