@@ -49,26 +49,39 @@ def gen(shape, seed, dtype, scale=1.0):
     return (torch.randn(shape, generator=g) * scale).to(dtype)
 
 
+EVENT_EVERY = 8  # steps between event-bracketed samples inside the timed region
+
+
 def time_steps(fns, steps, warmup):
-    """Runs `fns` (a list of launch callables) per step. Returns wall ms/step and
-    the mean duration (ms) of each callable from HIP events on the current stream."""
+    """Runs `fns` (a list of launch callables) once per step, `steps` times.
+
+    Returns the wall-clock ms per step over the whole timed region (bracketed by
+    device synchronisation) and the mean duration (ms) of each callable, taken
+    from HIP events recorded on the current stream around every callable of
+    every EVENT_EVERY-th step (each event record costs a few microseconds of GPU
+    time, so recording them on every step would inflate the step time)."""
     import torch
 
     for _ in range(warmup):
         for f in fns:
             f()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)] for _ in range(steps)]
+    sampled = list(range(0, steps, EVENT_EVERY))
+    evs = {s: [torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)] for s in sampled}
     t0 = time.perf_counter()
     for s in range(steps):
-        e = evs[s]
-        e[0].record()
-        for i, f in enumerate(fns):
-            f()
-            e[i + 1].record()
+        e = evs.get(s)
+        if e is None:
+            for f in fns:
+                f()
+        else:
+            e[0].record()
+            for i, f in enumerate(fns):
+                f()
+                e[i + 1].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    per = [sum(evs[s][i].elapsed_time(evs[s][i + 1]) for s in range(steps)) / steps for i in range(len(fns))]
+    per = [sum(evs[s][i].elapsed_time(evs[s][i + 1]) for s in sampled) / len(sampled) for i in range(len(fns))]
     return wall, per
 
 

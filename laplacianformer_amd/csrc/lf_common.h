@@ -79,6 +79,26 @@ __device__ __forceinline__ float mix_fms_fh(float s, uint32_t g, float acc) {
   return r;
 }
 
+// Same two operations with the packed halves in an SGPR (a wave-uniform value).
+template <int GS>
+__device__ __forceinline__ float mix_fma_fs(float s, uint32_t g, float acc) {
+  float r;
+  if constexpr (GS == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
+  return r;
+}
+template <int GS>
+__device__ __forceinline__ float mix_fms_fs(float s, uint32_t g, float acc) {
+  float r;
+  if constexpr (GS == 0)
+    asm("v_fma_mix_f32 %0, %1, -%2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, -%2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
+  return r;
+}
+
 // Wave-uniform value hint (moves a VGPR that is known to be uniform to an SGPR).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

@@ -173,10 +173,19 @@ def test_capi_direct(gpu):
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=gpu)
     torch.cuda.synchronize()
     s = ctypes.c_void_p(st.cuda_stream)
-    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out.data_ptr(), B, H, N, M, C, s))
+    fws_bytes = lib.lfamd_laplace_forward_workspace_size(dt, B, H, N, M, C)
+    fws = torch.empty(max(fws_bytes, 1), dtype=torch.uint8, device=gpu)
+    out_nows = torch.empty_like(out)
+    torch.cuda.synchronize()
+    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out.data_ptr(), B, H, N, M, C,
+                                       fws.data_ptr(), fws_bytes, s))
+    # Without a workspace the LDS-staged kernel runs; results are bit-identical.
+    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out_nows.data_ptr(), B, H, N, M, C,
+                                       None, 0, s))
     lf.check(lib.lfamd_laplace_backward(dt, gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), dq.data_ptr(),
                                         dk.data_ptr(), B, H, N, M, C, ws.data_ptr(), ws_bytes, s))
     st.synchronize()
+    assert torch.equal(out.cpu(), out_nows.cpu())
     assert_bitwise(out, oracle.laplace_forward(q, k, "f16"), "f16")
     check_l1(out, dq, dk, l1_refs(q, k, g, "f16"), "f16", "capi ")
     # Too small a workspace is rejected before anything is launched.
