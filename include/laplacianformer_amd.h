@@ -42,22 +42,14 @@ extern "C" {
 
 /* ---- LaplaceSubtraction ------------------------------------------------ */
 
-/* Bytes of optional device workspace for lfamd_laplace_forward (an fp32 copy of
- * the key). No reference counterpart. */
-size_t lfamd_laplace_forward_workspace_size(int dtype, int64_t batch, int64_t heads,
-                                            int64_t q_len, int64_t k_len, int64_t channels);
-
 /* out[b,h,i,j] = sum_c |query[b,h,i,c] - key[b,h,c,j]|, fp32 accumulation
  * (fp64 for LFAMD_F64), c ascending, rounded once to the element type.
- * `workspace` (may be NULL) of lfamd_laplace_forward_workspace_size bytes enables
- * the faster path; results are identical either way.
  * Replaces laplace::LaplaceSubtraction_forward_cuda
  * (reference include/LaplaceSubtraction.h:9-13, src/LaplaceSubtraction_cuda.cu:55-67,
  *  src/LaplaceSubtraction_cuda_kernel.cu:455-485). */
 int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* output,
                           int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
-                          int64_t channels, void* workspace, size_t workspace_bytes,
-                          void* stream);
+                          int64_t channels, void* stream);
 
 /* grad_query[b,h,i,c] = sum_j grad_output[b,h,i,j] * sgn(query[b,h,i,c] - key[b,h,c,j]),
  * sgn(0) = 0. Replaces laplace::LaplaceSubtraction_backward_query_cuda

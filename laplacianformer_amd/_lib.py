@@ -26,8 +26,7 @@ _capi = None
 _P, _I, _I64, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
 _DIMS = [_I64] * 5
 CAPI_PROTOTYPES = [
-    ("lfamd_laplace_forward_workspace_size", _SZ, [_I] + _DIMS),
-    ("lfamd_laplace_forward", _I, [_I, _P, _P, _P] + _DIMS + [_P, _SZ, _P]),
+    ("lfamd_laplace_forward", _I, [_I, _P, _P, _P] + _DIMS + [_P]),
     ("lfamd_laplace_backward_query", _I, [_I, _P, _P, _P, _P] + _DIMS + [_P]),
     ("lfamd_laplace_backward_workspace_size", _SZ, [_I] + _DIMS),
     ("lfamd_laplace_backward_key", _I, [_I, _P, _P, _P, _P] + _DIMS + [_P, _SZ, _P]),

@@ -209,126 +209,175 @@ laplace_fwd_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __
 }
 
 // ---------------------------------------------------------------------------
-// Forward, fp32-key path. A pre-pass writes the key once per call as fp32 rows
-// padded to `Mp` columns; the forward then reads each channel's JB key values
-// with one scalar load (wave-uniform, into SGPRs) and spends two full-rate VALU
-// operations per (c, j): v_sub_f32 with the SGPR operand and v_add_f32 with |.|.
-// The query row of the lane stays in VGPRs (widened once per channel).
+// Forward with the key broadcast from LDS. Lane = query row, R rows per lane;
+// a workgroup is the W = ceil(M / JB) waves that share one block of 64*R rows,
+// wave w owning key columns [w*JB, w*JB + JB). The key is widened to fp32 once
+// per workgroup into LDS; per channel a wave reads its JB key values as
+// wave-wide broadcasts (ds_read_b128: one read feeds 8*R VALU instructions) and
+// does |q - k| + acc as v_sub_f32 and v_add_f32 with an |.| modifier, both with
+// VGPR operands only (full issue rate; an SGPR operand halves it on gfx950).
+// The query is widened once per channel per row. Channels are summed in
+// ascending order in fp32 (fp64 is not handled here), the reference's serial
+// order, so results are bit-identical to it. The output tile of the 64*R rows
+// is staged in LDS and written as one contiguous span. Requires C % 8 == 0 and a
+// 16-byte aligned query (checked on the host).
 // ---------------------------------------------------------------------------
-// Key pre-pass of the SGPR forward: kf[bh][b][c][t] = f32(key[bh][c][b*JB + t]) for
-// column block b, channel c < KCp and t < JBS (JB rounded up to 8), zero outside
-// the key. Each channel of a block is one run of JBS floats, and two channels of
-// an 8-wide block are one 16-dword run: few, wide scalar loads.
-template <typename T>
-__global__ void __launch_bounds__(256)
-laplace_key_f32_kernel(const T* __restrict__ key, float* __restrict__ kf, int64_t BH, int C, int KCp, int M,
-                       int JB, int JBS, int nJB) {
-  const int64_t total = BH * nJB * KCp * JBS;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    int64_t r = e / JBS;
-    const int t = (int)(e - r * JBS);
-    const int c = (int)(r % KCp);
-    r /= KCp;
-    const int b = (int)(r % nJB);
-    const int64_t bh = r / nJB;
-    const int col = b * JB + t;
-    kf[e] = (t < JB && col < M && c < C) ? (float)to_acc(key[(bh * C + c) * M + col]) : 0.0f;
-  }
+template <typename T> __device__ __forceinline__ float elem_f32(const uint4& v, int e);
+template <> __device__ __forceinline__ float elem_f32<f16s>(const uint4& v, int e) {
+  const uint32_t w = (&v.x)[e >> 1];
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> (16 * (e & 1))));
+}
+template <> __device__ __forceinline__ float elem_f32<bf16s>(const uint4& v, int e) {
+  const uint32_t w = (&v.x)[e >> 1];
+  return __builtin_bit_cast(float, (e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+template <> __device__ __forceinline__ float elem_f32<float>(const uint4& v, int e) {
+  return __builtin_bit_cast(float, (&v.x)[e]);
 }
 
-constexpr int kFwdSgQV = 16;  // max 16-byte query vectors per row (256 bytes)
+constexpr int kFbKC = 8;  // channels per query chunk of the broadcast forward
 
-// NV = 16-byte query vectors per row (C <= NV*CK; the key copy is zero-padded
-// to NV*CK channels and the query vectors past C are zero).
-template <typename T, int JB, int NV>
+__host__ __device__ constexpr int fb_pitch(int jb) { return (jb + 3) & ~3; }
+
+template <typename T, int JB, int R>
 __global__ void __launch_bounds__(1024)
-laplace_fwd_sgpr_kernel(const T* __restrict__ query, const float* __restrict__ kf, T* __restrict__ out,
-                        int N, int M, int C, int nJB, int colsPerGroup, int flags) {
-  constexpr int CK = QChunk<T>::value;
-  constexpr int KCp = NV * CK;
-  constexpr int JBS = round_up(JB, 8);
+laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out,
+                         int N, int M, int C) {
+  constexpr int JBS = fb_pitch(JB);
+  constexpr int NG = JBS / 4;
+  constexpr int EV = 16 / (int)sizeof(T);  // elements per 16-byte vector
+  constexpr int NVC = kFbKC / EV;          // vectors per row per chunk
   const int W = blockDim.x >> 6;
-  const int wave = uniform(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int bh = blockIdx.z;
-  const int jg0 = blockIdx.y * colsPerGroup;
-  const int jblk = uniform(blockIdx.y * W + wave);
-  const int row0 = blockIdx.x * 64;
-  const int row = row0 + lane;
-  const int nv = C / CK;
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // Workgroup -> (slice, row block): every slice's full blocks first, the
+  // partial last blocks (N not a multiple of 64R) after all of them, so the
+  // workgroups dispatched last, onto CUs that already hold their share, are
+  // the short ones.
+  const int nFull = N / (64 * R);
+  const int BH = gridDim.y;
+  const int id = blockIdx.y * gridDim.x + blockIdx.x;
+  int bh, blk;
+  if (id < BH * nFull) {
+    bh = id / nFull;
+    blk = id - bh * nFull;
+  } else {
+    bh = id - BH * nFull;
+    blk = nFull;
+  }
+  const int i0 = blk * 64 * R;
+  const int rows = min(64 * R, N - i0);
+  const int KP = W * JBS;              // key tile pitch (floats per channel)
+  const int QV = C / EV;               // 16-byte vectors per query row
+  const int QP = QV + 1;               // query tile pitch in vectors (padding: fewer bank conflicts)
 
   extern __shared__ __align__(16) unsigned char smem[];
-  T* ot = reinterpret_cast<T*>(smem);  // [64][colsPerGroup]
+  float* ksm = reinterpret_cast<float*>(smem);                  // [C][W*JBS] key, fp32
+  uint4* qsm = reinterpret_cast<uint4*>(ksm + (size_t)C * KP);  // [64R][QP] query rows, raw
+  T* otile = reinterpret_cast<T*>(qsm);                         // [64R][M] output (after the sums)
 
-  // The lane's query row (rows past N read row N-1 and are never stored).
-  uint4 qv[NV];
-  const uint4* src = reinterpret_cast<const uint4*>(query + ((size_t)bh * N + min(row, N - 1)) * C);
-#pragma unroll
-  for (int t = 0; t < NV; ++t) qv[t] = t < nv ? src[t] : uint4{0u, 0u, 0u, 0u};
+  // The block's query rows are one contiguous span: coalesced 16-byte copies.
+  const uint4* qsrc = reinterpret_cast<const uint4*>(query + ((size_t)bh * N + i0) * C);
+  for (int u = threadIdx.x; u < rows * QV; u += blockDim.x) {
+    const int row = u / QV, v = u - row * QV;
+    qsm[row * QP + v] = qsrc[u];
+  }
+  // Key tile, fp32, zero outside [0, M); channel c staged by wave c % W.
+  const T* kb = key + (size_t)bh * C * M;
+  for (int c = wave; c < C; c += W) {
+    for (int t = lane; t < KP; t += 64) {
+      const int w = t / JBS, jj = t - w * JBS;
+      const int col = w * JB + jj;
+      ksm[c * KP + t] = (jj < JB && col < M) ? to_acc(kb[(size_t)c * M + col]) : 0.0f;
+    }
+  }
+  __syncthreads();
 
-  // This wave's column block: channel c's JB key values at kb + c*JBS.
-  const float* kb = kf + ((size_t)bh * nJB + min(jblk, nJB - 1)) * KCp * JBS;
-  float acc[JB];
+  float acc[R][JB];
 #pragma unroll
-  for (int j = 0; j < JB; ++j) acc[j] = 0.0f;
-  // Channels are processed in groups of KG: the group's key values are loaded
-  // (scalar loads, whole 16-byte groups) before any of them is used, so each
-  // group costs one scalar-load latency. Scalar loads may return out of order,
-  // so every wait is a wait for all of them; one wait per channel would expose
-  // the latency channel by channel.
-  constexpr int KG = (JBS >= 16 ? 4 : 8) < CK ? (JBS >= 16 ? 4 : 8) : CK;
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-  for (int t = 0; t < NV; ++t) {
-    const uint32_t w[4] = {qv[t].x, qv[t].y, qv[t].z, qv[t].w};
+    for (int j = 0; j < JB; ++j) acc[r][j] = 0.0f;
+  // Rows past the block's end read row 0 of the tile (their results are not stored).
+  const uint4* qrow[R];
 #pragma unroll
-    for (int u0 = 0; u0 < CK; u0 += KG) {
-      float kv[KG][JBS];
+  for (int r = 0; r < R; ++r) qrow[r] = qsm + (r * 64 + lane < rows ? r * 64 + lane : 0) * QP;
+  const float4* kw = reinterpret_cast<const float4*>(ksm + wave * JBS);
+  const int KP4 = KP / 4;
+  const int nChunks = C / kFbKC;
+  // Key values one channel ahead and query vectors one chunk ahead of the
+  // arithmetic; a compiler memory barrier per channel keeps it from hoisting a
+  // whole chunk's reads (registers).
+  uint4 qv[R][NVC];
 #pragma unroll
-      for (int g = 0; g < KG; ++g) {
-        const float4* kr4 = reinterpret_cast<const float4*>(kb + (t * CK + u0 + g) * JBS);
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int r = 0; r < JBS / 4; ++r) {
-          const float4 v = kr4[r];
-          kv[g][4 * r] = v.x; kv[g][4 * r + 1] = v.y; kv[g][4 * r + 2] = v.z; kv[g][4 * r + 3] = v.w;
+    for (int v = 0; v < NVC; ++v) qv[r][v] = qrow[r][v];
+  float4 kcur[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) kcur[g] = kw[g];
+  for (int kc = 0; kc < nChunks; ++kc) {
+    uint4 qn[R][NVC];
+    const int kn = min(kc + 1, nChunks - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int v = 0; v < NVC; ++v) qn[r][v] = qrow[r][kn * NVC + v];
+#pragma unroll
+    for (int cc = 0; cc < kFbKC; ++cc) {
+      const int cnext = min(kc * kFbKC + cc + 1, C - 1);
+      float4 knext[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        knext[g] = kw[cnext * KP4 + g];
+        // Use the padding lane too, so the read stays one ds_read_b128 (a
+        // narrower split, e.g. b96 + b32, costs more LDS cycles than b128).
+        asm volatile("" ::"v"(knext[g].w));
+      }
+      float qf[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) qf[r] = elem_f32<T>(qv[r][cc / EV], cc % EV);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float k4[4] = {kcur[g].x, kcur[g].y, kcur[g].z, kcur[g].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (g * 4 + t < JB) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][g * 4 + t] += fabsf(qf[r] - k4[t]);
+          }
         }
       }
 #pragma unroll
-      for (int g = 0; g < KG; ++g) {
-        const int u = u0 + g;
-        float q;
-        if constexpr (std::is_same<T, f16s>::value)
-          q = (float)__builtin_bit_cast(_Float16, (uint16_t)((u & 1) ? (w[u >> 1] >> 16) : (w[u >> 1] & 0xffffu)));
-        else if constexpr (std::is_same<T, bf16s>::value)
-          q = __builtin_bit_cast(float, (u & 1) ? (w[u >> 1] & 0xffff0000u) : (w[u >> 1] << 16));
-        else
-          q = __builtin_bit_cast(float, w[u]);
-#pragma unroll
-        for (int j = 0; j < JB; ++j) acc[j] += fabsf(q - kv[g][j]);
-      }
+      for (int g = 0; g < NG; ++g) kcur[g] = knext[g];
+      asm volatile("" ::: "memory");
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int v = 0; v < NVC; ++v) qv[r][v] = qn[r][v];
   }
 
+  __syncthreads();  // every wave is done with the query tile, which becomes the output tile
 #pragma unroll
-  for (int j = 0; j < JB; ++j) ot[lane * colsPerGroup + wave * JB + j] = from_acc<T>(acc[j]);
-  __syncthreads();
-  const int colsValid = min(colsPerGroup, M - jg0);
-  const int rowsValid = min(64, N - row0);
-  T* ob = out + ((size_t)bh * N + row0) * M + jg0;
-  if (colsPerGroup == M) {
-    const int total = rowsValid * M;
-    int done = 0;
-    if (flags & kFwdVecOut) {
-      constexpr int VE = 16 / (int)sizeof(T);
-      const int nvv = total / VE;
-      for (int e = threadIdx.x; e < nvv; e += blockDim.x)
-        reinterpret_cast<uint4*>(ob)[e] = reinterpret_cast<const uint4*>(ot)[e];
-      done = nvv * VE;
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int col = wave * JB + j;
+      if (col < M) otile[(r * 64 + lane) * M + col] = from_acc<T>(acc[r][j]);
     }
-    for (int e = done + threadIdx.x; e < total; e += blockDim.x) ob[e] = ot[e];
-  } else {
-    for (int r = wave; r < rowsValid; r += W)
-      for (int cidx = lane; cidx < colsValid; cidx += 64) ob[(size_t)r * M + cidx] = ot[r * colsPerGroup + cidx];
+  __syncthreads();
+  // Rows [i0, i0 + rows) are one contiguous span of rows*M elements.
+  const int n = rows * M;
+  T* dst = out + ((size_t)bh * N + i0) * M;
+  int done = 0;
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+    const int nv = n / EV;
+    const uint4* src4 = reinterpret_cast<const uint4*>(otile);
+    uint4* dst4 = reinterpret_cast<uint4*>(dst);
+    for (int t = threadIdx.x; t < nv; t += blockDim.x) dst4[t] = src4[t];
+    done = nv * EV;
   }
+  for (int t = done + threadIdx.x; t < n; t += blockDim.x) dst[t] = otile[t];
 }
 
 // ---------------------------------------------------------------------------
@@ -543,26 +592,75 @@ laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
 }
 
 // ---------------------------------------------------------------------------
-// fp16 backward with the grad_output rows in SGPRs (M == MC known at compile
-// time). A group of R2 rows (2 when MC is odd, so that the group starts on a
-// dword) is MC*R2/2 dwords: one scalar load, wave-uniform, consumed directly by
-// v_fma_mix_f32 with the half selected statically. No LDS traffic for
-// grad_output, no VGPRs for it, so 3 waves fit per SIMD. Requires N*MC even
-// and a 4-byte aligned grad_output (checked on the host).
+// fp16 backward, every per-triple instruction at the full VALU rate.
+//
+// With q' = 2^24 q and k' = 2^24 k (exact for fp16 values, whose nonzero
+// differences are at least 2^-24), d = q' - k' is 0 or at least 1 in magnitude,
+// so y = clamp(d/2 + 1/2) is exactly (sgn(q - k) + 1) / 2 and sgn = 2y - 1:
+//   grad_query[i,c] = sum_j (2 g_ij) y_ijc - sum_j g_ij
+//   grad_key[c,j]   = sum_i g_ij - sum_i (2 g_ij) y_ijc
+// Per triple: v_sub, v_fma+clamp, two v_fma, all with VGPR operands (an SGPR
+// operand, v_med3 or v_fma_mix would issue at half rate on gfx950).
+//
+// Lane = channel, key' and the grad_key sums of the MC columns in registers.
+// Each wave owns a row range and stages its grad rows, scaled by 2, in a private
+// LDS batch of RB rows; every lane reads them as wave-wide broadcasts (one
+// ds_read_b128 feeds 16 VALU instructions). The row sums sum_j g_ij and column
+// sums sum_i g_ij come from the same batch. No cross-wave synchronisation until
+// the final, wave-ordered grad_key reduction. Requires N*MC even and a 4-byte
+// aligned grad_output (checked on the host).
 // ---------------------------------------------------------------------------
-constexpr int kSgRB = 8;  // rows per query-prefetch batch (multiple of 2)
+constexpr int kBcRB = 8;  // grad rows per LDS batch
+constexpr int kBcBufs = 4;  // LDS accumulators of the workgroup grad_key reduction
 
-// Waves per workgroup of the SGPR path: the MC <= 49 variants fit 128 VGPRs
-// (4 waves per SIMD, one 16-wave workgroup per CU); MC = 64 needs ~154 (3 waves).
-__host__ __device__ constexpr int sgpr_max_waves(int mc) { return mc <= 49 ? 16 : 12; }
+// Workgroup sum of the per-wave grad_key partials v[MC] (lane = channel), in a
+// fixed order: wave w adds into LDS accumulator w % kBcBufs in rounds of
+// increasing w / kBcBufs, then the accumulators are summed 0, 1, ... and the
+// result is written to `out` column-major, [MC][64] (channel fastest: LDS reads
+// without bank conflicts, coalesced stores). Every read of a round is issued
+// before its writes. Needs kBcBufs * MC * 64 floats of LDS at `red`.
+template <int MC>
+__device__ __forceinline__ void bcast_reduce_dk(const float (&v)[MC], float* red, int W, int wave, int lane,
+                                                float* __restrict__ out) {
+  const int nb = min(W, kBcBufs);
+  float* buf = red + (wave % nb) * MC * 64;
+  __syncthreads();  // every wave is done with the LDS it used before
+  for (int round = 0; round * nb < W; ++round) {
+    if (wave / nb == round) {
+      if (round == 0) {
+#pragma unroll
+        for (int j = 0; j < MC; ++j) buf[j * 64 + lane] = v[j];
+      } else {
+        float pv[MC];
+#pragma unroll
+        for (int j = 0; j < MC; ++j) pv[j] = buf[j * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < MC; ++j) buf[j * 64 + lane] = pv[j] + v[j];
+      }
+    }
+    __syncthreads();
+  }
+  for (int t = threadIdx.x; t < 64 * MC; t += blockDim.x) {
+    float s = red[t];
+    for (int b = 1; b < nb; ++b) s += red[b * MC * 64 + t];
+    out[t] = s;
+  }
+}
+
+__host__ __device__ constexpr int bcast_max_waves(int mc) { return mc <= 16 ? 16 : 12; }
+// Row pitch (floats) of a staged grad row: whole 16-byte groups, an even number
+// of them (the row loop keeps two groups in flight in a two-slot ring).
+__host__ __device__ constexpr int bcast_pitch(int mc) { return (mc + 7) & ~7; }
 
 template <int MC, bool DQ, bool DK>
-__global__ void __launch_bounds__(64 * sgpr_max_waves(MC))
-laplace_bwd_sgpr_kernel(const f16s* __restrict__ gout, const f16s* __restrict__ query,
-                        const f16s* __restrict__ key, f16s* __restrict__ dq, f16s* __restrict__ dk,
-                        float* __restrict__ partial, int N, int C, int rowsPerWave) {
-  constexpr int R2 = (MC & 1) ? 2 : 1;
-  constexpr int GW = MC * R2 / 2;  // dwords per row group
+__global__ void __launch_bounds__(64 * bcast_max_waves(MC))
+laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__ query,
+                         const f16s* __restrict__ key, f16s* __restrict__ dq, f16s* __restrict__ dk,
+                         float* __restrict__ partial, int N, int C, int rowsPerWave) {
+  constexpr int RB = kBcRB;
+  constexpr int MP = bcast_pitch(MC);            // LDS row pitch (floats)
+  constexpr int GD = RB * MC / 2;                // grad dwords of a full batch
+  constexpr int NL = (GD + 63) / 64;             // dwords per lane per batch
   const int W = blockDim.x >> 6;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -574,15 +672,35 @@ laplace_bwd_sgpr_kernel(const f16s* __restrict__ gout, const f16s* __restrict__ 
   const int rowEnd = uniform(min(N, rowBeg + rowsPerWave));
 
   extern __shared__ __align__(16) unsigned char smem[];
-  float* ksm = reinterpret_cast<float*>(smem);  // [MC][64] scaled key tile
-  float* red = ksm + MC * 64;                   // [MC][64] (DK)
+  float* ksm = reinterpret_cast<float*>(smem);             // [MC][64] key tile, then grad_key sums
+  // This wave's batch: [RB][MP] 2g, [RB] -sum_j g, [MP] column sums, [RB][64] scaled query.
+  float* gsm = ksm + MC * 64 + wave * (RB * MP + RB + MP + RB * 64);
+  float* gneg = gsm + RB * MP;
+  float* hsm = gneg + RB;
+  float* qsm = hsm + MP;
 
   const f16s* qb = query + (size_t)bh * N * C;
   const uint32_t* gw = reinterpret_cast<const uint32_t*>(gout + (size_t)bh * N * MC);
   const f16s* kb = key + (size_t)bh * C * MC;
 
+  uint32_t gpre[NL];
+  uint16_t qpre[RB];
+  auto fetch = [&](int rb) {
+    const int words = min(RB, rowEnd - rb) * MC / 2;
+    const uint32_t* src = gw + (size_t)rb * MC / 2;
+#pragma unroll
+    for (int t = 0; t < NL; ++t) {
+      const int e = lane + 64 * t;
+      gpre[t] = e < words ? src[e] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) qpre[r] = (cval && rb + r < rowEnd) ? qb[(size_t)(rb + r) * C + c].bits : 0;
+  };
+  // The first batch's loads are in flight while the key tile is staged.
+  if (rowBeg < rowEnd) fetch(rowBeg);
+
   for (int t = threadIdx.x; t < 64 * MC; t += blockDim.x) {
-    const int cl = t & 63, j = t >> 6;  // lane-fastest: conflict-free LDS writes
+    const int cl = t & 63, j = t >> 6;
     const int cc = cb * 64 + cl;
     ksm[j * 64 + cl] = cc < C ? to_acc(kb[(size_t)cc * MC + j]) * 16777216.0f : 0.0f;
   }
@@ -591,84 +709,112 @@ laplace_bwd_sgpr_kernel(const f16s* __restrict__ gout, const f16s* __restrict__ 
 #pragma unroll
   for (int j = 0; j < MC; ++j) {
     kreg[j] = ksm[j * 64 + lane];
-    dka[j] = 0.0f;
+    if (DK) dka[j] = 0.0f;
   }
+  float hsum = 0.0f;  // lane j < MC: sum over this wave's rows of g[i][j]
 
-  uint16_t qpre[kSgRB];
-  auto fetch_q = [&](int rb) {
+  for (int rb = rowBeg; rb < rowEnd; rb += RB) {
+    const int nr = min(RB, rowEnd - rb);  // uniform
+    // Stage this batch: 2g as fp32 (exact), row-major [RB][MP].
 #pragma unroll
-    for (int r = 0; r < kSgRB; ++r) qpre[r] = (cval && rb + r < rowEnd) ? qb[(size_t)(rb + r) * C + c].bits : 0;
-  };
-  // The scalar loads of grad rows would each miss to HBM (every row is read by
-  // one wave only); one vector load per 128-byte line a batch ahead pulls the
-  // next batch's rows into L2 first. The loaded words feed a sink that is
-  // stored only under a condition the host never sets (rowsPerWave < 0).
-  uint32_t sink = 0;
-  auto warm_g = [&](int rb) {
-    const int words = min(kSgRB, rowEnd - rb) * MC / 2;
-    const uint32_t* nb = gw + (size_t)rb * MC / 2;
-    if (lane * 32 < words) sink ^= nb[lane * 32];
-  };
-  if (rowBeg < rowEnd) {
-    fetch_q(rowBeg);
-    warm_g(rowBeg);
-  }
-  for (int rb = rowBeg; rb < rowEnd; rb += kSgRB) {
-    float qcur[kSgRB];
-#pragma unroll
-    for (int r = 0; r < kSgRB; ++r) {
-      qcur[r] = (float)__builtin_bit_cast(_Float16, qpre[r]) * 16777216.0f;
-      // Keep the widened value in a register: folding the widening into each
-      // subtract (v_fma_mix_f32) would put a wait state after every one of them.
-      asm volatile("" : "+v"(qcur[r]));
-    }
-    if (rb + kSgRB < rowEnd) {
-      fetch_q(rb + kSgRB);
-      warm_g(rb + kSgRB);
+    for (int t = 0; t < NL; ++t) {
+      const int e = 2 * (lane + 64 * t);
+      if (e < RB * MC) {
+        const int r0 = e / MC, j0 = e - r0 * MC;
+        const int r1 = (e + 1) / MC, j1 = e + 1 - r1 * MC;
+        gsm[r0 * MP + j0] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] & 0xffffu));
+        gsm[r1 * MP + j1] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] >> 16));
+      }
     }
 #pragma unroll
-    for (int r0 = 0; r0 < kSgRB; r0 += R2) {
-      if (rb + r0 >= rowEnd) break;  // uniform; rows come in whole groups of R2
-      const uint32_t* gp = gw + (size_t)(rb + r0) * MC / 2;
-      uint32_t g[GW];
+    for (int r = 0; r < RB; ++r) qsm[r * 64 + lane] = (float)__builtin_bit_cast(_Float16, qpre[r]) * 16777216.0f;
+    wave_sync();
+    // Row sums (lane r) for grad_query and column sums (lane j) for grad_key.
+    // Rows past nr are zero in the batch. All reads of a sum are issued before
+    // the additions, so no chain of dependent LDS round trips.
+    if (DQ) {
+      const float4* rowp = reinterpret_cast<const float4*>(gsm + min(lane, RB - 1) * MP);
+      float4 v[MP / 4];
 #pragma unroll
-      for (int t = 0; t < GW; ++t) g[t] = gp[t];
+      for (int jq = 0; jq < MP / 4; ++jq) v[jq] = rowp[jq];
+      float sum = 0.0f;
 #pragma unroll
-      for (int rr = 0; rr < R2; ++rr) {
-        const float qv = qcur[r0 + rr];
-        float dqa = 0.0f;
+      for (int jq = 0; jq < MP / 4; ++jq) {
+        const float e[4] = {v[jq].x, v[jq].y, v[jq].z, v[jq].w};
 #pragma unroll
-        for (int j = 0; j < MC; ++j) {
-          const int h = rr * MC + j;  // half index inside the row group (compile-time)
-          const float s = __builtin_amdgcn_fmed3f(qv - kreg[j], -1.0f, 1.0f);
-          if (h & 1) {
-            if (DQ) dqa = mix_fma_fs<1>(s, g[h >> 1], dqa);
-            if (DK) dka[j] = mix_fms_fs<1>(s, g[h >> 1], dka[j]);
-          } else {
-            if (DQ) dqa = mix_fma_fs<0>(s, g[h >> 1], dqa);
-            if (DK) dka[j] = mix_fms_fs<0>(s, g[h >> 1], dka[j]);
+        for (int t = 0; t < 4; ++t)
+          if (jq * 4 + t < MC) sum += e[t];
+      }
+      if (lane < RB) gneg[lane] = -0.5f * sum;
+    }
+    if (DK) {
+      float hv[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) hv[r] = gsm[r * MP + min(lane, MC - 1)];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) hsum += hv[r];
+    }
+    wave_sync();
+    if (rb + RB < rowEnd) fetch(rb + RB);
+
+    // Row loop, software-pipelined two broadcast reads ahead (LDS latency under
+    // load exceeds one column group's VALU time); the next row's query value,
+    // initial sum and first two grad groups are read during the current row's
+    // last groups. The scheduling barriers keep the compiler from computing
+    // every column's step up front (MC more registers).
+    constexpr int NQ = MP / 4;
+    static_assert(NQ >= 2 && NQ % 2 == 0, "two groups in flight, slots aligned at every row start");
+    float qn = qsm[lane];
+    float accn = DQ ? gneg[0] : 0.0f;
+    float4 gq[2] = {reinterpret_cast<const float4*>(gsm)[0], reinterpret_cast<const float4*>(gsm)[1]};
+#pragma unroll 1
+    for (int r = 0; r < nr; ++r) {
+      const float4* g4 = reinterpret_cast<const float4*>(gsm + r * MP);
+      const float4* g4n = reinterpret_cast<const float4*>(gsm + min(r + 1, RB - 1) * MP);
+      const float qv = qn;
+      float acc = accn;
+#pragma unroll
+      for (int jq = 0; jq < NQ; ++jq) {
+        const float4 gv = gq[jq & 1];
+        if (jq + 2 < NQ) gq[jq & 1] = g4[jq + 2];
+        else gq[jq & 1] = g4n[jq + 2 - NQ];
+        if (jq == NQ - 1) {
+          qn = qsm[min(r + 1, RB - 1) * 64 + lane];
+          if (DQ) accn = gneg[min(r + 1, RB - 1)];
+        }
+        const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int j = jq * 4 + t;
+          if (j < MC) {
+            const float y = half_step(qv - kreg[j]);
+            if (DQ) acc = fmaf(gg[t], y, acc);
+            if (DK) {
+              dka[j] = fmaf(gg[t], y, dka[j]);
+              asm volatile("" : "+v"(dka[j]));  // update in place, not after the row
+            }
           }
         }
-        if (DQ && cval) dq[((size_t)bh * N + rb + r0 + rr) * C + c] = from_acc<f16s>(dqa);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (DQ) {
+        // Materialise the sum here: sunk into the store's branch, the
+        // accumulation would keep every column's step value live.
+        asm volatile("" : "+v"(acc));
+        if (cval) dq[((size_t)bh * N + rb + r) * C + c] = from_acc<f16s>(acc);
       }
     }
+    wave_sync();
   }
 
-  if (rowsPerWave < 0) partial[lane] = (float)sink;  // never taken; keeps the warming loads
-
   if (DK) {
-    for (int w = 0; w < W; ++w) {
-      if (wave == w) {
+    // This wave's grad_key partial: column sums of g minus the accumulated 2g*step.
+    if (lane < MC) hsm[lane] = 0.5f * hsum;
+    wave_sync();
 #pragma unroll
-        for (int j = 0; j < MC; ++j) red[j * 64 + lane] = (w == 0 ? 0.0f : red[j * 64 + lane]) + dka[j];
-      }
-      __syncthreads();
-    }
-    float* pb = partial + ((size_t)slice * nx + x) * 64 * MC;
-    for (int t = threadIdx.x; t < 64 * MC; t += blockDim.x) {
-      const int cl = t / MC, j = t - cl * MC;
-      pb[t] = red[j * 64 + cl];
-    }
+    for (int j = 0; j < MC; ++j) dka[j] = hsm[j] - dka[j];
+    bcast_reduce_dk<MC>(dka, reinterpret_cast<float*>(smem), W, wave, lane,
+                        partial + ((size_t)slice * nx + x) * 64 * MC);
   }
 }
 
@@ -688,8 +834,26 @@ laplace_dk_reduce_kernel(const typename AccOf<T>::type* __restrict__ partial, T*
   if (cc >= C) return;
   const A* pb = partial + (size_t)slice * nx * 64 * M + t;
   A s = A(0);
+#pragma unroll 8
   for (int x = 0; x < nx; ++x) s += pb[(size_t)x * 64 * M];
   dk[((size_t)bh * C + cc) * M + j] = from_acc<T>(s);
+}
+
+// Same sum over column-major partials ([M][64] per workgroup, channel fastest).
+__global__ void __launch_bounds__(256)
+laplace_dk_reduce_cm_kernel(const float* __restrict__ partial, f16s* __restrict__ dk, int nx, int M, int C) {
+  const int bh = blockIdx.z, cb = blockIdx.y;
+  const int slice = bh * gridDim.y + cb;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 64 * M) return;
+  const int j = t >> 6, cl = t & 63;
+  const int cc = cb * 64 + cl;
+  if (cc >= C) return;
+  const float* pb = partial + (size_t)slice * nx * 64 * M + t;
+  float s = 0.0f;
+#pragma unroll 8
+  for (int x = 0; x < nx; ++x) s += pb[(size_t)x * 64 * M];
+  dk[((size_t)bh * C + cc) * M + j] = from_acc<f16s>(s);
 }
 
 // ---------------------------------------------------------------------------
@@ -818,78 +982,72 @@ int pick_fwd_jb(int64_t M) {
   return best;
 }
 
-bool fwd_sgpr_ok(int dtype, const Dims& d, const void* q) {
-  if (dtype == LFAMD_F64) return false;
-  const int64_t ck = 16 / (int64_t)dtype_size(dtype);
-  return d.C % ck == 0 && d.C / ck <= kFwdSgQV && (reinterpret_cast<uintptr_t>(q) & 15) == 0;
+// Column block: the least padding W*JB - M with W = ceil(M/JB) <= 16 waves,
+// ties to the block count nearest 8 waves.
+int pick_fb_jb(int64_t M) {
+  int best = 16, bestWaste = 1 << 30, bestDist = 1 << 30;
+  for (int jb : {4, 7, 8, 16}) {
+    const int w = ceil_div((int)M, jb);
+    if (w > 16) continue;
+    const int waste = w * jb - (int)M, dist = std::abs(w - 8);
+    if (waste < bestWaste || (waste == bestWaste && dist < bestDist)) {
+      best = jb;
+      bestWaste = waste;
+      bestDist = dist;
+    }
+  }
+  return best;
 }
 
-// 16-byte query vectors per row rounded up to the instantiated 2, 4, 8, 16.
-int fwd_nv(int dtype, int64_t C) {
-  const int64_t ck = 16 / (int64_t)dtype_size(dtype);
-  const int64_t v = (C + ck - 1) / ck;
-  return v <= 2 ? 2 : v <= 4 ? 4 : v <= 8 ? 8 : 16;
+constexpr int kFbR = 2;  // query rows per lane of the broadcast forward
+
+template <typename T> constexpr int dtype_of();
+template <> constexpr int dtype_of<float>() { return LFAMD_F32; }
+template <> constexpr int dtype_of<f16s>() { return LFAMD_F16; }
+template <> constexpr int dtype_of<bf16s>() { return LFAMD_BF16; }
+template <> constexpr int dtype_of<double>() { return LFAMD_F64; }
+
+// LDS of the broadcast forward: fp32 key tile [C][W*JBS], then the query tile
+// [64R][C/EV + 1] 16-byte vectors, which the output tile [64R][M] reuses.
+size_t fb_lds_bytes(int dtype, const Dims& d) {
+  const int jb = pick_fb_jb(d.M);
+  const int W = ceil_div((int)d.M, jb);
+  const size_t es = dtype_size(dtype);
+  const size_t qtile = (size_t)64 * kFbR * (d.C * es / 16 + 1) * 16;
+  const size_t otile = (size_t)64 * kFbR * d.M * es;
+  return (size_t)W * d.C * fb_pitch(jb) * 4 + std::max(qtile, otile);
 }
 
-int pick_fwd_sgpr_jb(int64_t M);
-
-size_t fwd_workspace_bytes(int dtype, const Dims& d) {
-  if (dtype == LFAMD_F64) return 0;
-  const int64_t kcp = (int64_t)fwd_nv(dtype, d.C) * (16 / (int64_t)dtype_size(dtype));
-  const int jb = pick_fwd_sgpr_jb(d.M);
-  const int64_t njb = (d.M + jb - 1) / jb;
-  return (size_t)d.BH() * njb * kcp * round_up(jb, 8) * sizeof(float);
+// Broadcast forward: a non-fp64 type, C % 8 == 0, 16-byte aligned query,
+// M <= 256 and the key and output tiles within the LDS of one workgroup.
+bool fwd_bcast_ok(int dtype, const Dims& d, const void* q) {
+  if (dtype == LFAMD_F64 || d.C % kFbKC != 0 || d.M > 256) return false;
+  if ((reinterpret_cast<uintptr_t>(q) & 15) != 0) return false;
+  return fb_lds_bytes(dtype, d) <= (size_t)max_lds_bytes();
 }
 
-template <typename T, int JB, int NV>
-int launch_fwd_sgpr_jb(const T* q, const T* k, T* o, float* kf, const Dims& d, hipStream_t st) {
-  const int M = (int)d.M, N = (int)d.N, C = (int)d.C;
-  const int KCp = NV * QChunk<T>::value;
-  constexpr int JBS = round_up(JB, 8);
-  const int nJB = ceil_div(M, JB);
-  const int pblocks = (int)std::min<int64_t>(4096, (d.BH() * nJB * KCp * JBS + 255) / 256);
-  hipLaunchKernelGGL(laplace_key_f32_kernel<T>, dim3(pblocks), dim3(256), 0, st, k, kf, d.BH(), C, KCp, M, JB, JBS,
-                     nJB);
-  int s = check_launch("laplace forward key conversion");
-  if (s) return s;
-  const int W = std::min(16, ceil_div(M, JB));
-  const int cols = W * JB;
-  dim3 grid(ceil_div(N, 64), ceil_div(M, cols), (unsigned)d.BH());
-  int flags = 0;
-  if (cols == M && (reinterpret_cast<uintptr_t>(o) & 15) == 0 && ((size_t)N * M * sizeof(T)) % 16 == 0)
-    flags |= kFwdVecOut;
-  hipLaunchKernelGGL((laplace_fwd_sgpr_kernel<T, JB, NV>), grid, dim3(64 * W), (size_t)64 * cols * sizeof(T), st, q,
-                     kf, o, N, M, C, nJB, cols, flags);
+template <typename T, int JB>
+int launch_fwd_bcast_jb(const void* q, const void* k, void* o, const Dims& d, hipStream_t st) {
+  const int W = ceil_div((int)d.M, JB);
+  const size_t lds = fb_lds_bytes(dtype_of<T>(), d);
+  auto kern = laplace_fwd_bcast_kernel<T, JB, kFbR>;
+  if (lds > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
+  dim3 grid(ceil_div((int)d.N, 64 * kFbR), (unsigned)d.BH());
+  hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, st, static_cast<const T*>(q), static_cast<const T*>(k),
+                     static_cast<T*>(o), (int)d.N, (int)d.M, (int)d.C);
   return check_launch("laplace forward");
 }
 
-// Column block of the SGPR forward: at most 16 (32 fp32 key values per channel
-// would not fit the scalar register file once several channels are in flight).
-int pick_fwd_sgpr_jb(int64_t M) {
-  const int jb = pick_fwd_jb(M);
-  return jb > 16 ? 16 : jb;
-}
-
-template <typename T, int NV>
-int launch_fwd_sgpr_nv(const T* q, const T* k, T* o, float* kf, const Dims& d, hipStream_t st) {
-  switch (pick_fwd_sgpr_jb(d.M)) {
-    case 7: return launch_fwd_sgpr_jb<T, 7, NV>(q, k, o, kf, d, st);
-    case 8: return launch_fwd_sgpr_jb<T, 8, NV>(q, k, o, kf, d, st);
-    default: return launch_fwd_sgpr_jb<T, 16, NV>(q, k, o, kf, d, st);
-  }
-}
-
 template <typename T>
-int launch_fwd_sgpr(const void* q, const void* k, void* o, void* ws, int nv, const Dims& d, hipStream_t st) {
-  const T* qq = static_cast<const T*>(q);
-  const T* kk = static_cast<const T*>(k);
-  T* oo = static_cast<T*>(o);
-  float* kf = static_cast<float*>(ws);
-  switch (nv) {
-    case 2: return launch_fwd_sgpr_nv<T, 2>(qq, kk, oo, kf, d, st);
-    case 4: return launch_fwd_sgpr_nv<T, 4>(qq, kk, oo, kf, d, st);
-    case 8: return launch_fwd_sgpr_nv<T, 8>(qq, kk, oo, kf, d, st);
-    default: return launch_fwd_sgpr_nv<T, 16>(qq, kk, oo, kf, d, st);
+int launch_fwd_bcast(const void* q, const void* k, void* o, const Dims& d, hipStream_t st) {
+  switch (pick_fb_jb(d.M)) {
+    case 4: return launch_fwd_bcast_jb<T, 4>(q, k, o, d, st);
+    case 7: return launch_fwd_bcast_jb<T, 7>(q, k, o, d, st);
+    case 8: return launch_fwd_bcast_jb<T, 8>(q, k, o, d, st);
+    default: return launch_fwd_bcast_jb<T, 16>(q, k, o, d, st);
   }
 }
 
@@ -959,25 +1117,25 @@ BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes, size_t gByt
   return p;
 }
 
-// Plan of the SGPR fast path: 3 waves per SIMD resident, up to 12 waves per workgroup.
-struct SgPlan {
+// Plan of the fp16 broadcast backward: 3 waves per SIMD resident (4 for M <= 16).
+struct BcPlan {
   int W, nx, rowsPerWave, ncb;
   size_t lds, partialElems;
 };
 
-bool sgpr_path_ok(int dtype, const Dims& d, const void* g) {
+bool bcast_bwd_ok(int dtype, const Dims& d, const void* g) {
   if (dtype != LFAMD_F16) return false;
   if (!(d.M == 16 || d.M == 32 || d.M == 49 || d.M == 64)) return false;
   if ((d.N * d.M) % 2 != 0) return false;
   return (reinterpret_cast<uintptr_t>(g) & 3) == 0;
 }
 
-SgPlan plan_sgpr(const Dims& d, bool dkey) {
-  SgPlan p{};
+BcPlan plan_bcast(const Dims& d, bool dkey) {
+  BcPlan p{};
   p.ncb = ceil_div((int)d.C, 64);
   const int64_t slices = d.BH() * p.ncb;
   const int N = (int)std::max<int64_t>(d.N, 1);
-  const int wmax = sgpr_max_waves((int)d.M);
+  const int wmax = bcast_max_waves((int)d.M);
   const int target = wmax * num_cus();
   int64_t wps = std::max<int64_t>(1, ceil_div(target, (int)std::min<int64_t>(slices, target)));
   wps = std::min<int64_t>(wps, ceil_div(N, 8));
@@ -985,35 +1143,37 @@ SgPlan plan_sgpr(const Dims& d, bool dkey) {
   p.W = W;
   p.nx = ceil_div((int)wps, W);
   p.rowsPerWave = round_up(ceil_div(N, p.nx * W), 2);
-  p.lds = (size_t)d.M * 64 * 4 * (dkey ? 2 : 1);
+  const int mp = bcast_pitch((int)d.M);
+  p.lds = ((size_t)d.M * 64 + (size_t)W * (kBcRB * mp + kBcRB + mp + kBcRB * 64)) * 4;
+  if (dkey) p.lds = std::max(p.lds, (size_t)std::min(W, kBcBufs) * d.M * 64 * 4);
   p.partialElems = dkey ? (size_t)slices * p.nx * 64 * (size_t)d.M : 0;
   return p;
 }
 
 template <int MC, bool DQ, bool DK>
-int launch_sgpr_mc(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                   const SgPlan& p, hipStream_t st) {
+int launch_bcast_bwd_mc(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
+                   const BcPlan& p, hipStream_t st) {
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
-  hipLaunchKernelGGL((laplace_bwd_sgpr_kernel<MC, DQ, DK>), grid, dim3(64 * p.W), p.lds, st,
+  hipLaunchKernelGGL((laplace_bwd_bcast_kernel<MC, DQ, DK>), grid, dim3(64 * p.W), p.lds, st,
                      static_cast<const f16s*>(g), static_cast<const f16s*>(q), static_cast<const f16s*>(k),
                      static_cast<f16s*>(dq), static_cast<f16s*>(dk), static_cast<float*>(ws), (int)d.N, (int)d.C,
                      p.rowsPerWave);
   int s = check_launch("laplace backward");
   if (s || !DK) return s;
   dim3 rgrid(ceil_div(64 * MC, 256), p.ncb, (unsigned)d.BH());
-  hipLaunchKernelGGL(laplace_dk_reduce_kernel<f16s>, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
+  hipLaunchKernelGGL(laplace_dk_reduce_cm_kernel, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
                      static_cast<f16s*>(dk), p.nx, MC, (int)d.C);
   return check_launch("laplace backward_key reduction");
 }
 
 template <bool DQ, bool DK>
-int launch_sgpr(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                const SgPlan& p, hipStream_t st) {
+int launch_bcast_bwd(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
+                const BcPlan& p, hipStream_t st) {
   switch (d.M) {
-    case 16: return launch_sgpr_mc<16, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 32: return launch_sgpr_mc<32, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 49: return launch_sgpr_mc<49, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    default: return launch_sgpr_mc<64, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 16: return launch_bcast_bwd_mc<16, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 32: return launch_bcast_bwd_mc<32, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 49: return launch_bcast_bwd_mc<49, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    default: return launch_bcast_bwd_mc<64, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
   }
 }
 
@@ -1092,13 +1252,13 @@ int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq,
   }
   if (!g || !q || !k || (doDq && !dq) || (doDk && !dk)) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
-  if (sgpr_path_ok(dtype, d, g)) {
-    const SgPlan sp = plan_sgpr(d, doDk);
+  if (bcast_bwd_ok(dtype, d, g)) {
+    const BcPlan sp = plan_bcast(d, doDk);
     if (doDk && (!ws || wsBytes < sp.partialElems * 4))
       return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, sp.partialElems * 4, wsBytes);
-    if (doDq && doDk) return launch_sgpr<true, true>(g, q, k, dq, dk, ws, d, sp, st);
-    if (doDq) return launch_sgpr<true, false>(g, q, k, dq, dk, ws, d, sp, st);
-    return launch_sgpr<false, true>(g, q, k, dq, dk, ws, d, sp, st);
+    if (doDq && doDk) return launch_bcast_bwd<true, true>(g, q, k, dq, dk, ws, d, sp, st);
+    if (doDq) return launch_bcast_bwd<true, false>(g, q, k, dq, dk, ws, d, sp, st);
+    return launch_bcast_bwd<false, true>(g, q, k, dq, dk, ws, d, sp, st);
   }
   const BwdPlan p = plan_bwd(d, doDq, doDk, acc, dtype == LFAMD_F16 ? 2 : acc);
   if (doDk) {
@@ -1118,16 +1278,9 @@ using namespace lfamd;
 
 extern "C" {
 
-size_t lfamd_laplace_forward_workspace_size(int dtype, int64_t batch, int64_t heads, int64_t q_len,
-                                            int64_t k_len, int64_t channels) {
-  const Dims d{batch, heads, q_len, k_len, channels};
-  if (!valid_dtype(dtype) || check_dims(d, "workspace") || empty(d) || d.C == 0) return 0;
-  return fwd_workspace_bytes(dtype, d);
-}
-
 int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* output,
                           int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
-                          int64_t channels, void* workspace, size_t workspace_bytes, void* stream) {
+                          int64_t channels, void* stream) {
   if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "laplace forward: unsupported dtype %d", dtype);
   const Dims d{batch, heads, q_len, k_len, channels};
   int s = check_dims(d, "laplace forward");
@@ -1136,12 +1289,11 @@ int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* o
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d.C == 0) return zero_fill(output, d.BH() * d.N * d.M * (int64_t)dtype_size(dtype), st);
   if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace forward: null pointer");
-  if (workspace && workspace_bytes >= fwd_workspace_bytes(dtype, d) && fwd_sgpr_ok(dtype, d, query)) {
-    const int nv = fwd_nv(dtype, d.C);
+  if (fwd_bcast_ok(dtype, d, query)) {
     switch (dtype) {
-      case LFAMD_F32: return launch_fwd_sgpr<float>(query, key, output, workspace, nv, d, st);
-      case LFAMD_F16: return launch_fwd_sgpr<f16s>(query, key, output, workspace, nv, d, st);
-      default: return launch_fwd_sgpr<bf16s>(query, key, output, workspace, nv, d, st);
+      case LFAMD_F32: return launch_fwd_bcast<float>(query, key, output, d, st);
+      case LFAMD_F16: return launch_fwd_bcast<f16s>(query, key, output, d, st);
+      default: return launch_fwd_bcast<bf16s>(query, key, output, d, st);
     }
   }
   switch (dtype) {
@@ -1169,7 +1321,7 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
   // Either backward path may run (the fp16 SGPR path also depends on pointer alignment).
   size_t bytes = plan_bwd(d, true, true, acc, dtype == LFAMD_F16 ? 2 : acc).partialElems * acc;
-  if (dtype == LFAMD_F16) bytes = std::max(bytes, plan_sgpr(d, true).partialElems * 4);
+  if (dtype == LFAMD_F16) bytes = std::max(bytes, plan_bcast(d, true).partialElems * 4);
   return bytes;
 }
 

@@ -79,28 +79,25 @@ __device__ __forceinline__ float mix_fms_fh(float s, uint32_t g, float acc) {
   return r;
 }
 
-// Same two operations with the packed halves in an SGPR (a wave-uniform value).
-template <int GS>
-__device__ __forceinline__ float mix_fma_fs(float s, uint32_t g, float acc) {
-  float r;
-  if constexpr (GS == 0)
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
-  else
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
-  return r;
-}
-template <int GS>
-__device__ __forceinline__ float mix_fms_fs(float s, uint32_t g, float acc) {
-  float r;
-  if constexpr (GS == 0)
-    asm("v_fma_mix_f32 %0, %1, -%2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
-  else
-    asm("v_fma_mix_f32 %0, %1, -%2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "s"(g), "v"(acc));
-  return r;
-}
-
 // Wave-uniform value hint (moves a VGPR that is known to be uniform to an SGPR).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Orders the LDS accesses of one wave around this point: what any lane of the
+// wave wrote before it is visible to every lane of the wave after it.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Half step of a scaled difference: clamp(0.5 * d + 0.5) to [0, 1]. The
+// compiler folds the median into the clamp output modifier of the v_fma_f32
+// (kernels run with DX10 clamping), one full-rate VALU instruction with inline
+// constants. For a d that is 0 or at least 1 in magnitude the result is exactly
+// 0 (d < 0), 0.5 (d == 0) or 1 (d > 0), i.e. (sgn(d) + 1) / 2.
+__device__ __forceinline__ float half_step(float d) {
+  return __builtin_amdgcn_fmed3f(__builtin_fmaf(d, 0.5f, 0.5f), 0.0f, 1.0f);
+}
 
 __host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int round_up(int a, int b) { return ceil_div(a, b) * b; }

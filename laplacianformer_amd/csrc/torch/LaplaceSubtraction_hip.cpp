@@ -50,11 +50,8 @@ void LaplaceSubtraction_forward_cuda(const at::Tensor query, const at::Tensor ke
   const Sizes s = sizes_of(query, key);
   check_out(query, output, {s.B, s.H, s.N, s.M}, "output");
   at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
-  const size_t ws_bytes = lfamd_laplace_forward_workspace_size(dt, s.B, s.H, s.N, s.M, s.C);
-  at::Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, query.options().dtype(at::kByte));
   detail::check_status(lfamd_laplace_forward(dt, query.data_ptr(), key.data_ptr(), output.data_ptr(), s.B,
-                                             s.H, s.N, s.M, s.C, ws.data_ptr(), ws_bytes,
-                                             detail::stream_of(query)));
+                                             s.H, s.N, s.M, s.C, detail::stream_of(query)));
 }
 
 void LaplaceSubtraction_backward_query_cuda(const at::Tensor gradOutput, const at::Tensor query,

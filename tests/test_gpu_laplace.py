@@ -62,11 +62,11 @@ def test_laplace_parity(gpu, shape, dt):
     refs = l1_refs(q, k, g, dt)
     check_l1(out, dq, dk, refs, dt, "separate ")
     check_l1(out, dq2, dk2, refs, dt, "fused ")
-    # Forward and dq follow the reference's serial order exactly: bit-identical
-    # to the fp32 (fp64 for double) serial oracle.
+    # The forward follows the reference's serial channel order exactly: bit-identical
+    # to the fp32 (fp64 for double) serial oracle. The gradients are held to the
+    # tolerance only (the fp16 backward sums 2g*step - g instead of g*sgn).
     assert_bitwise(out, oracle.laplace_forward(q, k, dt), dt, "forward bits")
-    if M <= 64:
-        assert_bitwise(dq, oracle.laplace_backward_query(g, q, k, dt), dt, "dq bits")
+    assert torch.equal(dq.cpu(), dq2.cpu()), "grad_query differs between the separate and fused entry points"
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
@@ -96,7 +96,7 @@ def test_laplace_config2_full(gpu):
     check_l1(out, dq, dk, refs, "f16", "separate ")
     check_l1(out, dq2, dk2, refs, "f16", "fused ")
     assert_bitwise(out, oracle.laplace_forward(q, k, "f16"), "f16", "forward bits")
-    assert_bitwise(dq, oracle.laplace_backward_query(g, q, k, "f16"), "f16", "dq bits")
+    assert torch.equal(dq.cpu(), dq2.cpu())
     # Size-independent identity: sum_i dq[i,c] + sum_j dk[c,j] = 0 (exactly, in real arithmetic).
     s = dq2.double().sum(dim=2) + dk2.double().sum(dim=3)
     assert s.abs().max().item() < 0.05 * dq2.double().abs().sum(dim=2).max().item() + 1.0
@@ -173,19 +173,10 @@ def test_capi_direct(gpu):
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=gpu)
     torch.cuda.synchronize()
     s = ctypes.c_void_p(st.cuda_stream)
-    fws_bytes = lib.lfamd_laplace_forward_workspace_size(dt, B, H, N, M, C)
-    fws = torch.empty(max(fws_bytes, 1), dtype=torch.uint8, device=gpu)
-    out_nows = torch.empty_like(out)
-    torch.cuda.synchronize()
-    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out.data_ptr(), B, H, N, M, C,
-                                       fws.data_ptr(), fws_bytes, s))
-    # Without a workspace the LDS-staged kernel runs; results are bit-identical.
-    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out_nows.data_ptr(), B, H, N, M, C,
-                                       None, 0, s))
+    lf.check(lib.lfamd_laplace_forward(dt, qd.data_ptr(), kd.data_ptr(), out.data_ptr(), B, H, N, M, C, s))
     lf.check(lib.lfamd_laplace_backward(dt, gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), dq.data_ptr(),
                                         dk.data_ptr(), B, H, N, M, C, ws.data_ptr(), ws_bytes, s))
     st.synchronize()
-    assert torch.equal(out.cpu(), out_nows.cpu())
     assert_bitwise(out, oracle.laplace_forward(q, k, "f16"), "f16")
     check_l1(out, dq, dk, l1_refs(q, k, g, "f16"), "f16", "capi ")
     # Too small a workspace is rejected before anything is launched.
