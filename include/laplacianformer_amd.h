@@ -102,19 +102,30 @@ int lfamd_laplace_reduce_forward(int dtype, const void* query, const void* key,
 
 /* ---- NewtonInverse ------------------------------------------------------ */
 
+/* Bytes of device workspace lfamd_newton_forward / lfamd_newton_backward need:
+ * 0 for n <= 128 (matrices stay in LDS) and for fp64; for 128 < n <= 256 four
+ * fp32 copies per matrix padded to 64*ceil(n/64) (the products run as batched
+ * GEMMs). No reference counterpart (the reference stops at n = 128). */
+size_t lfamd_newton_workspace_size(int dtype, int64_t batch_heads, int64_t n);
+
 /* Newton-Schulz inverse of P = mat + 0.01*I for each of the batch_heads n x n
- * matrices: alpha = 1.8 / (max_i sum_j P_ij)^2, V0 = alpha*P,
- * V <- 2V - V(PV) `iters` times (fp32 accumulation; fp64 for LFAMD_F64).
- * Supported for 1 <= n <= 128. Replaces laplace::NewtonInverse_forward_cuda
+ * matrices: alpha = 1.8 / (max_i sum_j P_ij)^2, V0 = alpha*P, then `iters`
+ * steps V <- 2V - V(PV) (the reference's order for n <= 112 and here for
+ * n > 128) or V <- 2V - (VP)V (its order for 112 < n <= 128); fp32 arithmetic
+ * (fp64 for LFAMD_F64), one rounding at the store. 1 <= n <= 256 (fp64:
+ * n <= 96). `workspace` (16-byte aligned) of lfamd_newton_workspace_size bytes;
+ * NULL when that is 0. Replaces laplace::NewtonInverse_forward_cuda
  * (reference include/NewtonInverse.h:9-12, src/NewtonInverse_cuda_kernel.cu:764-794). */
 int lfamd_newton_forward(int dtype, const void* mat, void* output, int64_t batch_heads,
-                         int64_t n, int iters, void* stream);
+                         int64_t n, int iters, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
-/* grad_mat = -(V^T G) V^T for V = inverse, G = grad_output.
- * Replaces laplace::NewtonInverse_backward_cuda
+/* grad_mat = -(V^T G) V^T for V = inverse, G = grad_output; workspace as for
+ * lfamd_newton_forward. Replaces laplace::NewtonInverse_backward_cuda
  * (reference include/NewtonInverse.h:14-17, src/NewtonInverse_cuda_kernel.cu:796-833). */
 int lfamd_newton_backward(int dtype, const void* grad_output, const void* inverse,
-                          void* grad_mat, int64_t batch_heads, int64_t n, void* stream);
+                          void* grad_mat, int64_t batch_heads, int64_t n, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* 1 if n is inside the NewtonInverse envelope on this build, else 0.
  * Replaces laplace::NewtonInverse_supports

@@ -32,8 +32,9 @@ CAPI_PROTOTYPES = [
     ("lfamd_laplace_backward_key", _I, [_I, _P, _P, _P, _P] + _DIMS + [_P, _SZ, _P]),
     ("lfamd_laplace_backward", _I, [_I, _P, _P, _P, _P, _P] + _DIMS + [_P, _SZ, _P]),
     ("lfamd_laplace_reduce_forward", _I, [_I, _P, _P, _P] + _DIMS + [_P]),
-    ("lfamd_newton_forward", _I, [_I, _P, _P, _I64, _I64, _I, _P]),
-    ("lfamd_newton_backward", _I, [_I, _P, _P, _P, _I64, _I64, _P]),
+    ("lfamd_newton_workspace_size", _SZ, [_I, _I64, _I64]),
+    ("lfamd_newton_forward", _I, [_I, _P, _P, _I64, _I64, _I, _P, _SZ, _P]),
+    ("lfamd_newton_backward", _I, [_I, _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
     ("lfamd_newton_is_supported", _I, [_I64]),
     ("lfamd_runtime_version", _I, []),
     ("lfamd_status_string", ctypes.c_char_p, [_I]),

@@ -311,12 +311,250 @@ newton_bwd_f64_kernel(const double* __restrict__ gout, const double* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Large matrices, 128 < n <= 256 (no reference counterpart: the reference
+// rejects n > 128). An n x n fp32 matrix no longer fits one workgroup's LDS
+// with its iterate, so each Newton-Schulz step is two batched GEMMs on the
+// matrix cores over fp32 copies in a caller workspace, zero-padded to
+// NP = 64*ceil(n/64):  T = P V,  V' = 2V - V T  (the V(PV) order, ping-pong V).
+// ---------------------------------------------------------------------------
+constexpr int kBgTile = 64;  // output tile per workgroup (4 waves, 32 x 32 each)
+constexpr int kBgK = 16;     // k per LDS stage
+
+// P = f32(mat) + 0.01 I and V0 = alpha P, padded to NP x NP with zeros; alpha
+// from the signed row sums in ascending j (one thread per row, as the
+// LDS-resident kernel does). One workgroup of NP threads per matrix.
+template <typename T>
+__global__ void __launch_bounds__(256)
+newton_big_init_kernel(const T* __restrict__ mat, float* __restrict__ P, float* __restrict__ V, int n, int NP) {
+  __shared__ float red[4];
+  const int i = threadIdx.x;
+  const T* M = mat + (size_t)blockIdx.x * n * n;
+  float* Pm = P + (size_t)blockIdx.x * NP * NP;
+  float* Vm = V + (size_t)blockIdx.x * NP * NP;
+  float rowsum = -3.4e38f;
+  if (i < n) {
+    float sum = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const float p = to_acc(M[(size_t)i * n + j]) + (i == j ? 0.01f : 0.0f);
+      Pm[(size_t)i * NP + j] = p;
+      sum += p;
+    }
+    rowsum = sum;
+  }
+  if (i < NP) {
+    for (int j = (i < n ? n : 0); j < NP; ++j) Pm[(size_t)i * NP + j] = 0.0f;
+  }
+  for (int off = 32; off > 0; off >>= 1) rowsum = fmaxf(rowsum, __shfl_xor(rowsum, off));
+  if ((i & 63) == 0) red[i >> 6] = rowsum;
+  __syncthreads();
+  float m = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = fmaxf(m, red[w]);
+  const float alpha = 1.8f / (m * m);
+  // Each thread scales the row it wrote itself (program order, no barrier needed).
+  if (i < NP)
+    for (int j = 0; j < NP; ++j) Vm[(size_t)i * NP + j] = alpha * Pm[(size_t)i * NP + j];
+}
+
+// f32 copy of an n x n matrix, zero-padded to NP x NP.
+template <typename T>
+__global__ void __launch_bounds__(256)
+newton_big_pack_kernel(const T* __restrict__ src, float* __restrict__ dst, int n, int NP) {
+  const size_t m = blockIdx.y;
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= NP * NP) return;
+  const int i = e / NP, j = e - i * NP;
+  dst[m * NP * NP + e] = (i < n && j < n) ? to_acc(src[m * n * n + (size_t)i * n + j]) : 0.0f;
+}
+
+// dst[i][j] = src[i][j] (i, j < n), rounded once to T; SIGN = -1 negates.
+template <typename T, int SIGN>
+__global__ void __launch_bounds__(256)
+newton_big_unpack_kernel(const float* __restrict__ src, T* __restrict__ dst, int n, int NP) {
+  const size_t m = blockIdx.y;
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n * n) return;
+  const int i = e / n, j = e - i * n;
+  dst[m * n * n + e] = from_acc<T>(SIGN * src[m * NP * NP + (size_t)i * NP + j]);
+}
+
+// Batched D = op(X) op(Y) over NP x NP fp32 matrices (row-major, matrix stride
+// NP*NP), op = transpose when TX / TY. MODE 0: D = XY; 1: D = 2E - XY. Grid: (NP/64)^2 tiles x matrices, flattened so that all tiles of a
+// matrix share blockIdx.x mod 8 (workgroups are dealt to the 8 XCDs round
+// robin, so a matrix's tiles share one L2). Both operands are staged k-major in
+// LDS ([k][64]): the MFMA operand reads (16 consecutive rows or columns per k)
+// are then conflict-free. Two LDS stages, one barrier per stage.
+template <bool TX, bool TY, int MODE>
+__global__ void __launch_bounds__(256)
+newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ E,
+                       float* __restrict__ D, int NP, int nMat) {
+  __shared__ __align__(16) float As[2][kBgK][kBgTile];
+  __shared__ __align__(16) float Bs[2][kBgK][kBgTile];
+  const int nt = NP / kBgTile;
+  const int tiles = nt * nt;
+  // Inverse of the flattening: id = (m % 8) + 8 * (t + tiles * (m / 8)).
+  const int id = blockIdx.x;
+  const int lo = id & 7, hi = id >> 3;
+  const int t = hi % tiles, mg = hi / tiles;
+  const int m = mg * 8 + lo;
+  if (m >= nMat) return;  // whole workgroup
+  const int ti = t / nt, tj = t - ti * nt;
+  const size_t mo = (size_t)m * NP * NP;
+  const float* Xm = X + mo;
+  const float* Ym = Y + mo;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+
+  // Global -> register staging of one k stage: 64 x 16 of op(X) and 16 x 64 of op(Y), one float4 each.
+  float4 ra, rb;
+  auto load = [&](int k0) {
+    if (TX) {  // A[i][k] = X[k][i]: 16 rows of X, 64 contiguous columns
+      const int k = tid >> 4, iq = (tid & 15) * 4;
+      ra = *reinterpret_cast<const float4*>(Xm + (size_t)(k0 + k) * NP + ti * kBgTile + iq);
+    } else {   // A[i][k] = X[i][k]: 64 rows of X, 16 contiguous columns
+      const int i = tid >> 2, kq = (tid & 3) * 4;
+      ra = *reinterpret_cast<const float4*>(Xm + (size_t)(ti * kBgTile + i) * NP + k0 + kq);
+    }
+    if (TY) {  // B[k][j] = Y[j][k]
+      const int j = tid >> 2, kq = (tid & 3) * 4;
+      rb = *reinterpret_cast<const float4*>(Ym + (size_t)(tj * kBgTile + j) * NP + k0 + kq);
+    } else {   // B[k][j] = Y[k][j]
+      const int k = tid >> 4, jq = (tid & 15) * 4;
+      rb = *reinterpret_cast<const float4*>(Ym + (size_t)(k0 + k) * NP + tj * kBgTile + jq);
+    }
+  };
+  auto store = [&](int b) {
+    if (TX) {
+      const int k = tid >> 4, iq = (tid & 15) * 4;
+      *reinterpret_cast<float4*>(&As[b][k][iq]) = ra;
+    } else {
+      const int i = tid >> 2, kq = (tid & 3) * 4;
+      As[b][kq + 0][i] = ra.x; As[b][kq + 1][i] = ra.y; As[b][kq + 2][i] = ra.z; As[b][kq + 3][i] = ra.w;
+    }
+    if (TY) {
+      const int j = tid >> 2, kq = (tid & 3) * 4;
+      Bs[b][kq + 0][j] = rb.x; Bs[b][kq + 1][j] = rb.y; Bs[b][kq + 2][j] = rb.z; Bs[b][kq + 3][j] = rb.w;
+    } else {
+      const int k = tid >> 4, jq = (tid & 15) * 4;
+      *reinterpret_cast<float4*>(&Bs[b][k][jq]) = rb;
+    }
+  };
+
+  v4f acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) acc[r][c] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int nk = NP / kBgK;
+  load(0);
+  store(0);
+  __syncthreads();
+  const int li = lane & 15, lk = lane >> 4;
+  for (int kc = 0; kc < nk; ++kc) {
+    const int b = kc & 1;
+    if (kc + 1 < nk) load((kc + 1) * kBgK);
+#pragma unroll
+    for (int ks = 0; ks < kBgK; ks += 4) {
+      float a[2], bb[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) a[r] = As[b][ks + lk][wr + 16 * r + li];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) bb[c] = Bs[b][ks + lk][wc + 16 * c + li];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], bb[c], acc[r][c], 0, 0, 0);
+    }
+    if (kc + 1 < nk) store(b ^ 1);
+    __syncthreads();
+  }
+
+  float* Dm = D + mo;
+  const float* Em = MODE == 1 ? E + mo : nullptr;
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = ti * kBgTile + wr + 16 * r + 4 * lk + q;
+        const int j = tj * kBgTile + wc + 16 * c + li;
+        const size_t o = (size_t)i * NP + j;
+        float v = acc[r][c][q];
+        if (MODE == 1) v = 2.0f * Em[o] - v;
+        Dm[o] = v;
+      }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kMaxN = 128;
-constexpr int kF64MaxN = 96;  // two fp64 96x97 buffers fill most of gfx950's 160 KB LDS
+constexpr int kMaxLdsN = 128;  // LDS-resident kernels (the reference's envelope)
+constexpr int kMaxN = 256;     // fp32 / fp16 / bf16 through the batched GEMM path
+constexpr int kF64MaxN = 96;   // two fp64 96x97 buffers fill most of gfx950's 160 KB LDS
+
+int big_np(int64_t n) { return (int)((n + kBgTile - 1) / kBgTile) * kBgTile; }
+
+// fp32 NP x NP buffers per matrix the GEMM path uses: P, V, V', T (forward),
+// V, G, S (backward).
+constexpr int kBigBuffers = 4;
+size_t big_workspace_bytes(int64_t bh, int64_t n) {
+  const size_t np = (size_t)big_np(n);
+  return (size_t)bh * kBigBuffers * np * np * 4;
+}
+
+unsigned big_gemm_blocks(int np, int64_t bh) {
+  const int tiles = (np / kBgTile) * (np / kBgTile);
+  return (unsigned)(8 * tiles * ((bh + 7) / 8));  // matrices rounded up to a multiple of 8
+}
+
+template <typename T>
+int big_fwd(const T* mat, T* out, int64_t bh, int n, int iters, float* ws, hipStream_t st) {
+  const int np = big_np(n);
+  const size_t mat_elems = (size_t)np * np;
+  float* P = ws;
+  float* Va = ws + (size_t)bh * mat_elems;
+  float* Vb = ws + 2 * (size_t)bh * mat_elems;
+  float* Tm = ws + 3 * (size_t)bh * mat_elems;
+  hipLaunchKernelGGL(newton_big_init_kernel<T>, dim3((unsigned)bh), dim3(np), 0, st, mat, P, Va, n, np);
+  int s = check_launch("newton forward init");
+  if (s) return s;
+  const unsigned blocks = big_gemm_blocks(np, bh);
+  for (int it = 0; it < iters; ++it) {
+    hipLaunchKernelGGL((newton_big_gemm_kernel<false, false, 0>), dim3(blocks), dim3(256), 0, st, P, Va,
+                       static_cast<const float*>(nullptr), Tm, np, (int)bh);  // T = P V
+    hipLaunchKernelGGL((newton_big_gemm_kernel<false, false, 1>), dim3(blocks), dim3(256), 0, st, Va, Tm, Va, Vb,
+                       np, (int)bh);  // V' = 2V - V T
+    if ((s = check_launch("newton forward step"))) return s;
+    std::swap(Va, Vb);
+  }
+  dim3 ug(ceil_div(n * n, 256), (unsigned)bh);
+  hipLaunchKernelGGL((newton_big_unpack_kernel<T, 1>), ug, dim3(256), 0, st, Va, out, n, np);
+  return check_launch("newton forward output");
+}
+
+template <typename T>
+int big_bwd(const T* g, const T* inv, T* out, int64_t bh, int n, float* ws, hipStream_t st) {
+  const int np = big_np(n);
+  const size_t mat_elems = (size_t)np * np;
+  float* Vf = ws;
+  float* Gf = ws + (size_t)bh * mat_elems;
+  float* S = ws + 2 * (size_t)bh * mat_elems;
+  dim3 pg(ceil_div(np * np, 256), (unsigned)bh);
+  hipLaunchKernelGGL(newton_big_pack_kernel<T>, pg, dim3(256), 0, st, inv, Vf, n, np);
+  hipLaunchKernelGGL(newton_big_pack_kernel<T>, pg, dim3(256), 0, st, g, Gf, n, np);
+  const unsigned blocks = big_gemm_blocks(np, bh);
+  hipLaunchKernelGGL((newton_big_gemm_kernel<true, false, 0>), dim3(blocks), dim3(256), 0, st, Vf, Gf,
+                     static_cast<const float*>(nullptr), S, np, (int)bh);  // S = V^T G
+  hipLaunchKernelGGL((newton_big_gemm_kernel<false, true, 0>), dim3(blocks), dim3(256), 0, st, S, Vf,
+                     static_cast<const float*>(nullptr), Gf, np, (int)bh);  // R = S V^T (into G's slot)
+  int s = check_launch("newton backward products");
+  if (s) return s;
+  dim3 ug(ceil_div(n * n, 256), (unsigned)bh);
+  hipLaunchKernelGGL((newton_big_unpack_kernel<T, -1>), ug, dim3(256), 0, st, Gf, out, n, np);
+  return check_launch("newton backward output");
+}
 
 int bucket(int64_t n) { return (int)((n + 15) / 16) * 16; }
 
@@ -397,9 +635,24 @@ int check_common(int dtype, int64_t bh, int64_t n, const char* who) {
   if (bh < 0 || n < 0) return fail(LFAMD_ERR_ARG, "%s: negative size", who);
   if (n < 1 || n > kMaxN)
     return fail(LFAMD_ERR_UNSUPPORTED, "NewtonInverse: N=%lld is not supported on this device (insufficient smem or out of range)", (long long)n);
-  if (bh > INT32_MAX) return fail(LFAMD_ERR_UNSUPPORTED, "%s: too many matrices", who);
+  if (bh > INT32_MAX / 64) return fail(LFAMD_ERR_UNSUPPORTED, "%s: too many matrices", who);
   if (dtype == LFAMD_F64 && n > kF64MaxN)
     return fail(LFAMD_ERR_UNSUPPORTED, "NewtonInverse: fp64 N=%lld needs more LDS than this device allows (fp64 limit %d)", (long long)n, kF64MaxN);
+  return LFAMD_OK;
+}
+
+size_t workspace_for(int dtype, int64_t bh, int64_t n) {
+  if (dtype == LFAMD_F64 || n <= kMaxLdsN || n > kMaxN || bh <= 0) return 0;
+  return big_workspace_bytes(bh, n);
+}
+
+int check_workspace(int dtype, int64_t bh, int64_t n, const void* ws, size_t bytes, const char* who) {
+  const size_t need = workspace_for(dtype, bh, n);
+  if (need && (!ws || bytes < need))
+    return fail(LFAMD_ERR_ARG, "%s: N=%lld needs a workspace of %zu bytes, %zu given", who, (long long)n, need,
+                ws ? bytes : (size_t)0);
+  if (need && (reinterpret_cast<uintptr_t>(ws) & 15) != 0)
+    return fail(LFAMD_ERR_ARG, "%s: workspace must be 16-byte aligned", who);
   return LFAMD_OK;
 }
 
@@ -412,14 +665,28 @@ extern "C" {
 
 int lfamd_newton_is_supported(int64_t n) { return n >= 1 && n <= kMaxN ? 1 : 0; }
 
+size_t lfamd_newton_workspace_size(int dtype, int64_t batch_heads, int64_t n) {
+  if (!valid_dtype(dtype) || n < 1 || n > kMaxN) return 0;
+  return workspace_for(dtype, batch_heads, n);
+}
+
 int lfamd_newton_forward(int dtype, const void* mat, void* output, int64_t batch_heads,
-                         int64_t n, int iters, void* stream) {
+                         int64_t n, int iters, void* workspace, size_t workspace_bytes, void* stream) {
   int s = check_common(dtype, batch_heads, n, "newton forward");
   if (s) return s;
   if (batch_heads == 0) return ok();
   if (!mat || !output) return fail(LFAMD_ERR_ARG, "newton forward: null pointer");
+  if ((s = check_workspace(dtype, batch_heads, n, workspace, workspace_bytes, "newton forward"))) return s;
   if (iters < 0) iters = 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n > kMaxLdsN) {
+    float* ws = static_cast<float*>(workspace);
+    switch (dtype) {
+      case LFAMD_F32: return big_fwd<float>(static_cast<const float*>(mat), static_cast<float*>(output), batch_heads, (int)n, iters, ws, st);
+      case LFAMD_F16: return big_fwd<f16s>(static_cast<const f16s*>(mat), static_cast<f16s*>(output), batch_heads, (int)n, iters, ws, st);
+      default: return big_fwd<bf16s>(static_cast<const bf16s*>(mat), static_cast<bf16s*>(output), batch_heads, (int)n, iters, ws, st);
+    }
+  }
   switch (dtype) {
     case LFAMD_F32: return fwd_t<float>(mat, output, batch_heads, (int)n, iters, st);
     case LFAMD_F16: return fwd_t<f16s>(mat, output, batch_heads, (int)n, iters, st);
@@ -436,12 +703,22 @@ int lfamd_newton_forward(int dtype, const void* mat, void* output, int64_t batch
 }
 
 int lfamd_newton_backward(int dtype, const void* grad_output, const void* inverse,
-                          void* grad_mat, int64_t batch_heads, int64_t n, void* stream) {
+                          void* grad_mat, int64_t batch_heads, int64_t n, void* workspace,
+                          size_t workspace_bytes, void* stream) {
   int s = check_common(dtype, batch_heads, n, "newton backward");
   if (s) return s;
   if (batch_heads == 0) return ok();
   if (!grad_output || !inverse || !grad_mat) return fail(LFAMD_ERR_ARG, "newton backward: null pointer");
+  if ((s = check_workspace(dtype, batch_heads, n, workspace, workspace_bytes, "newton backward"))) return s;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n > kMaxLdsN) {
+    float* ws = static_cast<float*>(workspace);
+    switch (dtype) {
+      case LFAMD_F32: return big_bwd<float>(static_cast<const float*>(grad_output), static_cast<const float*>(inverse), static_cast<float*>(grad_mat), batch_heads, (int)n, ws, st);
+      case LFAMD_F16: return big_bwd<f16s>(static_cast<const f16s*>(grad_output), static_cast<const f16s*>(inverse), static_cast<f16s*>(grad_mat), batch_heads, (int)n, ws, st);
+      default: return big_bwd<bf16s>(static_cast<const bf16s*>(grad_output), static_cast<const bf16s*>(inverse), static_cast<bf16s*>(grad_mat), batch_heads, (int)n, ws, st);
+    }
+  }
   switch (dtype) {
     case LFAMD_F32: return bwd_t<float>(grad_output, inverse, grad_mat, batch_heads, (int)n, st);
     case LFAMD_F16: return bwd_t<f16s>(grad_output, inverse, grad_mat, batch_heads, (int)n, st);

@@ -19,7 +19,12 @@ void NewtonInverse_forward_cuda(const at::Tensor mat, at::Tensor output, int ite
               " is not supported on this device (insufficient smem or out of range)");
   const int dt = detail::abi_dtype(mat, "newton_inverse_forward");
   detail::same_type(mat, output, "output");
+  // n > 128 runs as batched GEMMs over fp32 copies in a workspace (0 bytes otherwise).
+  const size_t ws_bytes = lfamd_newton_workspace_size(dt, BH, N);
+  at::Tensor ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, mat.options().dtype(at::kByte));
   detail::check_status(lfamd_newton_forward(dt, mat.data_ptr(), output.data_ptr(), BH, N, iter,
+                                            ws_bytes ? ws.data_ptr() : nullptr, ws_bytes,
                                             detail::stream_of(mat)));
 }
 
@@ -35,8 +40,12 @@ void NewtonInverse_backward_cuda(const at::Tensor grad_output, const at::Tensor 
   const int dt = detail::abi_dtype(inverse, "newton_inverse_backward");
   detail::same_type(inverse, grad_output, "grad_output");
   detail::same_type(inverse, grad_mat, "grad_mat");
+  const size_t ws_bytes = lfamd_newton_workspace_size(dt, BH, N);
+  at::Tensor ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, inverse.options().dtype(at::kByte));
   detail::check_status(lfamd_newton_backward(dt, grad_output.data_ptr(), inverse.data_ptr(),
-                                             grad_mat.data_ptr(), BH, N, detail::stream_of(inverse)));
+                                             grad_mat.data_ptr(), BH, N, ws_bytes ? ws.data_ptr() : nullptr,
+                                             ws_bytes, detail::stream_of(inverse)));
 }
 
 }  // namespace laplace

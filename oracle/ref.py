@@ -188,9 +188,10 @@ def laplace_reduce_forward(q, k, dtype: str):
 # ---------------------------------------------------------------------------
 def newton_variant(n: int) -> str:
     """Association order the reference picks for size n (src/NewtonInverse_cuda_kernel.cu:693-728):
-    3-buffer V(PV) below N_MAX=128 (96/112 fit in 160 KB of LDS), 2-buffer (VP)V at 128."""
+    3-buffer V(PV) below N_MAX=128 (96/112 fit in 160 KB of LDS), 2-buffer (VP)V at 128.
+    n > 128 is outside the reference's envelope; this build computes it in the V(PV) order."""
     nmax = ((n + 15) // 16) * 16
-    return "2buf" if nmax >= 128 else "3buf"
+    return "2buf" if nmax == 128 else "3buf"
 
 
 def newton_alpha(P: np.ndarray) -> np.ndarray:

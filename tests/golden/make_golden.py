@@ -78,20 +78,24 @@ def config1():
 def newton_closed():
     rng = np.random.default_rng(7)
     cases = {}
-    for n in (5, 49, 64):
+    for n in (5, 49, 64, 136):
         # Landmark Gram matrix of the BASELINE recipe: exp(-L1(k_i, k_j) / sqrt(d)) + 1e-3 I.
         # Non-negative and symmetric, so lambda_max <= max row sum and alpha*lambda^2 <= 1.8.
         d = 16
         kk = rng.standard_normal((n, d))
         D = np.abs(kk[:, None, :] - kk[None, :, :]).sum(-1)
         A = np.exp(-D / np.sqrt(d)) + 1e-3 * np.eye(n)
+        # n > 128 (the batched-GEMM path) is stored in fp32 to keep the fixture small; its
+        # closed form is computed from exactly the stored fp32 matrix.
+        store = np.float32 if n > 128 else np.float64
+        A = A.astype(store).astype(np.float64)
         P = A + 0.01 * np.eye(n)
         w, U = np.linalg.eigh(P)
         alpha = 1.8 / P.sum(axis=1).max() ** 2
         for it in (0, 1, 4, 10):
             x = (1.0 - (1.0 - alpha * w * w) ** (2 ** it)) / w
-            cases[f"A_{n}"] = A
-            cases[f"X_{n}_{it}"] = (U * x) @ U.T
+            cases[f"A_{n}"] = A.astype(store)
+            cases[f"X_{n}_{it}"] = ((U * x) @ U.T).astype(store)
     np.savez_compressed(os.path.join(HERE, "newton_closed.npz"), **cases)
 
 

@@ -31,7 +31,7 @@ def test_version_probes(L):
     assert L.has_cuda() is False
     assert L.get_cuda_version().startswith("HIP ")
     assert L.get_compiler_version()
-    assert L.NewtonInverse_is_supported(128) and not L.NewtonInverse_is_supported(129)
+    assert L.NewtonInverse_is_supported(256) and not L.NewtonInverse_is_supported(257)
 
 
 def test_cpu_tensors_raise_reference_errors(L):

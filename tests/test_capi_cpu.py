@@ -45,7 +45,7 @@ def test_status_strings_and_version(lib):
 
 
 def test_newton_envelope(lib):
-    table = {0: 0, 1: 1, 16: 1, 49: 1, 64: 1, 100: 1, 128: 1, 129: 0, 256: 0, -3: 0}
+    table = {0: 0, 1: 1, 16: 1, 49: 1, 64: 1, 100: 1, 128: 1, 129: 1, 256: 1, 257: 0, -3: 0}
     for n, want in table.items():
         assert lib.lfamd_newton_is_supported(n) == want, n
 
@@ -58,9 +58,18 @@ def test_argument_errors_without_device(lib):
     # Empty problems succeed without launching anything.
     assert lib.lfamd_laplace_forward(0, null, null, null, 0, 4, 5, 6, 7, null) == 0
     assert lib.lfamd_laplace_backward(1, null, null, null, null, null, 2, 2, 0, 3, 4, null, 0, null) in (0, 4)
-    assert lib.lfamd_newton_forward(0, null, null, 4, 129, 3, null) == 3
-    assert b"N=129" in lib.lfamd_last_error()
-    assert lib.lfamd_newton_forward(3, null, null, 4, 100, 3, null) == 3  # fp64 envelope is n <= 96
-    assert lib.lfamd_newton_backward(9, null, null, null, 4, 16, null) == 2
+    assert lib.lfamd_newton_forward(0, null, null, 4, 257, 3, null, 0, null) == 3
+    assert b"N=257" in lib.lfamd_last_error()
+    assert lib.lfamd_newton_forward(3, null, null, 4, 100, 3, null, 0, null) == 3  # fp64 envelope is n <= 96
+    assert lib.lfamd_newton_backward(9, null, null, null, 4, 16, null, 0, null) == 2
+    # 128 < n <= 256 needs the fp32 workspace; without one the call is rejected before any launch.
+    ws = lib.lfamd_newton_workspace_size(0, 4, 200)
+    assert ws == 4 * 4 * 256 * 256 * 4
+    assert lib.lfamd_newton_workspace_size(0, 4, 128) == 0
+    assert lib.lfamd_newton_workspace_size(3, 4, 90) == 0
+    dummy = ctypes.c_void_p(16)
+    assert lib.lfamd_newton_forward(0, dummy, dummy, 4, 200, 3, null, 0, null) == 1
+    assert b"workspace" in lib.lfamd_last_error()
+    assert lib.lfamd_newton_backward(0, dummy, dummy, dummy, 4, 200, null, ws - 1, null) == 1
     assert lib.lfamd_laplace_backward_workspace_size(1, 32, 1, 3136, 49, 64) > 0
     assert lib.lfamd_laplace_backward_workspace_size(1, 0, 1, 3136, 49, 64) == 0

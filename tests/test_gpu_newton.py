@@ -104,14 +104,14 @@ def test_newton_errors(gpu):
     import laplacianformer_amd as lf
 
     L = lf.ext()
-    A = torch.zeros((1, 1, 129, 129), device=gpu)
-    with pytest.raises(RuntimeError, match="N=129 is not supported"):
+    A = torch.zeros((1, 1, 257, 257), device=gpu)
+    with pytest.raises(RuntimeError, match="N=257 is not supported"):
         L.NewtonInverse_forward(A, torch.empty_like(A), 3)
     with pytest.raises(RuntimeError, match="must be 4D"):
         L.NewtonInverse_forward(torch.zeros((3, 4, 4), device=gpu), torch.empty((3, 4, 4), device=gpu), 3)
     with pytest.raises(RuntimeError, match="same shape"):
         L.NewtonInverse_forward(torch.zeros((1, 1, 4, 4), device=gpu), torch.empty((1, 1, 5, 5), device=gpu), 3)
-    assert L.NewtonInverse_is_supported(128) and not L.NewtonInverse_is_supported(129)
+    assert L.NewtonInverse_is_supported(256) and not L.NewtonInverse_is_supported(257)
     assert not L.NewtonInverse_is_supported(0)
 
 
@@ -134,9 +134,80 @@ def test_newton_golden_closed_form(gpu):
     import laplacianformer_amd as lf
 
     z = np.load(os.path.join(os.path.dirname(__file__), "golden", "newton_closed.npz"))
-    for n in (5, 49, 64):
+    for n in (5, 49, 64, 136):
         A = torch.from_numpy(z[f"A_{n}"]).float().reshape(1, 1, n, n)
         for it in (0, 1, 4, 10):
             out = torch.empty_like(A, device=gpu)
             lf.ext().NewtonInverse_forward(A.to(gpu), out, it)
             assert_newton_close(out, z[f"X_{n}_{it}"][None, None], "f32", f"closed n={n} it={it}")
+
+
+# ---- 128 < n <= 256: batched-GEMM path (beyond the reference's n <= 128) ----
+
+@pytest.mark.parametrize("n", [129, 130, 192, 200, 256])
+@pytest.mark.parametrize("iters", [0, 1, 10])
+def test_newton_large_forward_f32(gpu, n, iters):
+    import laplacianformer_amd as lf
+
+    print(f"newton large forward n={n} iters={iters}", flush=True)
+    A = torch.from_numpy(gram(3, n, 32, seed=n)).float().reshape(3, 1, n, n)
+    out = torch.empty_like(A, device=gpu)
+    lf.ext().NewtonInverse_forward(A.to(gpu), out, iters)
+    assert_newton_close(out, oracle.newton_forward(A, iters, "f32"), "f32", f"n={n} it={iters}")
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_newton_large_forward_dtypes(gpu, dt):
+    import laplacianformer_amd as lf
+
+    n = 200
+    print(f"newton large forward {dt} n={n}", flush=True)
+    A = torch.from_numpy(gram(2, n, 64, seed=300)).reshape(1, 2, n, n).to(TORCH_DT[dt])
+    out = torch.empty_like(A, device=gpu)
+    lf.ext().NewtonInverse_forward(A.to(gpu), out, 10)
+    assert_newton_close(out, oracle.newton_forward(A, 10, dt), dt, f"{dt} n={n}")
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("n", [129, 200, 256])
+def test_newton_large_backward(gpu, dt, n):
+    import laplacianformer_amd as lf
+
+    print(f"newton large backward {dt} n={n}", flush=True)
+    V = gen((2, 1, n, n), 17 + n, dt, scale=0.1)
+    G = gen((2, 1, n, n), 18 + n, dt)
+    out = torch.empty_like(V, device=gpu)
+    lf.ext().NewtonInverse_backward(G.to(gpu), V.to(gpu), out)
+    assert_newton_close(out, oracle.newton_backward(G, V, dt), dt, f"bwd {dt} n={n}", rtol=1e-5)
+
+
+def test_newton_large_closed_form(gpu):
+    """Diagonal A = c I at n = 256: X_k = (1 - (-0.8)^(2^k)) / (c + 0.01) * I, off-diagonal exactly 0."""
+    import laplacianformer_amd as lf
+
+    n, c = 256, 0.3
+    mu = c + 0.01
+    A = (c * torch.eye(n)).reshape(1, 1, n, n)
+    for k in (0, 2, 5):
+        out = torch.empty_like(A, device=gpu)
+        lf.ext().NewtonInverse_forward(A.to(gpu), out, k)
+        d = torch.diagonal(out.cpu().double(), dim1=-2, dim2=-1)
+        assert torch.allclose(d, torch.full_like(d, (1 - (-0.8) ** (2 ** k)) / mu), rtol=2e-6), k
+        assert (out.cpu().double() - torch.diag_embed(d)).abs().max().item() == 0.0
+
+
+def test_newton_config4(gpu):
+    """BASELINE config 4 (Newton part): 128 Gram matrices 256x256 fp32, 16 iterations, fwd + bwd."""
+    import laplacianformer_amd as lf
+
+    print("newton config 4", flush=True)
+    A = torch.from_numpy(gram(128, 256, 64, seed=1004, scale=0.5)).float().reshape(16, 8, 256, 256)
+    G = gen((16, 8, 256, 256), 1014, "f32")
+    Ad, Gd = A.to(gpu), G.to(gpu)
+    V = torch.empty_like(Ad)
+    dA = torch.empty_like(Ad)
+    lf.ext().NewtonInverse_forward(Ad, V, 16)
+    lf.ext().NewtonInverse_backward(Gd, V, dA)
+    ref = oracle.newton_forward(A, 16, "f32")
+    assert_newton_close(V, ref, "f32", "cfg4 fwd")
+    assert_newton_close(dA, oracle.newton_backward(G, V.cpu(), "f32"), "f32", "cfg4 bwd", rtol=1e-5)
