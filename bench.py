@@ -36,7 +36,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU timing (approx)")
-    p.add_argument("--only", choices=["laplace", "newton", "all"], default="all")
+    p.add_argument("--only", choices=["laplace", "newton", "layer", "all"], default="all")
     p.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                    help="after timing, run one plain device copy of MIB MiB (HBM counter calibration)")
     return p.parse_args()
@@ -140,6 +140,31 @@ def bench_newton(args, dev):
     resid = torch.linalg.matrix_norm(P @ V.double() - torch.eye(n, device=dev, dtype=torch.float64)).mean().item()
     return {"wall_ms": wall, "fwd_ms": t_fwd, "bwd_ms": t_bwd, "flops_fwd": flops_fwd, "flops_bwd": flops_bwd,
             "residual_fro_mean": resid, "A": A.cpu(), "G": G.cpu(), "n_mats": nm, "n": n, "iters": iters}
+
+
+def bench_layer(args, dev):
+    """LaplacianFormer attention layer fwd+bwd (B=64 H=2 N=784 d=64 fp16,
+    4x4-pooled landmarks M=49, NewtonInverse 10 it) through the autograd API."""
+    import torch
+
+    import laplacianformer_amd as lf
+
+    B, H, N, d = 64, 2, 784, 64
+    q, k, v, g = (gen((B, H, N, d), 1005 + i, torch.float16).to(dev) for i in range(4))
+    q.requires_grad_()
+    k.requires_grad_()
+    v.requires_grad_()
+
+    def step():
+        out = lf.laplacian_attention(q, k, v, grid=(28, 28), pool=4, iters=10)
+        out.backward(g)
+
+    steps = max(1, args.steps // 10)
+    wall, _ = time_steps([step], steps, max(1, args.warmup // 10))
+    T = B * H * (2 * N * 49 + 49 * 49) * d
+    return {"workload": "BASELINE config 5: LaplacianFormer attention fwd+bwd, B=64 H=2 N=784 (28x28) d=64 "
+                        "fp16, M=49 (4x4 pooled K), NewtonInverse 10 it",
+            "ms_per_step": wall, "l1_triples": T, "steps": steps}
 
 
 def cpu_baseline(lap, ns, budget):
@@ -248,6 +273,7 @@ def main():
     props = torch.cuda.get_device_properties(dev)
     lap = bench_laplace(args, dev) if args.only in ("laplace", "all") else None
     ns = bench_newton(args, dev) if args.only in ("newton", "all") else None
+    layer = bench_layer(args, dev) if args.only in ("layer", "all") else None
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
@@ -297,6 +323,8 @@ def main():
         if not lap:
             line.update({"value": tf, "unit": "TFLOP/s", "ms_per_step": ns["wall_ms"],
                          "config": {"workload": line["newton"]["workload"]}})
+    if layer:
+        line["layer"] = layer
     if args.calib_copy:
         src = torch.empty(args.calib_copy << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)

@@ -5,10 +5,12 @@ returns a module with the same name and exports, backed by hand-written gfx950
 HIP kernels behind the C ABI of ``include/laplacianformer_amd.h``.
 """
 from ._lib import EXT_PATH, LIB_PATH, capi, check, dtype_code, ext
+from .attention import LaplacianAttention, laplacian_attention
 from .functional import (LaplaceSubtractionFunction, NewtonInverseFunction, laplace_subtraction,
                          newton_inverse)
 
 __all__ = [
     "EXT_PATH", "LIB_PATH", "capi", "check", "dtype_code", "ext", "LaplaceSubtractionFunction",
-    "NewtonInverseFunction", "laplace_subtraction", "newton_inverse",
+    "NewtonInverseFunction", "LaplacianAttention", "laplace_subtraction", "laplacian_attention",
+    "newton_inverse",
 ]

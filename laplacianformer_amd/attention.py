@@ -1,0 +1,85 @@
+"""LaplacianFormer attention layer: the immediate caller of LaplaceSubtraction
+and NewtonInverse (no counterpart in the reference, which ships the two ops
+only; the composition follows BASELINE config 5 of this build).
+
+For each (batch, head), with tokens on a grid of gh x gw:
+  Km   = pool x pool average pooling of K over the grid        (M landmarks)
+  Kxy  = exp(-L1(x, y) / sqrt(d))                              (Laplacian kernel)
+  out  = K_qm . NewtonInverse(K_mm, iters) . (K_mk . V)
+The landmark-to-token kernel K_mk is taken as the transpose of K_km
+(L1 is symmetric), so every distance uses the landmarks as the channel-major
+key and no [B,H,d,N] copy of K is made. Everything from the distances on is
+computed in fp32 (fp64 for fp64 inputs): an fp16 distance (~70 at d = 64)
+rounded to its storage type would move exp(-dist/8) by ~0.4 %. The result is
+returned in the input type.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from .functional import LaplaceSubtractionFunction, newton_inverse
+
+
+def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor:
+    """pool x pool average pooling of k [B,H,N,d] over its gh x gw token grid -> [B,H,M,d]."""
+    B, H, N, d = k.shape
+    gh, gw = grid
+    if gh * gw != N or gh % pool or gw % pool:
+        raise ValueError(f"token grid {gh}x{gw} does not match N={N} or pool={pool}")
+    x = k.reshape(B * H, gh, gw, d).permute(0, 3, 1, 2)
+    x = F.avg_pool2d(x, pool)
+    return x.permute(0, 2, 3, 1).reshape(B, H, -1, d).contiguous()
+
+
+def laplace_kernel(x: torch.Tensor, key_cm: torch.Tensor, scale: float) -> torch.Tensor:
+    """exp(-L1(x, key) * scale), key channel-major [B,H,d,M]."""
+    return torch.exp(-LaplaceSubtractionFunction.apply(x, key_cm) * scale)
+
+
+def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid: tuple[int, int] | None = None,
+                        pool: int = 4, iters: int = 10) -> torch.Tensor:
+    """LaplacianFormer attention of q, k, v [B,H,N,d] (autograd through the HIP ops).
+
+    ``grid`` is the token grid (default square); landmarks are ``pool x pool`` averages of k.
+    Returns [B,H,N,d] in the input type.
+    """
+    in_dtype = q.dtype
+    B, H, N, d = q.shape
+    if grid is None:
+        side = math.isqrt(N)
+        grid = (side, side)
+    ct = torch.float64 if q.dtype == torch.float64 else torch.float32
+    q, k, v = q.to(ct), k.to(ct), v.to(ct)
+    km = landmarks(k, grid, pool)
+    km_cm = km.transpose(-1, -2).contiguous()  # [B,H,d,M]: the reference's key layout
+    s = 1.0 / math.sqrt(d)
+    k_qm = laplace_kernel(q, km_cm, s)         # [B,H,N,M]
+    k_mm = laplace_kernel(km, km_cm, s)        # [B,H,M,M]
+    k_km = laplace_kernel(k, km_cm, s)         # [B,H,N,M] = K_mk^T
+    inv = newton_inverse(k_mm, iters)          # [B,H,M,M]
+    kv = torch.matmul(k_km.transpose(-1, -2).contiguous(), v)  # [B,H,M,d]
+    out = torch.matmul(k_qm, torch.matmul(inv, kv))
+    return out.to(in_dtype)
+
+
+class LaplacianAttention(torch.nn.Module):
+    """Multi-head LaplacianFormer attention on a token grid: qkv projection, the
+    Laplacian-kernel Nystrom attention above, output projection."""
+
+    def __init__(self, dim: int, heads: int, pool: int = 4, iters: int = 10):
+        super().__init__()
+        if dim % heads:
+            raise ValueError("dim must be divisible by heads")
+        self.heads, self.pool, self.iters = heads, pool, iters
+        self.qkv = torch.nn.Linear(dim, 3 * dim)
+        self.proj = torch.nn.Linear(dim, dim)
+
+    def forward(self, x: torch.Tensor, grid: tuple[int, int] | None = None) -> torch.Tensor:
+        B, N, C = x.shape
+        qkv = self.qkv(x).reshape(B, N, 3, self.heads, C // self.heads).permute(2, 0, 3, 1, 4)
+        q, k, v = (t.contiguous() for t in qkv)
+        o = laplacian_attention(q, k, v, grid=grid, pool=self.pool, iters=self.iters)
+        return self.proj(o.transpose(1, 2).reshape(B, N, C))

@@ -77,5 +77,5 @@ def laplace_subtraction(query: torch.Tensor, key: torch.Tensor, key_layout: str 
 
 
 def newton_inverse(mat: torch.Tensor, iters: int) -> torch.Tensor:
-    """Newton-Schulz inverse with autograd; mat is ``[B,H,n,n]``, 1 <= n <= 128."""
+    """Newton-Schulz inverse with autograd; mat is ``[B,H,n,n]``, 1 <= n <= 256."""
     return NewtonInverseFunction.apply(mat, iters)

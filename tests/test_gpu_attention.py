@@ -1,0 +1,112 @@
+"""LaplacianFormer attention layer through the HIP ops, against an
+fp64 CPU composition built from torch.cdist (p=1) and the NewtonInverse oracle."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lfcheck import gen
+
+pytestmark = pytest.mark.gpu
+
+
+class _NewtonRef(torch.autograd.Function):
+    """fp64 CPU NewtonInverse: the oracle's iteration forward, -V^T G V^T backward."""
+
+    @staticmethod
+    def forward(ctx, mat, iters):
+        V = torch.from_numpy(oracle.newton_forward(mat.detach().numpy(), iters, "f64"))
+        ctx.save_for_backward(V)
+        return V
+
+    @staticmethod
+    def backward(ctx, g):
+        (V,) = ctx.saved_tensors
+        return torch.from_numpy(oracle.newton_backward(g.numpy(), V.numpy(), "f64")), None
+
+
+def _ref_attention(q, k, v, grid, pool, iters):
+    B, H, N, d = q.shape
+    km = torch.nn.functional.avg_pool2d(k.reshape(B * H, *grid, d).permute(0, 3, 1, 2), pool)
+    km = km.permute(0, 2, 3, 1).reshape(B, H, -1, d)
+    s = 1.0 / math.sqrt(d)
+    k_qm = torch.exp(-torch.cdist(q, km, p=1) * s)
+    k_mm = torch.exp(-torch.cdist(km, km, p=1) * s)
+    k_mk = torch.exp(-torch.cdist(km, k, p=1) * s)
+    inv = _NewtonRef.apply(k_mm, iters)
+    return k_qm @ (inv @ (k_mk @ v))
+
+
+def _norm_close(got, ref, tol, what):
+    got = got.detach().cpu().double()
+    err = (got - ref).abs().max().item()
+    assert err <= tol * ref.abs().max().item(), (what, err, ref.abs().max().item())
+
+
+def _run(gpu, B, H, grid, d, dtype, seed, pool=4, iters=10, slices=None):
+    import laplacianformer_amd as lf
+
+    N = grid[0] * grid[1]
+    q, k, v = (gen((B, H, N, d), seed + i, dtype) for i in range(3))
+    g = gen((B, H, N, d), seed + 3, dtype)
+    qd, kd, vd = (t.to(gpu).requires_grad_() for t in (q, k, v))
+    out = lf.laplacian_attention(qd, kd, vd, grid=grid, pool=pool, iters=iters)
+    out.backward(g.to(gpu))
+    assert out.dtype == q.dtype and out.shape == q.shape
+    sl = slices if slices is not None else [slice(None)]
+    tol = 2e-3 if dtype in ("f16", "bf16") else 1e-4
+    if dtype == "bf16":
+        tol = 2 ** -8
+    for b in sl:
+        qr, kr, vr = (t[b].double().requires_grad_() for t in (q, k, v))
+        ref = _ref_attention(qr, kr, vr, grid, pool, iters)
+        ref.backward(g[b].double())
+        _norm_close(out[b], ref.detach(), tol, "out")
+        _norm_close(qd.grad[b], qr.grad, tol, "dq")
+        _norm_close(kd.grad[b], kr.grad, tol, "dk")
+        _norm_close(vd.grad[b], vr.grad, tol, "dv")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_attention_small(gpu, dtype):
+    print(f"attention small {dtype}", flush=True)
+    _run(gpu, 2, 2, (8, 8), 32, dtype, seed=50)
+
+
+def test_attention_rect_grid(gpu):
+    print("attention rectangular grid", flush=True)
+    _run(gpu, 1, 3, (8, 12), 16, "f32", seed=60, pool=2)
+
+
+def test_attention_config5(gpu):
+    """B=64 H=2 N=784 (28x28) d=64 fp16, 4x4 pooled landmarks (M=49), 10 iterations;
+    full GPU run, CPU fp64 reference on sampled batch entries."""
+    print("attention config 5", flush=True)
+    _run(gpu, 64, 2, (28, 28), 64, "f16", seed=1005, slices=[slice(0, 1), slice(37, 38), slice(63, 64)])
+
+
+def test_attention_gradcheck(gpu):
+    """fp64 end to end on the GPU: torch.autograd.gradcheck of the layer (Newton run to
+    convergence, where -V^T G V^T is the exact derivative)."""
+    import laplacianformer_amd as lf
+
+    print("attention gradcheck", flush=True)
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 1, 16, 4, dtype=torch.float64, device=gpu, requires_grad=True) for _ in range(3))
+    f = lambda a, b, c: lf.laplacian_attention(a, b, c, grid=(4, 4), pool=2, iters=60)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (q, k, v), eps=1e-6, atol=1e-5, rtol=1e-4)
+
+
+def test_attention_module(gpu):
+    import laplacianformer_amd as lf
+
+    torch.manual_seed(1)
+    m = lf.LaplacianAttention(64, 2).to(gpu)
+    x = torch.randn(2, 64, 64, device=gpu, requires_grad=True)
+    y = m(x)
+    y.sum().backward()
+    assert y.shape == x.shape and torch.isfinite(x.grad).all()
+    with pytest.raises(ValueError):
+        lf.LaplacianAttention(63, 2)

@@ -215,6 +215,27 @@ def test_autograd_function(gpu):
     check_l1(out, qd.grad, kd.grad, l1_refs(q, k, g, "f32"), "f32", "autograd ")
 
 
+def test_key_layout_mc(gpu):
+    """key_layout="mc" takes the key as [B,H,M,d] (BASELINE config 1 fixture holds that layout and
+    its fp64 gradient from torch.cdist)."""
+    import os
+
+    import laplacianformer_amd as lf
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "config1_l1.npz"))
+    qd = torch.from_numpy(z["q"]).to(gpu).requires_grad_()
+    kd = torch.from_numpy(z["k_mc"]).to(gpu).requires_grad_()
+    out = lf.laplace_subtraction(qd, kd, key_layout="mc")
+    out.backward(torch.from_numpy(z["g"]).to(gpu))
+    ga = np.abs(z["g"].astype(np.float64))
+    assert_l1_close(out, z["out"], "f32", "mc forward")
+    assert_l1_close(qd.grad, z["dq"], "f32", "mc dq", np.broadcast_to(ga.sum(3, keepdims=True), qd.shape))
+    assert_l1_close(kd.grad, z["dk_mc"], "f32", "mc dk",
+                    np.broadcast_to(np.swapaxes(ga.sum(2, keepdims=True), -1, -2), kd.shape))
+    with pytest.raises(ValueError):
+        lf.laplace_subtraction(qd, kd, key_layout="xy")
+
+
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "f64"])
 def test_golden_kat(gpu, dt):
     """Integer known-answer fixture (tests/golden/kat_l1.npz): exact in every type."""
