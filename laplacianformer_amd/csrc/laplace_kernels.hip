@@ -772,7 +772,10 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__
       const float4* g4 = reinterpret_cast<const float4*>(gsm + r * MP);
       const float4* g4n = reinterpret_cast<const float4*>(gsm + min(r + 1, RB - 1) * MP);
       const float qv = qn;
-      float acc = accn;
+      // grad_query of the row as four independent partial sums (columns j = t
+      // mod 4), combined once at the end: a single chain of MC dependent FMAs
+      // would stall a wave on every column.
+      float acc[4] = {accn, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int jq = 0; jq < NQ; ++jq) {
         const float4 gv = gq[jq & 1];
@@ -788,7 +791,7 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__
           const int j = jq * 4 + t;
           if (j < MC) {
             const float y = half_step(qv - kreg[j]);
-            if (DQ) acc = fmaf(gg[t], y, acc);
+            if (DQ) acc[t] = fmaf(gg[t], y, acc[t]);
             if (DK) {
               dka[j] = fmaf(gg[t], y, dka[j]);
               asm volatile("" : "+v"(dka[j]));  // update in place, not after the row
@@ -798,10 +801,11 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__
         __builtin_amdgcn_sched_barrier(0);
       }
       if (DQ) {
+        float total = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         // Materialise the sum here: sunk into the store's branch, the
         // accumulation would keep every column's step value live.
-        asm volatile("" : "+v"(acc));
-        if (cval) dq[((size_t)bh * N + rb + r) * C + c] = from_acc<f16s>(acc);
+        asm volatile("" : "+v"(total));
+        if (cval) dq[((size_t)bh * N + rb + r) * C + c] = from_acc<f16s>(total);
       }
     }
     wave_sync();
