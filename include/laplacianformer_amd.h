@@ -100,6 +100,36 @@ int lfamd_laplace_reduce_forward(int dtype, const void* query, const void* key,
                                  int64_t q_len, int64_t k_len, int64_t channels,
                                  void* stream);
 
+/* ---- Fused Laplacian kernel K = exp(-scale * dist) ----------------------- */
+
+/* output[b,h,i,j] = expf(-scale * dist[b,h,i,j]) in fp32, dist as in
+ * lfamd_laplace_forward but kept in fp32 (not rounded to the element type).
+ * The exp is applied in the forward's epilogue, so dist never reaches HBM.
+ * No single reference counterpart: it replaces the model-side composition
+ * torch.exp(-LaplaceSubtraction_forward(...) * scale) around
+ * laplace::LaplaceSubtraction_forward_cuda (reference src/wrapper.cpp:81-82).
+ * Returns LFAMD_ERR_UNSUPPORTED outside the fused path (fp64, C % 8 != 0 or
+ * C == 0, M > 256, a query not 16-byte aligned, tiles beyond one workgroup's
+ * LDS); callers then compose the unfused ops. */
+int lfamd_laplace_kernel_forward(int dtype, const void* query, const void* key, float* output,
+                                 int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                                 int64_t channels, float scale, void* stream);
+
+/* Backward of output = expf(-scale * dist): with g = -scale * grad_kernel * kernel
+ * (fp32, formed while staging, never stored), grad_query and grad_key as
+ * lfamd_laplace_backward_query / lfamd_laplace_backward_key give for grad_output = g.
+ * `kernel` is this op's forward output, `grad_kernel` its gradient, both fp32
+ * [B,H,N,M]. Either of grad_query / grad_key may be NULL to skip it; grad_key
+ * needs the workspace lfamd_laplace_backward_workspace_size reports. Fused path:
+ * LFAMD_F16 with M in {16, 32, 49, 64}; LFAMD_ERR_UNSUPPORTED elsewhere. No single
+ * reference counterpart (replaces the composition around
+ * laplace::LaplaceSubtraction_backward_{query,key}_cuda, reference src/wrapper.cpp:84-88). */
+int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const float* kernel,
+                                  const void* query, const void* key, void* grad_query, void* grad_key,
+                                  int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                                  int64_t channels, float scale, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
 /* ---- NewtonInverse ------------------------------------------------------ */
 
 /* Bytes of device workspace lfamd_newton_forward / lfamd_newton_backward need:

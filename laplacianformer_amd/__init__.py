@@ -6,11 +6,11 @@ HIP kernels behind the C ABI of ``include/laplacianformer_amd.h``.
 """
 from ._lib import EXT_PATH, LIB_PATH, capi, check, dtype_code, ext
 from .attention import LaplacianAttention, laplacian_attention
-from .functional import (LaplaceSubtractionFunction, NewtonInverseFunction, laplace_subtraction,
-                         newton_inverse)
+from .functional import (LaplaceKernelFunction, LaplaceSubtractionFunction, NewtonInverseFunction,
+                         laplace_kernel, laplace_subtraction, newton_inverse)
 
 __all__ = [
-    "EXT_PATH", "LIB_PATH", "capi", "check", "dtype_code", "ext", "LaplaceSubtractionFunction",
-    "NewtonInverseFunction", "LaplacianAttention", "laplace_subtraction", "laplacian_attention",
-    "newton_inverse",
+    "EXT_PATH", "LIB_PATH", "capi", "check", "dtype_code", "ext", "LaplaceKernelFunction",
+    "LaplaceSubtractionFunction", "NewtonInverseFunction", "LaplacianAttention", "laplace_kernel",
+    "laplace_subtraction", "laplacian_attention", "newton_inverse",
 ]

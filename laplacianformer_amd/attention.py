@@ -8,10 +8,13 @@ For each (batch, head), with tokens on a grid of gh x gw:
   out  = K_qm . NewtonInverse(K_mm, iters) . (K_mk . V)
 The landmark-to-token kernel K_mk is taken as the transpose of K_km
 (L1 is symmetric), so every distance uses the landmarks as the channel-major
-key and no [B,H,d,N] copy of K is made. Everything from the distances on is
-computed in fp32 (fp64 for fp64 inputs): an fp16 distance (~70 at d = 64)
-rounded to its storage type would move exp(-dist/8) by ~0.4 %. The result is
-returned in the input type.
+key and no [B,H,d,N] copy of K is made. q, k and the landmarks (pooled in
+fp32, stored in the input type) enter the distances in the input type; the
+distances accumulate in fp32 and are never rounded to it (an fp16 distance,
+~70 at d = 64, would move exp(-dist/8) by ~0.4 %): the Laplacian kernels come
+out of the fused distance+exp op in fp32 (fp64 for fp64 inputs), and the
+products from there on run in that type. The result is returned in the input
+type.
 """
 from __future__ import annotations
 
@@ -20,7 +23,7 @@ import math
 import torch
 import torch.nn.functional as F
 
-from .functional import LaplaceSubtractionFunction, newton_inverse
+from .functional import laplace_kernel, newton_inverse
 
 
 def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor:
@@ -32,11 +35,6 @@ def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor
     x = k.reshape(B * H, gh, gw, d).permute(0, 3, 1, 2)
     x = F.avg_pool2d(x, pool)
     return x.permute(0, 2, 3, 1).reshape(B, H, -1, d).contiguous()
-
-
-def laplace_kernel(x: torch.Tensor, key_cm: torch.Tensor, scale: float) -> torch.Tensor:
-    """exp(-L1(x, key) * scale), key channel-major [B,H,d,M]."""
-    return torch.exp(-LaplaceSubtractionFunction.apply(x, key_cm) * scale)
 
 
 def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid: tuple[int, int] | None = None,
@@ -52,15 +50,14 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
         side = math.isqrt(N)
         grid = (side, side)
     ct = torch.float64 if q.dtype == torch.float64 else torch.float32
-    q, k, v = q.to(ct), k.to(ct), v.to(ct)
-    km = landmarks(k, grid, pool)
+    km = landmarks(k.to(ct), grid, pool).to(in_dtype)
     km_cm = km.transpose(-1, -2).contiguous()  # [B,H,d,M]: the reference's key layout
     s = 1.0 / math.sqrt(d)
     k_qm = laplace_kernel(q, km_cm, s)         # [B,H,N,M]
     k_mm = laplace_kernel(km, km_cm, s)        # [B,H,M,M]
     k_km = laplace_kernel(k, km_cm, s)         # [B,H,N,M] = K_mk^T
     inv = newton_inverse(k_mm, iters)          # [B,H,M,M]
-    kv = torch.matmul(k_km.transpose(-1, -2).contiguous(), v)  # [B,H,M,d]
+    kv = torch.matmul(k_km.transpose(-1, -2).contiguous(), v.to(ct))  # [B,H,M,d]
     out = torch.matmul(k_qm, torch.matmul(inv, kv))
     return out.to(in_dtype)
 

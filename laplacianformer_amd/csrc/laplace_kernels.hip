@@ -239,10 +239,18 @@ constexpr int kFbKC = 8;  // channels per query chunk of the broadcast forward
 
 __host__ __device__ constexpr int fb_pitch(int jb) { return (jb + 3) & ~3; }
 
-template <typename T, int JB, int R>
+// Epilogue of the broadcast forward: the distance rounded to the element type,
+// or the Laplacian kernel exp(-scale * distance) in fp32 (LaplacianFormer's
+// K_xy; fp32 because the distance rounded to fp16 would move it by ~0.4 %).
+enum FwdEpi { kEpiDist = 0, kEpiExp = 1 };
+template <typename T, int EPI> struct FwdOut { using type = T; };
+template <typename T> struct FwdOut<T, kEpiExp> { using type = float; };
+
+template <typename T, int JB, int R, int EPI = kEpiDist>
 __global__ void __launch_bounds__(1024)
-laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out,
-                         int N, int M, int C) {
+laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
+                         typename FwdOut<T, EPI>::type* __restrict__ out, int N, int M, int C, float scale) {
+  using O = typename FwdOut<T, EPI>::type;
   constexpr int JBS = fb_pitch(JB);
   constexpr int NG = JBS / 4;
   constexpr int EV = 16 / (int)sizeof(T);  // elements per 16-byte vector
@@ -273,7 +281,7 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
   extern __shared__ __align__(16) unsigned char smem[];
   float* ksm = reinterpret_cast<float*>(smem);                  // [C][W*JBS] key, fp32
   uint4* qsm = reinterpret_cast<uint4*>(ksm + (size_t)C * KP);  // [64R][QP] query rows, raw
-  T* otile = reinterpret_cast<T*>(qsm);                         // [64R][M] output (after the sums)
+  O* otile = reinterpret_cast<O*>(qsm);                         // [64R][M] output (after the sums)
 
   // The block's query rows are one contiguous span: coalesced 16-byte copies.
   const uint4* qsrc = reinterpret_cast<const uint4*>(query + ((size_t)bh * N + i0) * C);
@@ -363,19 +371,25 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
       const int col = wave * JB + j;
-      if (col < M) otile[(r * 64 + lane) * M + col] = from_acc<T>(acc[r][j]);
+      if (col < M) {
+        if constexpr (EPI == kEpiExp)
+          otile[(r * 64 + lane) * M + col] = expf(-scale * acc[r][j]);
+        else
+          otile[(r * 64 + lane) * M + col] = from_acc<T>(acc[r][j]);
+      }
     }
   __syncthreads();
   // Rows [i0, i0 + rows) are one contiguous span of rows*M elements.
   const int n = rows * M;
-  T* dst = out + ((size_t)bh * N + i0) * M;
+  constexpr int OV = 16 / (int)sizeof(O);  // output elements per 16-byte vector
+  O* dst = out + ((size_t)bh * N + i0) * M;
   int done = 0;
   if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-    const int nv = n / EV;
+    const int nv = n / OV;
     const uint4* src4 = reinterpret_cast<const uint4*>(otile);
     uint4* dst4 = reinterpret_cast<uint4*>(dst);
     for (int t = threadIdx.x; t < nv; t += blockDim.x) dst4[t] = src4[t];
-    done = nv * EV;
+    done = nv * OV;
   }
   for (int t = done + threadIdx.x; t < n; t += blockDim.x) dst[t] = otile[t];
 }
@@ -652,15 +666,21 @@ __host__ __device__ constexpr int bcast_max_waves(int mc) { return mc <= 16 ? 16
 // of them (the row loop keeps two groups in flight in a two-slot ring).
 __host__ __device__ constexpr int bcast_pitch(int mc) { return (mc + 7) & ~7; }
 
-template <int MC, bool DQ, bool DK>
+// Where the backward's grad_output comes from: fp16 elements, or (LaplacianFormer's
+// kernel K = exp(-s * dist)) the gradient of K in fp32 together with K, from which
+// the distance's gradient g = -s * gK * K is formed while a batch is staged.
+enum BwdGrad { kGradF16 = 0, kGradKernel = 1 };
+
+template <int MC, bool DQ, bool DK, int GSRC = kGradF16>
 __global__ void __launch_bounds__(64 * bcast_max_waves(MC))
-laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__ query,
+laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict__ gkern,
+                         const float* __restrict__ kern, float gscale, const f16s* __restrict__ query,
                          const f16s* __restrict__ key, f16s* __restrict__ dq, f16s* __restrict__ dk,
                          float* __restrict__ partial, int N, int C, int rowsPerWave) {
   constexpr int RB = kBcRB;
   constexpr int MP = bcast_pitch(MC);            // LDS row pitch (floats)
-  constexpr int GD = RB * MC / 2;                // grad dwords of a full batch
-  constexpr int NL = (GD + 63) / 64;             // dwords per lane per batch
+  constexpr int GD = GSRC == kGradF16 ? RB * MC / 2 : RB * MC;  // grad words of a full batch
+  constexpr int NL = (GD + 63) / 64;             // words per lane per batch
   const int W = blockDim.x >> 6;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -684,14 +704,32 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__
   const f16s* kb = key + (size_t)bh * C * MC;
 
   uint32_t gpre[NL];
+  float kpre[GSRC == kGradKernel ? NL : 1];
+  const float gscale2 = -2.0f * gscale;  // 2 * (-s * gK) * K == (-2s * gK) * K exactly
+  int kwords = 0;                        // valid words of the fetched kernel-gradient batch
   uint16_t qpre[RB];
   auto fetch = [&](int rb) {
-    const int words = min(RB, rowEnd - rb) * MC / 2;
-    const uint32_t* src = gw + (size_t)rb * MC / 2;
+    if constexpr (GSRC == kGradF16) {
+      const int words = min(RB, rowEnd - rb) * MC / 2;
+      const uint32_t* src = gw + (size_t)rb * MC / 2;
 #pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const int e = lane + 64 * t;
-      gpre[t] = e < words ? src[e] : 0u;
+      for (int t = 0; t < NL; ++t) {
+        const int e = lane + 64 * t;
+        gpre[t] = e < words ? src[e] : 0u;
+      }
+    } else {
+      // Branch-free: lanes past the batch re-read its last element (rb < rowEnd,
+      // so words >= MC >= 1) and are zeroed when the batch is staged.
+      const int words = min(RB, rowEnd - rb) * MC;
+      const float* gs = gkern + ((size_t)bh * N + rb) * MC;
+      const float* ks = kern + ((size_t)bh * N + rb) * MC;
+#pragma unroll
+      for (int t = 0; t < NL; ++t) {
+        const int e = min(lane + 64 * t, words - 1);
+        gpre[t] = __builtin_bit_cast(uint32_t, gs[e]);
+        kpre[t] = ks[e];
+      }
+      kwords = words;
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r) qpre[r] = (cval && rb + r < rowEnd) ? qb[(size_t)(rb + r) * C + c].bits : 0;
@@ -715,15 +753,28 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const f16s* __restrict__
 
   for (int rb = rowBeg; rb < rowEnd; rb += RB) {
     const int nr = min(RB, rowEnd - rb);  // uniform
-    // Stage this batch: 2g as fp32 (exact), row-major [RB][MP].
+    // Stage this batch: 2g as fp32, row-major [RB][MP] (exact for fp16 g; for the
+    // kernel gradient g = -s * gK * K, rounded once, then doubled exactly).
+    if constexpr (GSRC == kGradF16) {
 #pragma unroll
-    for (int t = 0; t < NL; ++t) {
-      const int e = 2 * (lane + 64 * t);
-      if (e < RB * MC) {
-        const int r0 = e / MC, j0 = e - r0 * MC;
-        const int r1 = (e + 1) / MC, j1 = e + 1 - r1 * MC;
-        gsm[r0 * MP + j0] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] & 0xffffu));
-        gsm[r1 * MP + j1] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] >> 16));
+      for (int t = 0; t < NL; ++t) {
+        const int e = 2 * (lane + 64 * t);
+        if (e < RB * MC) {
+          const int r0 = e / MC, j0 = e - r0 * MC;
+          const int r1 = (e + 1) / MC, j1 = e + 1 - r1 * MC;
+          gsm[r0 * MP + j0] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] & 0xffffu));
+          gsm[r1 * MP + j1] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] >> 16));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NL; ++t) {
+        const int e = lane + 64 * t;
+        if (e < RB * MC) {
+          const int r = e / MC, j = e - r * MC;
+          const float v = (gscale2 * __builtin_bit_cast(float, gpre[t])) * kpre[t];
+          gsm[r * MP + j] = e < kwords ? v : 0.0f;
+        }
       }
     }
 #pragma unroll
@@ -1012,46 +1063,48 @@ template <> constexpr int dtype_of<bf16s>() { return LFAMD_BF16; }
 template <> constexpr int dtype_of<double>() { return LFAMD_F64; }
 
 // LDS of the broadcast forward: fp32 key tile [C][W*JBS], then the query tile
-// [64R][C/EV + 1] 16-byte vectors, which the output tile [64R][M] reuses.
-size_t fb_lds_bytes(int dtype, const Dims& d) {
+// [64R][C/EV + 1] 16-byte vectors, which the output tile [64R][M] (elements of
+// out_bytes) reuses.
+size_t fb_lds_bytes(int dtype, const Dims& d, size_t out_bytes) {
   const int jb = pick_fb_jb(d.M);
   const int W = ceil_div((int)d.M, jb);
   const size_t es = dtype_size(dtype);
   const size_t qtile = (size_t)64 * kFbR * (d.C * es / 16 + 1) * 16;
-  const size_t otile = (size_t)64 * kFbR * d.M * es;
+  const size_t otile = (size_t)64 * kFbR * d.M * out_bytes;
   return (size_t)W * d.C * fb_pitch(jb) * 4 + std::max(qtile, otile);
 }
 
 // Broadcast forward: a non-fp64 type, C % 8 == 0, 16-byte aligned query,
 // M <= 256 and the key and output tiles within the LDS of one workgroup.
-bool fwd_bcast_ok(int dtype, const Dims& d, const void* q) {
+bool fwd_bcast_ok(int dtype, const Dims& d, const void* q, size_t out_bytes) {
   if (dtype == LFAMD_F64 || d.C % kFbKC != 0 || d.M > 256) return false;
   if ((reinterpret_cast<uintptr_t>(q) & 15) != 0) return false;
-  return fb_lds_bytes(dtype, d) <= (size_t)max_lds_bytes();
+  return fb_lds_bytes(dtype, d, out_bytes) <= (size_t)max_lds_bytes();
 }
 
-template <typename T, int JB>
-int launch_fwd_bcast_jb(const void* q, const void* k, void* o, const Dims& d, hipStream_t st) {
+template <typename T, int JB, int EPI>
+int launch_fwd_bcast_jb(const void* q, const void* k, void* o, const Dims& d, float scale, hipStream_t st) {
+  using O = typename FwdOut<T, EPI>::type;
   const int W = ceil_div((int)d.M, JB);
-  const size_t lds = fb_lds_bytes(dtype_of<T>(), d);
-  auto kern = laplace_fwd_bcast_kernel<T, JB, kFbR>;
+  const size_t lds = fb_lds_bytes(dtype_of<T>(), d, sizeof(O));
+  auto kern = laplace_fwd_bcast_kernel<T, JB, kFbR, EPI>;
   if (lds > 65536 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds) != hipSuccess)
     return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
   dim3 grid(ceil_div((int)d.N, 64 * kFbR), (unsigned)d.BH());
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, st, static_cast<const T*>(q), static_cast<const T*>(k),
-                     static_cast<T*>(o), (int)d.N, (int)d.M, (int)d.C);
+                     static_cast<O*>(o), (int)d.N, (int)d.M, (int)d.C, scale);
   return check_launch("laplace forward");
 }
 
-template <typename T>
-int launch_fwd_bcast(const void* q, const void* k, void* o, const Dims& d, hipStream_t st) {
+template <typename T, int EPI = kEpiDist>
+int launch_fwd_bcast(const void* q, const void* k, void* o, const Dims& d, hipStream_t st, float scale = 0.0f) {
   switch (pick_fb_jb(d.M)) {
-    case 4: return launch_fwd_bcast_jb<T, 4>(q, k, o, d, st);
-    case 7: return launch_fwd_bcast_jb<T, 7>(q, k, o, d, st);
-    case 8: return launch_fwd_bcast_jb<T, 8>(q, k, o, d, st);
-    default: return launch_fwd_bcast_jb<T, 16>(q, k, o, d, st);
+    case 4: return launch_fwd_bcast_jb<T, 4, EPI>(q, k, o, d, scale, st);
+    case 7: return launch_fwd_bcast_jb<T, 7, EPI>(q, k, o, d, scale, st);
+    case 8: return launch_fwd_bcast_jb<T, 8, EPI>(q, k, o, d, scale, st);
+    default: return launch_fwd_bcast_jb<T, 16, EPI>(q, k, o, d, scale, st);
   }
 }
 
@@ -1154,14 +1207,21 @@ BcPlan plan_bcast(const Dims& d, bool dkey) {
   return p;
 }
 
-template <int MC, bool DQ, bool DK>
+// Kernel-gradient source of the backward (LaplacianFormer's K = exp(-s * dist)).
+struct KernGrad {
+  const float* gk = nullptr;
+  const float* kv = nullptr;
+  float scale = 0.0f;
+};
+
+template <int MC, bool DQ, bool DK, int GSRC = kGradF16>
 int launch_bcast_bwd_mc(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                   const BcPlan& p, hipStream_t st) {
+                        const BcPlan& p, hipStream_t st, KernGrad kg = {}) {
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
-  hipLaunchKernelGGL((laplace_bwd_bcast_kernel<MC, DQ, DK>), grid, dim3(64 * p.W), p.lds, st,
-                     static_cast<const f16s*>(g), static_cast<const f16s*>(q), static_cast<const f16s*>(k),
-                     static_cast<f16s*>(dq), static_cast<f16s*>(dk), static_cast<float*>(ws), (int)d.N, (int)d.C,
-                     p.rowsPerWave);
+  hipLaunchKernelGGL((laplace_bwd_bcast_kernel<MC, DQ, DK, GSRC>), grid, dim3(64 * p.W), p.lds, st,
+                     static_cast<const f16s*>(g), kg.gk, kg.kv, kg.scale, static_cast<const f16s*>(q),
+                     static_cast<const f16s*>(k), static_cast<f16s*>(dq), static_cast<f16s*>(dk),
+                     static_cast<float*>(ws), (int)d.N, (int)d.C, p.rowsPerWave);
   int s = check_launch("laplace backward");
   if (s || !DK) return s;
   dim3 rgrid(ceil_div(64 * MC, 256), p.ncb, (unsigned)d.BH());
@@ -1170,15 +1230,20 @@ int launch_bcast_bwd_mc(const void* g, const void* q, const void* k, void* dq, v
   return check_launch("laplace backward_key reduction");
 }
 
-template <bool DQ, bool DK>
+template <bool DQ, bool DK, int GSRC = kGradF16>
 int launch_bcast_bwd(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                const BcPlan& p, hipStream_t st) {
+                     const BcPlan& p, hipStream_t st, KernGrad kg = {}) {
   switch (d.M) {
-    case 16: return launch_bcast_bwd_mc<16, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 32: return launch_bcast_bwd_mc<32, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 49: return launch_bcast_bwd_mc<49, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    default: return launch_bcast_bwd_mc<64, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 16: return launch_bcast_bwd_mc<16, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 32: return launch_bcast_bwd_mc<32, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 49: return launch_bcast_bwd_mc<49, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    default: return launch_bcast_bwd_mc<64, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
   }
+}
+
+// The fused kernel-gradient backward runs on the fp16 broadcast path only.
+bool kernel_bwd_ok(int dtype, const Dims& d) {
+  return dtype == LFAMD_F16 && (d.M == 16 || d.M == 32 || d.M == 49 || d.M == 64);
 }
 
 template <typename T, int JB, bool DQ, bool DK>
@@ -1293,7 +1358,7 @@ int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* o
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d.C == 0) return zero_fill(output, d.BH() * d.N * d.M * (int64_t)dtype_size(dtype), st);
   if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace forward: null pointer");
-  if (fwd_bcast_ok(dtype, d, query)) {
+  if (fwd_bcast_ok(dtype, d, query, dtype_size(dtype))) {
     switch (dtype) {
       case LFAMD_F32: return launch_fwd_bcast<float>(query, key, output, d, st);
       case LFAMD_F16: return launch_fwd_bcast<f16s>(query, key, output, d, st);
@@ -1347,6 +1412,55 @@ int lfamd_laplace_backward(int dtype, const void* grad_output, const void* query
   return bwd_common(dtype, grad_output, query, key, grad_query, grad_key,
                     Dims{batch, heads, q_len, k_len, channels}, workspace, workspace_bytes, stream,
                     true, true, "laplace backward");
+}
+
+int lfamd_laplace_kernel_forward(int dtype, const void* query, const void* key, float* output,
+                                 int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                                 int64_t channels, float scale, void* stream) {
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "laplace kernel forward: unsupported dtype %d", dtype);
+  const Dims d{batch, heads, q_len, k_len, channels};
+  int s = check_dims(d, "laplace kernel forward");
+  if (s) return s;
+  if (empty(d)) return ok();
+  if (d.C == 0 || !fwd_bcast_ok(dtype, d, query, sizeof(float)))
+    return fail(LFAMD_ERR_UNSUPPORTED, "laplace kernel forward: no fused path for dtype %d, M=%lld, C=%lld",
+                dtype, (long long)d.M, (long long)d.C);
+  if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace kernel forward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LFAMD_F32: return launch_fwd_bcast<float, kEpiExp>(query, key, output, d, st, scale);
+    case LFAMD_F16: return launch_fwd_bcast<f16s, kEpiExp>(query, key, output, d, st, scale);
+    default: return launch_fwd_bcast<bf16s, kEpiExp>(query, key, output, d, st, scale);
+  }
+}
+
+int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const float* kernel,
+                                  const void* query, const void* key, void* grad_query, void* grad_key,
+                                  int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                                  int64_t channels, float scale, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  const char* who = "laplace kernel backward";
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dtype);
+  const Dims d{batch, heads, q_len, k_len, channels};
+  int s = check_dims(d, who);
+  if (s) return s;
+  const bool doDq = grad_query != nullptr, doDk = grad_key != nullptr;
+  if (d.BH() == 0 || d.C == 0 || !(doDq || doDk)) return ok();
+  if (d.N == 0 || !kernel_bwd_ok(dtype, d))
+    return fail(LFAMD_ERR_UNSUPPORTED, "%s: no fused path for dtype %d, N=%lld, M=%lld", who, dtype,
+                (long long)d.N, (long long)d.M);
+  if (!grad_kernel || !kernel || !query || !key) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const BcPlan sp = plan_bcast(d, doDk);
+  if (doDk && (!workspace || workspace_bytes < sp.partialElems * 4))
+    return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, sp.partialElems * 4,
+                workspace_bytes);
+  const KernGrad kg{grad_kernel, kernel, scale};
+  if (doDq && doDk)
+    return launch_bcast_bwd<true, true, kGradKernel>(nullptr, query, key, grad_query, grad_key, workspace, d, sp, st, kg);
+  if (doDq)
+    return launch_bcast_bwd<true, false, kGradKernel>(nullptr, query, key, grad_query, nullptr, workspace, d, sp, st, kg);
+  return launch_bcast_bwd<false, true, kGradKernel>(nullptr, query, key, nullptr, grad_key, workspace, d, sp, st, kg);
 }
 
 int lfamd_laplace_reduce_forward(int dtype, const void* query, const void* key,

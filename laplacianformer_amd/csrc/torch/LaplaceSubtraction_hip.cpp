@@ -107,6 +107,58 @@ void LaplaceSubtraction_backward_cuda(const at::Tensor gradOutput, const at::Ten
   backward_impl(gradOutput, query, key, &gradQuery, &gradKey, "laplace_backward_fused");
 }
 
+namespace {
+void check_kernel_tensor(const at::Tensor& query, const at::Tensor& t, const Sizes& s, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be float32");
+  TORCH_CHECK(t.is_cuda() && t.device() == query.device(), name, " must be on the same GPU as the inputs");
+  TORCH_CHECK(t.sizes() == at::IntArrayRef({s.B, s.H, s.N, s.M}), name, " must have shape [B,H,N,M]");
+  TORCH_CHECK(t.is_contiguous(), name, " has to be contiguous");
+}
+
+// LFAMD_ERR_UNSUPPORTED means "compose the unfused ops"; any other error raises.
+bool fused_status(int status) {
+  if (status == LFAMD_ERR_UNSUPPORTED) return false;
+  detail::check_status(status);
+  return true;
+}
+}  // namespace
+
+bool LaplaceKernel_forward_cuda(const at::Tensor query, const at::Tensor key, at::Tensor output, double scale) {
+  shape_check(query, key);
+  const int dt = detail::abi_dtype(query, "laplace_kernel_forward");
+  detail::same_type(query, key, "key");
+  const Sizes s = sizes_of(query, key);
+  check_kernel_tensor(query, output, s, "output");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  return fused_status(lfamd_laplace_kernel_forward(dt, query.data_ptr(), key.data_ptr(),
+                                                   output.data_ptr<float>(), s.B, s.H, s.N, s.M, s.C,
+                                                   (float)scale, detail::stream_of(query)));
+}
+
+bool LaplaceKernel_backward_cuda(const at::Tensor gradKernel, const at::Tensor kernel, const at::Tensor query,
+                                 const at::Tensor key, std::optional<at::Tensor> gradQuery,
+                                 std::optional<at::Tensor> gradKey, double scale) {
+  shape_check(query, key);
+  const int dt = detail::abi_dtype(query, "laplace_kernel_backward");
+  detail::same_type(query, key, "key");
+  const Sizes s = sizes_of(query, key);
+  check_kernel_tensor(query, kernel, s, "kernel");
+  TORCH_CHECK(gradKernel.scalar_type() == at::kFloat && gradKernel.sizes() == kernel.sizes(),
+              "gradKernel must be float32 of the kernel's shape");
+  const bool dq = gradQuery.has_value() && gradQuery->defined();
+  const bool dk = gradKey.has_value() && gradKey->defined();
+  if (dq) check_out(query, *gradQuery, {s.B, s.H, s.N, s.C}, "gradQuery");
+  if (dk) check_out(query, *gradKey, {s.B, s.H, s.C, s.M}, "gradKey");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(query.device());
+  const at::Tensor gk = gradKernel.contiguous();
+  const size_t ws_bytes = dk ? lfamd_laplace_backward_workspace_size(dt, s.B, s.H, s.N, s.M, s.C) : 0;
+  at::Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, query.options().dtype(at::kByte));
+  return fused_status(lfamd_laplace_kernel_backward(
+      dt, gk.data_ptr<float>(), kernel.data_ptr<float>(), query.data_ptr(), key.data_ptr(),
+      dq ? gradQuery->data_ptr() : nullptr, dk ? gradKey->data_ptr() : nullptr, s.B, s.H, s.N, s.M, s.C,
+      (float)scale, ws.data_ptr(), ws_bytes, detail::stream_of(query)));
+}
+
 void LaplaceSubtraction_reduce_forward_cuda(const at::Tensor query, const at::Tensor key, at::Tensor output) {
   shape_check(query, key);
   const int dt = detail::abi_dtype(query, "subtraction_reduce_laplace_forward_cuda");

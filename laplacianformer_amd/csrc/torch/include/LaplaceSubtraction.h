@@ -8,6 +8,8 @@
 #pragma once
 #include <torch/types.h>
 
+#include <optional>
+
 namespace laplace {
 
 #if defined(WITH_HIP)
@@ -20,6 +22,14 @@ void LaplaceSubtraction_reduce_forward_cuda(const at::Tensor query, const at::Te
 // Superset: grad_query and grad_key in one pass (no reference counterpart).
 void LaplaceSubtraction_backward_cuda(const at::Tensor gradOutput, const at::Tensor query,
                                       const at::Tensor key, at::Tensor gradQuery, at::Tensor gradKey);
+// Superset: the Laplacian kernel exp(-scale * dist) in fp32 with the exp fused
+// into the forward, and its backward with -scale * gradKernel * kernel formed in
+// the backward's staging. Both return false (and write nothing) where the fused
+// path does not cover the sizes or type; the caller then composes the ops above.
+bool LaplaceKernel_forward_cuda(const at::Tensor query, const at::Tensor key, at::Tensor output, double scale);
+bool LaplaceKernel_backward_cuda(const at::Tensor gradKernel, const at::Tensor kernel, const at::Tensor query,
+                                 const at::Tensor key, std::optional<at::Tensor> gradQuery,
+                                 std::optional<at::Tensor> gradKey, double scale);
 #endif
 
 inline void LaplaceSubtraction_forward(const at::Tensor query, const at::Tensor key, at::Tensor output) {
@@ -73,6 +83,30 @@ inline void LaplaceSubtraction_backward(const at::Tensor gradOutput, const at::T
   if (gradOutput.is_cuda() && query.is_cuda() && key.is_cuda()) {
 #if defined(WITH_HIP)
     return LaplaceSubtraction_backward_cuda(gradOutput, query, key, gradQuery, gradKey);
+#else
+    AT_ERROR("Not compiled with GPU support");
+#endif
+  }
+  AT_ERROR("Not implemented on the CPU");
+}
+
+inline bool LaplaceKernel_forward(const at::Tensor query, const at::Tensor key, at::Tensor output, double scale) {
+  if (query.is_cuda() && key.is_cuda()) {
+#if defined(WITH_HIP)
+    return LaplaceKernel_forward_cuda(query, key, output, scale);
+#else
+    AT_ERROR("Not compiled with GPU support");
+#endif
+  }
+  AT_ERROR("Not implemented on the CPU");
+}
+
+inline bool LaplaceKernel_backward(const at::Tensor gradKernel, const at::Tensor kernel, const at::Tensor query,
+                                   const at::Tensor key, std::optional<at::Tensor> gradQuery,
+                                   std::optional<at::Tensor> gradKey, double scale) {
+  if (gradKernel.is_cuda() && query.is_cuda() && key.is_cuda()) {
+#if defined(WITH_HIP)
+    return LaplaceKernel_backward_cuda(gradKernel, kernel, query, key, gradQuery, gradKey, scale);
 #else
     AT_ERROR("Not compiled with GPU support");
 #endif

@@ -1,6 +1,7 @@
 // pybind11 module of the MI355X build. Same module name and the same ten
 // exports as the reference module (src/wrapper.cpp:73-99), plus the fused
-// backward LaplaceSubtraction_backward.
+// backward LaplaceSubtraction_backward and the fused Laplacian-kernel pair
+// LaplaceKernel_forward / LaplaceKernel_backward.
 #include <torch/extension.h>
 
 #include <sstream>
@@ -52,6 +53,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("NewtonInverse_is_supported", &NewtonInverse_is_supported, "NewtonInverse_is_supported (N)");
   m.def("LaplaceSubtraction_backward", &LaplaceSubtraction_backward,
         "LaplaceSubtraction_backward (gradOutput, query, key, gradQuery, gradKey): fused dq+dk");
+  m.def("LaplaceKernel_forward", &LaplaceKernel_forward,
+        "LaplaceKernel_forward (query, key, output, scale): output = exp(-scale * dist) in float32; "
+        "False where the fused path does not apply");
+  m.def("LaplaceKernel_backward", &LaplaceKernel_backward,
+        "LaplaceKernel_backward (gradKernel, kernel, query, key, gradQuery, gradKey, scale): "
+        "gradQuery / gradKey may be None; False where the fused path does not apply");
 }
 
 }  // namespace laplace

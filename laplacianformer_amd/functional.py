@@ -5,7 +5,9 @@ the repository); these Functions pair forward with backward the way a model
 uses them: LaplaceSubtraction forward (reference src/wrapper.cpp:81-82) with
 the fused dq+dk backward (one pass; equal to backward_query + backward_key,
 src/wrapper.cpp:84-88), and NewtonInverse forward with its -V^T G V^T backward
-(src/wrapper.cpp:93-96).
+(src/wrapper.cpp:93-96). LaplaceKernelFunction is the caller-side
+exp(-scale * dist) of the LaplacianFormer layer with the exp fused into the
+HIP kernels where the fused path covers the sizes.
 """
 from __future__ import annotations
 
@@ -44,6 +46,62 @@ class LaplaceSubtractionFunction(torch.autograd.Function):
         return dq, dk
 
 
+def _acc_type(dtype: torch.dtype) -> torch.dtype:
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+class LaplaceKernelFunction(torch.autograd.Function):
+    """K[b,h,i,j] = exp(-scale * sum_c |query[b,h,i,c] - key[b,h,c,j]|), key channel-major.
+
+    K is fp32 (fp64 for fp64 inputs); the distance is never rounded to the input
+    type. Where the fused HIP path applies, the exp runs in the forward's epilogue
+    and the backward forms g = -scale * dK * K while staging its batches; elsewhere
+    both sides compose the plain ops on inputs upcast to the accumulation type,
+    which is the same arithmetic (fp32 accumulation of exact differences).
+    """
+
+    @staticmethod
+    def forward(ctx, query: torch.Tensor, key: torch.Tensor, scale: float) -> torch.Tensor:
+        query = query.contiguous()
+        key = key.contiguous()
+        B, H, N, _ = query.shape
+        M = key.shape[3]
+        scale = float(scale)
+        acc = _acc_type(query.dtype)
+        out = torch.empty((B, H, N, M), dtype=acc, device=query.device)
+        if not (acc == torch.float32 and ext().LaplaceKernel_forward(query, key, out, scale)):
+            dist = torch.empty_like(out)
+            ext().LaplaceSubtraction_forward(query.to(acc), key.to(acc), dist)
+            out = torch.exp(dist * -scale)
+        ctx.scale = scale
+        ctx.save_for_backward(query, key, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad: torch.Tensor):
+        query, key, kern = ctx.saved_tensors
+        need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_q or need_k):
+            return None, None, None
+        grad = grad.contiguous().to(kern.dtype)
+        dq = torch.empty_like(query) if need_q else None
+        dk = torch.empty_like(key) if need_k else None
+        if kern.dtype == torch.float32 and ext().LaplaceKernel_backward(grad, kern, query, key, dq, dk, ctx.scale):
+            return dq, dk, None
+        acc = kern.dtype
+        g = grad * kern * -ctx.scale
+        qa, ka = query.to(acc), key.to(acc)
+        dqa = torch.empty_like(qa) if need_q else None
+        dka = torch.empty_like(ka) if need_k else None
+        if need_q and need_k:
+            ext().LaplaceSubtraction_backward(g, qa, ka, dqa, dka)
+        elif need_q:
+            ext().LaplaceSubtraction_backward_query(g, qa, ka, dqa)
+        else:
+            ext().LaplaceSubtraction_backward_key(g, qa, ka, dka)
+        return (dqa.to(query.dtype) if need_q else None), (dka.to(key.dtype) if need_k else None), None
+
+
 class NewtonInverseFunction(torch.autograd.Function):
     """Newton-Schulz approximate inverse of mat + 0.01 I; backward -V^T G V^T."""
 
@@ -74,6 +132,12 @@ def laplace_subtraction(query: torch.Tensor, key: torch.Tensor, key_layout: str 
     elif key_layout != "cm":
         raise ValueError("key_layout must be 'cm' or 'mc'")
     return LaplaceSubtractionFunction.apply(query, key)
+
+
+def laplace_kernel(query: torch.Tensor, key: torch.Tensor, scale: float) -> torch.Tensor:
+    """exp(-scale * L1(query, key)) with autograd, key channel-major ``[B,H,C,M]``;
+    fp32 result (fp64 for fp64 inputs)."""
+    return LaplaceKernelFunction.apply(query, key, scale)
 
 
 def newton_inverse(mat: torch.Tensor, iters: int) -> torch.Tensor:

@@ -71,5 +71,19 @@ def test_argument_errors_without_device(lib):
     assert lib.lfamd_newton_forward(0, dummy, dummy, 4, 200, 3, null, 0, null) == 1
     assert b"workspace" in lib.lfamd_last_error()
     assert lib.lfamd_newton_backward(0, dummy, dummy, dummy, 4, 200, null, ws - 1, null) == 1
+    # Fused Laplacian-kernel pair: dtype and envelope checks come before any pointer use.
+    assert lib.lfamd_laplace_kernel_forward(7, null, null, null, 1, 1, 4, 4, 8, 0.5, null) == 2
+    assert lib.lfamd_laplace_kernel_forward(3, null, null, null, 1, 1, 4, 4, 8, 0.5, null) == 3  # fp64
+    assert lib.lfamd_laplace_kernel_forward(0, null, null, null, 1, 1, 4, 4, 12, 0.5, null) == 3  # C % 8
+    assert lib.lfamd_laplace_kernel_forward(0, null, null, null, 1, 1, 4, 300, 8, 0.5, null) == 3  # M > 256
+    assert lib.lfamd_laplace_kernel_forward(1, null, null, null, 1, 1, 4, 49, 64, 0.5, null) == 1  # null
+    assert lib.lfamd_laplace_kernel_forward(1, null, null, null, 0, 1, 4, 49, 64, 0.5, null) == 0  # empty
+    kb = lib.lfamd_laplace_kernel_backward
+    assert kb(0, null, null, null, null, dummy, null, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 3  # fp32
+    assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 50, 64, 0.5, null, 0, null) == 3  # M = 50
+    assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 1  # null
+    assert kb(1, null, null, null, null, null, dummy, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 1  # ws
+    assert b"workspace" in lib.lfamd_last_error() or b"null" in lib.lfamd_last_error()
+    assert kb(1, null, null, null, null, null, null, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 0  # nothing asked
     assert lib.lfamd_laplace_backward_workspace_size(1, 32, 1, 3136, 49, 64) > 0
     assert lib.lfamd_laplace_backward_workspace_size(1, 0, 1, 3136, 49, 64) == 0

@@ -27,10 +27,19 @@ class _NewtonRef(torch.autograd.Function):
         return torch.from_numpy(oracle.newton_backward(g.numpy(), V.numpy(), "f64")), None
 
 
-def _ref_attention(q, k, v, grid, pool, iters):
+def _ref_attention(q, k, v, grid, pool, iters, store_dtype=None):
+    """fp64 composition. ``store_dtype``: the landmarks are pooled in fp32 and stored in
+    that type first, as the layer stores them in its input type (fp16 landmarks tie
+    with fp16 queries now and then, and a tie's subgradient is 0 on both sides)."""
     B, H, N, d = q.shape
-    km = torch.nn.functional.avg_pool2d(k.reshape(B * H, *grid, d).permute(0, 3, 1, 2), pool)
-    km = km.permute(0, 2, 3, 1).reshape(B, H, -1, d)
+
+    def pool2(x):
+        x = torch.nn.functional.avg_pool2d(x.reshape(B * H, *grid, d).permute(0, 3, 1, 2), pool)
+        return x.permute(0, 2, 3, 1).reshape(B, H, -1, d)
+
+    km = pool2(k)
+    if store_dtype is not None:  # stored value, fp64 gradient (straight through the rounding)
+        km = km + (pool2(k.detach().float()).to(store_dtype).double() - km).detach()
     s = 1.0 / math.sqrt(d)
     k_qm = torch.exp(-torch.cdist(q, km, p=1) * s)
     k_mm = torch.exp(-torch.cdist(km, km, p=1) * s)
@@ -61,7 +70,7 @@ def _run(gpu, B, H, grid, d, dtype, seed, pool=4, iters=10, slices=None):
         tol = 2 ** -8
     for b in sl:
         qr, kr, vr = (t[b].double().requires_grad_() for t in (q, k, v))
-        ref = _ref_attention(qr, kr, vr, grid, pool, iters)
+        ref = _ref_attention(qr, kr, vr, grid, pool, iters, None if dtype == "f32" else q.dtype)
         ref.backward(g[b].double())
         _norm_close(out[b], ref.detach(), tol, "out")
         _norm_close(qd.grad[b], qr.grad, tol, "dq")

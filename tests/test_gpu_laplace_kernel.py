@@ -1,0 +1,161 @@
+"""Fused Laplacian kernel K = exp(-s * L1(q, key)) and its backward (the attention
+layer's caller-side op, exp fused into the HIP distance kernels), against the
+oracle composition: K = exp(-s * dist) with dist the fp32 serial oracle (which the
+distance kernels match bit for bit), g = -s * gK * K, and dq / dk from the fp64 L1
+oracle for that g."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lfcheck import assert_l1_close, gen
+
+pytestmark = pytest.mark.gpu
+
+# (B, H, N, M, C): fused-forward shapes (C % 8 == 0, M <= 256), incl. one-row and tail cases.
+FWD_SHAPES = [
+    (2, 2, 196, 49, 32),
+    (1, 1, 1, 1, 8),
+    (1, 3, 130, 64, 64),
+    (2, 1, 65, 16, 16),
+    (1, 2, 100, 100, 40),
+    (1, 1, 129, 128, 64),
+    (2, 1, 3136, 49, 64),
+]
+# Fused-backward shapes: fp16, M in {16, 32, 49, 64}; odd N * M and single rows included.
+BWD_SHAPES = [
+    (2, 2, 196, 49, 32),
+    (1, 1, 1, 49, 64),
+    (1, 1, 7, 49, 64),
+    (1, 2, 131, 16, 80),
+    (2, 1, 200, 32, 64),
+    (1, 1, 97, 64, 130),
+    (2, 1, 3136, 49, 64),
+]
+
+
+def _kernel_ref(q, k, dt, s):
+    """fp64 exp(-s * dist32) with dist32 the fp32 serial-order oracle distance."""
+    d32 = oracle.laplace_forward(q, k, "f64" if dt == "f64" else "f32").astype(np.float64)
+    return np.exp(-s * d32), d32
+
+
+def _check_kernel(got, ref, d32, s, what):
+    """|K - exp(-s d)| <= K 2^-21 (1 + s d): fp32 s, the fp32 product s*d and expf, nothing else."""
+    g = got.detach().cpu().double().numpy()
+    assert np.isfinite(g).all(), what
+    lim = ref * (2.0 ** -21) * (1.0 + s * d32) + 1e-38
+    bad = np.abs(g - ref) > lim
+    assert not bad.any(), (what, int(bad.sum()), float((np.abs(g - ref) / np.maximum(ref, 1e-300)).max()))
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", FWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_kernel_forward(gpu, shape, dt):
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = shape
+    print(f"laplace kernel forward {shape} {dt}", flush=True)
+    q = gen((B, H, N, C), 300 + N + M, dt)
+    k = gen((B, H, C, M), 301 + N + M, dt)
+    s = 1.0 / math.sqrt(C)
+    out = torch.empty((B, H, N, M), dtype=torch.float32, device=gpu)
+    assert lf.ext().LaplaceKernel_forward(q.to(gpu), k.to(gpu), out, s) is True
+    ref, d32 = _kernel_ref(q, k, dt, s)
+    _check_kernel(out, ref, d32, s, "K")
+
+
+@pytest.mark.parametrize("shape", BWD_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_kernel_backward_f16(gpu, shape):
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = shape
+    print(f"laplace kernel backward {shape}", flush=True)
+    q = gen((B, H, N, C), 400 + N + M, "f16")
+    k = gen((B, H, C, M), 401 + N + M, "f16")
+    gk = gen((B, H, N, M), 402 + N + M, "f32")
+    s = 1.0 / math.sqrt(C)
+    # K at the scale of the layer's kernels: exp of minus a few units (nonzero everywhere).
+    kern = torch.exp(-torch.rand((B, H, N, M), generator=torch.Generator().manual_seed(N), dtype=torch.float32) * 4)
+    qd, kd, gkd, kernd = q.to(gpu), k.to(gpu), gk.to(gpu), kern.to(gpu)
+    L = lf.ext()
+    dq, dk = torch.empty_like(qd), torch.empty_like(kd)
+    assert L.LaplaceKernel_backward(gkd, kernd, qd, kd, dq, dk, s) is True
+    dq1, dk1 = torch.empty_like(qd), torch.empty_like(kd)
+    assert L.LaplaceKernel_backward(gkd, kernd, qd, kd, dq1, None, s) is True
+    assert L.LaplaceKernel_backward(gkd, kernd, qd, kd, None, dk1, s) is True
+    torch.cuda.synchronize()
+    g64 = -s * gk.double().numpy() * kern.double().numpy()
+    rq = oracle.laplace_backward_query(g64, q, k, "f64")
+    rk = oracle.laplace_backward_key(g64, q, k, "f64")
+    ga = np.abs(g64)
+    assert_l1_close(dq, rq, "f16", "dq", np.broadcast_to(ga.sum(axis=3, keepdims=True), rq.shape))
+    assert_l1_close(dk, rk, "f16", "dk", np.broadcast_to(ga.sum(axis=2, keepdims=True), rk.shape))
+    assert torch.equal(dq.cpu(), dq1.cpu()), "grad_query differs between the fused and query-only calls"
+    assert torch.equal(dk.cpu(), dk1.cpu()), "grad_key differs between the fused and key-only calls"
+
+
+def test_kernel_unsupported_reports_false(gpu):
+    """Outside the fused paths the exports return False and leave the outputs alone."""
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    q = gen((1, 1, 10, 12), 1, "f32").to(gpu)  # C % 8 != 0
+    k = gen((1, 1, 12, 5), 2, "f32").to(gpu)
+    out = torch.full((1, 1, 10, 5), 7.0, device=gpu)
+    assert L.LaplaceKernel_forward(q, k, out, 0.5) is False
+    assert bool((out == 7.0).all())
+    q2 = gen((1, 1, 10, 16), 3, "f32").to(gpu)
+    k2 = gen((1, 1, 16, 49), 4, "f32").to(gpu)
+    kern = torch.rand((1, 1, 10, 49), device=gpu)
+    dq = torch.full_like(q2, 7.0)
+    assert L.LaplaceKernel_backward(kern, kern, q2, k2, dq, None, 0.5) is False  # fp32: no fused backward
+    assert bool((dq == 7.0).all())
+    q3 = gen((1, 1, 10, 16), 5, "f16").to(gpu)
+    k3 = gen((1, 1, 16, 50), 6, "f16").to(gpu)  # M = 50
+    kern3 = torch.rand((1, 1, 10, 50), device=gpu)
+    assert L.LaplaceKernel_backward(kern3, kern3, q3, k3, torch.empty_like(q3), None, 0.5) is False
+    # M = 256: the fp32 output tile of 128 rows plus the key tile exceed one workgroup's LDS.
+    q4 = gen((1, 1, 129, 64), 7, "f16").to(gpu)
+    k4 = gen((1, 1, 64, 256), 8, "f16").to(gpu)
+    assert L.LaplaceKernel_forward(q4, k4, torch.empty((1, 1, 129, 256), device=gpu), 0.5) is False
+    with pytest.raises(RuntimeError):
+        L.LaplaceKernel_forward(q2, k2, torch.empty((1, 1, 10, 49), dtype=torch.float16, device=gpu), 0.5)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_kernel_autograd(gpu, dt):
+    """LaplaceKernelFunction through autograd (fused where it applies, composed
+    elsewhere) against the oracle composition."""
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = 2, 1, 150, 49, 64
+    print(f"laplace kernel autograd {dt}", flush=True)
+    q = gen((B, H, N, C), 500, dt)
+    k = gen((B, H, C, M), 501, dt)
+    gk = gen((B, H, N, M), 502, "f32")
+    s = 1.0 / math.sqrt(C)
+    qd, kd = q.to(gpu).requires_grad_(), k.to(gpu).requires_grad_()
+    K = lf.laplace_kernel(qd, kd, s)
+    assert K.dtype == torch.float32
+    K.backward(gk.to(gpu))
+    ref, d32 = _kernel_ref(q, k, dt, s)
+    _check_kernel(K, ref, d32, s, "K")
+    g64 = -s * gk.double().numpy() * K.detach().cpu().double().numpy()
+    rq = oracle.laplace_backward_query(g64, q, k, "f64")
+    rk = oracle.laplace_backward_key(g64, q, k, "f64")
+    ga = np.abs(g64)
+    assert_l1_close(qd.grad, rq, dt, "dq", np.broadcast_to(ga.sum(axis=3, keepdims=True), rq.shape))
+    assert_l1_close(kd.grad, rk, dt, "dk", np.broadcast_to(ga.sum(axis=2, keepdims=True), rk.shape))
+
+
+def test_kernel_gradcheck_f64(gpu):
+    """fp64 (the composed path): torch.autograd.gradcheck of exp(-s * L1)."""
+    import laplacianformer_amd as lf
+
+    torch.manual_seed(3)
+    q = torch.randn(1, 2, 5, 3, dtype=torch.float64, device=gpu, requires_grad=True)
+    k = torch.randn(1, 2, 3, 4, dtype=torch.float64, device=gpu, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda a, b: lf.laplace_kernel(a, b, 0.7), (q, k), eps=1e-6, atol=1e-7)
