@@ -21,7 +21,6 @@ from __future__ import annotations
 import math
 
 import torch
-import torch.nn.functional as F
 
 from .functional import laplace_kernel, newton_inverse
 
@@ -32,9 +31,10 @@ def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor
     gh, gw = grid
     if gh * gw != N or gh % pool or gw % pool:
         raise ValueError(f"token grid {gh}x{gw} does not match N={N} or pool={pool}")
-    x = k.reshape(B * H, gh, gw, d).permute(0, 3, 1, 2)
-    x = F.avg_pool2d(x, pool)
-    return x.permute(0, 2, 3, 1).reshape(B, H, -1, d).contiguous()
+    # A mean over the two in-window axes of a view: its backward is a broadcast,
+    # cheaper than avg_pool2d's on this channel-last layout.
+    x = k.reshape(B, H, gh // pool, pool, gw // pool, pool, d)
+    return x.mean(dim=(3, 5)).reshape(B, H, -1, d)
 
 
 def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid: tuple[int, int] | None = None,
@@ -57,7 +57,7 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
     k_mm = laplace_kernel(km, km_cm, s)        # [B,H,M,M]
     k_km = laplace_kernel(k, km_cm, s)         # [B,H,N,M] = K_mk^T
     inv = newton_inverse(k_mm, iters)          # [B,H,M,M]
-    kv = torch.matmul(k_km.transpose(-1, -2).contiguous(), v.to(ct))  # [B,H,M,d]
+    kv = torch.matmul(k_km.transpose(-1, -2), v.to(ct))  # [B,H,M,d], transposed fp32 operand
     out = torch.matmul(k_qm, torch.matmul(inv, kv))
     return out.to(in_dtype)
 
