@@ -33,24 +33,53 @@ template <int NP> struct NsLayout {
 
 // acc[t] = X(rows of this wave) * Y(:, tile t), X and Y row-major in LDS.
 // TRANS_X: X is read transposed (X[i][k] := Xs[k][i]); TRANS_Y likewise.
+//
+// The k index is walked in blocks of 16 with k = k0 + 4*lk + s for MFMA step s
+// (lane group lk = lane/16 supplies the MFMA's inner index lk): every k of the
+// block is used once, by the same inner index in A and B. With the row stride
+// LS = NP + 4 this makes every operand read free of LDS bank conflicts: a
+// row-major A operand and a transposed B operand are one 16-byte read per lane
+// for four steps (lanes of one lk group on distinct 16-byte bank groups), a
+// row-major B operand and a transposed A operand one 4-byte read per step on
+// 64 distinct banks (the step-order k = k0 + lk puts 4 lanes on one bank).
 template <int NP, bool TRANS_X, bool TRANS_Y>
 __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, const float* __restrict__ Ys,
                                               int wave, int lane, v4f (&acc)[NP / 16]) {
   using L = NsLayout<NP>;
+  static_assert(L::LS % 64 == 4 || L::LS % 64 == 20 || L::LS % 64 == 36 || L::LS % 64 == 52,
+                "row stride 4 (mod 16) floats");
   const int li = lane & 15, lk = lane >> 4;
+  const int i = 16 * wave + li;
 #pragma unroll
   for (int t = 0; t < L::NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int k0 = 0; k0 < NP; k0 += 4) {
-    const int k = k0 + lk;
-    const int i = 16 * wave + li;
-    const float a = TRANS_X ? Xs[k * L::LS + i] : Xs[i * L::LS + k];
+#pragma unroll 1
+  for (int k0 = 0; k0 < NP; k0 += 16) {
+    const int kb = k0 + 4 * lk;  // this lane's 4 consecutive k
+    float a[4];
+    if constexpr (TRANS_X) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) a[s] = Xs[(kb + s) * L::LS + i];
+    } else {
+      const float4 v = *reinterpret_cast<const float4*>(&Xs[i * L::LS + kb]);
+      a[0] = v.x; a[1] = v.y; a[2] = v.z; a[3] = v.w;
+    }
+    float b[L::NT][4];
 #pragma unroll
     for (int t = 0; t < L::NT; ++t) {
       const int j = 16 * t + li;
-      const float b = TRANS_Y ? Ys[j * L::LS + k] : Ys[k * L::LS + j];
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[t], 0, 0, 0);
+      if constexpr (TRANS_Y) {
+        const float4 v = *reinterpret_cast<const float4*>(&Ys[j * L::LS + kb]);
+        b[t][0] = v.x; b[t][1] = v.y; b[t][2] = v.z; b[t][3] = v.w;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) b[t][s] = Ys[(kb + s) * L::LS + j];
+      }
     }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < L::NT; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
   }
 }
 
