@@ -24,11 +24,17 @@ namespace lfamd {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int NP> struct NsLayout {
-  static constexpr int NT = NP / 16;       // tiles per dimension = waves per workgroup
+// WPR waves per 16-row strip: wave w owns strip w / WPR and the column tiles
+// [(w % WPR) * TW, (w % WPR + 1) * TW). WPR = 2 doubles the waves of a matrix
+// (more latency hiding when there are few matrices per CU).
+template <int NP, int WPR = 1> struct NsLayout {
+  static constexpr int NT = NP / 16;       // tiles per dimension
+  static constexpr int TW = NT / WPR;      // column tiles per wave
+  static constexpr int NW = NT * WPR;      // waves per workgroup
   static constexpr int LS = NP + 4;        // LDS row stride (floats)
   static constexpr int ELEMS = NP * LS;
-  static constexpr int THREADS = NT * 64;
+  static constexpr int THREADS = NW * 64;
+  static_assert(NT % WPR == 0, "whole tiles per wave");
 };
 
 // acc[t] = X(rows of this wave) * Y(:, tile t), X and Y row-major in LDS.
@@ -42,16 +48,17 @@ template <int NP> struct NsLayout {
 // for four steps (lanes of one lk group on distinct 16-byte bank groups), a
 // row-major B operand and a transposed A operand one 4-byte read per step on
 // 64 distinct banks (the step-order k = k0 + lk puts 4 lanes on one bank).
-template <int NP, bool TRANS_X, bool TRANS_Y>
+template <int NP, int WPR, bool TRANS_X, bool TRANS_Y>
 __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, const float* __restrict__ Ys,
-                                              int wave, int lane, v4f (&acc)[NP / 16]) {
-  using L = NsLayout<NP>;
+                                              int wave, int lane, v4f (&acc)[NP / 16 / WPR]) {
+  using L = NsLayout<NP, WPR>;
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
   static_assert(L::LS % 64 == 4 || L::LS % 64 == 20 || L::LS % 64 == 36 || L::LS % 64 == 52,
                 "row stride 4 (mod 16) floats");
   const int li = lane & 15, lk = lane >> 4;
-  const int i = 16 * wave + li;
+  const int i = 16 * strip + li;
 #pragma unroll
-  for (int t = 0; t < L::NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < L::TW; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
   for (int k0 = 0; k0 < NP; k0 += 16) {
     const int kb = k0 + 4 * lk;  // this lane's 4 consecutive k
@@ -63,10 +70,10 @@ __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, cons
       const float4 v = *reinterpret_cast<const float4*>(&Xs[i * L::LS + kb]);
       a[0] = v.x; a[1] = v.y; a[2] = v.z; a[3] = v.w;
     }
-    float b[L::NT][4];
+    float b[L::TW][4];
 #pragma unroll
-    for (int t = 0; t < L::NT; ++t) {
-      const int j = 16 * t + li;
+    for (int t = 0; t < L::TW; ++t) {
+      const int j = 16 * (t0 + t) + li;
       if constexpr (TRANS_Y) {
         const float4 v = *reinterpret_cast<const float4*>(&Ys[j * L::LS + kb]);
         b[t][0] = v.x; b[t][1] = v.y; b[t][2] = v.z; b[t][3] = v.w;
@@ -78,39 +85,43 @@ __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, cons
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int t = 0; t < L::NT; ++t)
+      for (int t = 0; t < L::TW; ++t)
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
   }
 }
 
-// Element (r) of tile t held by this lane: row 16*wave + 4*(lane/16) + r, col 16t + lane%16.
-template <int NP>
-__device__ __forceinline__ void store_strip(float* __restrict__ Ds, int wave, int lane, const v4f (&acc)[NP / 16]) {
-  using L = NsLayout<NP>;
+// Element (r) of this wave's tile t: row 16*strip + 4*(lane/16) + r, col 16*(t0 + t) + lane%16.
+template <int NP, int WPR>
+__device__ __forceinline__ void store_strip(float* __restrict__ Ds, int wave, int lane,
+                                            const v4f (&acc)[NP / 16 / WPR]) {
+  using L = NsLayout<NP, WPR>;
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
 #pragma unroll
-  for (int t = 0; t < L::NT; ++t)
+  for (int t = 0; t < L::TW; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      Ds[(16 * wave + 4 * (lane >> 4) + r) * L::LS + 16 * t + (lane & 15)] = acc[t][r];
+      Ds[(16 * strip + 4 * (lane >> 4) + r) * L::LS + 16 * (t0 + t) + (lane & 15)] = acc[t][r];
 }
 
 // V <- 2V - U on this wave's strip.
-template <int NP>
-__device__ __forceinline__ void update_strip(float* __restrict__ Vs, int wave, int lane, const v4f (&acc)[NP / 16]) {
-  using L = NsLayout<NP>;
+template <int NP, int WPR>
+__device__ __forceinline__ void update_strip(float* __restrict__ Vs, int wave, int lane,
+                                             const v4f (&acc)[NP / 16 / WPR]) {
+  using L = NsLayout<NP, WPR>;
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
 #pragma unroll
-  for (int t = 0; t < L::NT; ++t)
+  for (int t = 0; t < L::TW; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float* p = &Vs[(16 * wave + 4 * (lane >> 4) + r) * L::LS + 16 * t + (lane & 15)];
+      float* p = &Vs[(16 * strip + 4 * (lane >> 4) + r) * L::LS + 16 * (t0 + t) + (lane & 15)];
       *p = 2.0f * (*p) - acc[t][r];
     }
 }
 
 // P = f32(mat) + 0.01 I on the live n x n block; zero padding elsewhere when `pad`.
-template <typename T, int NP>
+template <typename T, int NP, int WPR>
 __device__ __forceinline__ void load_P(float* __restrict__ Ps, const T* __restrict__ M, int n, bool pad) {
-  using L = NsLayout<NP>;
+  using L = NsLayout<NP, WPR>;
   if (pad)
     for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Ps[e] = 0.f;
   if (pad) __syncthreads();
@@ -121,9 +132,9 @@ __device__ __forceinline__ void load_P(float* __restrict__ Ps, const T* __restri
 }
 
 // alpha = 1.8 / (max_i sum_j P_ij)^2; row sums in ascending j, one thread per row.
-template <int NP>
+template <int NP, int WPR>
 __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int n, float* __restrict__ red) {
-  using L = NsLayout<NP>;
+  using L = NsLayout<NP, WPR>;
   const int tid = threadIdx.x;
   float row = -1e30f;
   if (tid < n) {
@@ -135,16 +146,16 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
   if ((tid & 63) == 0) red[tid >> 6] = row;
   __syncthreads();
   float m = red[0];
-  for (int w = 1; w < L::NT; ++w) m = fmaxf(m, red[w]);
+  for (int w = 1; w < L::NW; ++w) m = fmaxf(m, red[w]);
   return 1.8f / (m * m);
 }
 
-template <typename T, int NP, bool THREE_BUF>
-__global__ void __launch_bounds__(NP * 4)
+template <typename T, int NP, bool THREE_BUF, int WPR = 1>
+__global__ void __launch_bounds__(NP * 4 * WPR)
 newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
-  using L = NsLayout<NP>;
+  using L = NsLayout<NP, WPR>;
   extern __shared__ __align__(16) float nsm[];
-  __shared__ float red[8];
+  __shared__ float red[16];
   float* Ps = nsm;                 // P (2-buffer: P, then W = VP)
   float* Vs = nsm + L::ELEMS;      // V
   float* Ts = nsm + 2 * L::ELEMS;  // T = PV (3-buffer only)
@@ -155,30 +166,33 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
 
   if (pad)
     for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = 0.f;
-  load_P<T, NP>(Ps, Mg, n, pad);
+  load_P<T, NP, WPR>(Ps, Mg, n, pad);
   __syncthreads();
-  const float alpha = compute_alpha<NP>(Ps, n, red);
+  const float alpha = compute_alpha<NP, WPR>(Ps, n, red);
   for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = Ps[e] * alpha;
   __syncthreads();
 
-  v4f acc[L::NT];
+  v4f acc[L::TW];
   for (int it = 0; it < iters; ++it) {
     if constexpr (THREE_BUF) {
-      mfma_rowstrip<NP, false, false>(Ps, Vs, wave, lane, acc);  // T = P V
-      store_strip<NP>(Ts, wave, lane, acc);
+      mfma_rowstrip<NP, WPR, false, false>(Ps, Vs, wave, lane, acc);  // T = P V
+      store_strip<NP, WPR>(Ts, wave, lane, acc);
       __syncthreads();
-      mfma_rowstrip<NP, false, false>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
-      update_strip<NP>(Vs, wave, lane, acc);                      // V = 2V - U
+      mfma_rowstrip<NP, WPR, false, false>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
+      // With WPR > 1 the waves of a strip read all of its V rows and each then
+      // updates part of them: every read first.
+      if constexpr (WPR > 1) __syncthreads();
+      update_strip<NP, WPR>(Vs, wave, lane, acc);                      // V = 2V - U
       __syncthreads();
     } else {
-      mfma_rowstrip<NP, false, false>(Vs, Ps, wave, lane, acc);  // W = V P
+      mfma_rowstrip<NP, WPR, false, false>(Vs, Ps, wave, lane, acc);  // W = V P
       __syncthreads();                                            // P reads done
-      store_strip<NP>(Ps, wave, lane, acc);
+      store_strip<NP, WPR>(Ps, wave, lane, acc);
       __syncthreads();
-      mfma_rowstrip<NP, false, false>(Ps, Vs, wave, lane, acc);  // U = W V
+      mfma_rowstrip<NP, WPR, false, false>(Ps, Vs, wave, lane, acc);  // U = W V
       __syncthreads();                                            // V reads done
-      update_strip<NP>(Vs, wave, lane, acc);
-      if (it + 1 < iters) load_P<T, NP>(Ps, Mg, n, false);        // padding of slot P is still zero
+      update_strip<NP, WPR>(Vs, wave, lane, acc);
+      if (it + 1 < iters) load_P<T, NP, WPR>(Ps, Mg, n, false);        // padding of slot P is still zero
       __syncthreads();
     }
   }
@@ -188,10 +202,10 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
   }
 }
 
-template <typename T, int NP>
-__global__ void __launch_bounds__(NP * 4)
+template <typename T, int NP, int WPR = 1>
+__global__ void __launch_bounds__(NP * 4 * WPR)
 newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __restrict__ gmat, int n) {
-  using L = NsLayout<NP>;
+  using L = NsLayout<NP, WPR>;
   extern __shared__ __align__(16) float nsm[];
   float* Vs = nsm;
   float* Gs = nsm + L::ELEMS;  // G, then S = V^T G
@@ -206,17 +220,18 @@ newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __re
     Gs[i * L::LS + j] = to_acc(gout[off + e]);
   }
   __syncthreads();
-  v4f acc[L::NT];
-  mfma_rowstrip<NP, true, false>(Vs, Gs, wave, lane, acc);  // S = V^T G
+  v4f acc[L::TW];
+  mfma_rowstrip<NP, WPR, true, false>(Vs, Gs, wave, lane, acc);  // S = V^T G
   __syncthreads();
-  store_strip<NP>(Gs, wave, lane, acc);
+  store_strip<NP, WPR>(Gs, wave, lane, acc);
   __syncthreads();
-  mfma_rowstrip<NP, false, true>(Gs, Vs, wave, lane, acc);  // R = S V^T
+  mfma_rowstrip<NP, WPR, false, true>(Gs, Vs, wave, lane, acc);  // R = S V^T
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
 #pragma unroll
-  for (int t = 0; t < L::NT; ++t)
+  for (int t = 0; t < L::TW; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 16 * wave + 4 * (lane >> 4) + r, j = 16 * t + (lane & 15);
+      const int i = 16 * strip + 4 * (lane >> 4) + r, j = 16 * (t0 + t) + (lane & 15);
       if (i < n && j < n) gmat[off + (size_t)i * n + j] = from_acc<T>(-acc[t][r]);
     }
 }
@@ -598,32 +613,56 @@ int set_lds(Kern k, size_t bytes) {
   return LFAMD_OK;
 }
 
-template <typename T, int NP>
-int fwd_np(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
+// Waves per 16-row strip: the most (up to 4) that split the strip's tiles evenly
+// within 16 waves per workgroup.
+template <int NP> constexpr int pick_wpr() {
+  constexpr int nt = NP / 16;
+  return (nt % 4 == 0 && nt * 4 <= 16) ? 4 : (nt % 2 == 0 && nt * 2 <= 16) ? 2 : 1;
+}
+
+template <typename T, int NP, int WPR>
+int fwd_np_w(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
   // Mirrors the reference's buffer choice: 3 buffers unless they do not fit.
   const bool three = NP < 128 && fwd_lds<NP>(true) <= (size_t)max_lds_bytes();
   if (three) {
-    auto k = newton_fwd_kernel<T, NP, true>;
+    auto k = newton_fwd_kernel<T, NP, true, WPR>;
     int s = set_lds(k, fwd_lds<NP>(true));
     if (s) return s;
-    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4), fwd_lds<NP>(true), st, m, o, n, iters);
+    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(true), st, m, o, n, iters);
   } else {
-    auto k = newton_fwd_kernel<T, NP, false>;
+    auto k = newton_fwd_kernel<T, NP, false, WPR>;
     int s = set_lds(k, fwd_lds<NP>(false));
     if (s) return s;
-    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4), fwd_lds<NP>(false), st, m, o, n, iters);
+    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(false), st, m, o, n, iters);
   }
   return check_launch("newton forward");
 }
 
-template <typename T, int NP>
-int bwd_np(const T* g, const T* v, T* o, int64_t bh, int n, hipStream_t st) {
-  auto k = newton_bwd_kernel<T, NP>;
+template <typename T, int NP, int WPR>
+int bwd_np_w(const T* g, const T* v, T* o, int64_t bh, int n, hipStream_t st) {
+  auto k = newton_bwd_kernel<T, NP, WPR>;
   const size_t lds = 2 * (size_t)NsLayout<NP>::ELEMS * 4;
   int s = set_lds(k, lds);
   if (s) return s;
-  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4), lds, st, g, v, o, n);
+  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), lds, st, g, v, o, n);
   return check_launch("newton backward");
+}
+
+// Four waves per strip only while there are fewer than two matrices per CU
+// (latency-bound); with more, two per strip keep more matrices resident.
+template <int NP> bool use_wide(int64_t bh) { return pick_wpr<NP>() == 4 && bh < 2 * (int64_t)num_cus(); }
+template <int NP> constexpr int narrow_wpr() { return pick_wpr<NP>() == 4 ? 2 : pick_wpr<NP>(); }
+
+template <typename T, int NP>
+int fwd_np(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
+  if (use_wide<NP>(bh)) return fwd_np_w<T, NP, pick_wpr<NP>()>(m, o, bh, n, iters, st);
+  return fwd_np_w<T, NP, narrow_wpr<NP>()>(m, o, bh, n, iters, st);
+}
+
+template <typename T, int NP>
+int bwd_np(const T* g, const T* v, T* o, int64_t bh, int n, hipStream_t st) {
+  if (use_wide<NP>(bh)) return bwd_np_w<T, NP, pick_wpr<NP>()>(g, v, o, bh, n, st);
+  return bwd_np_w<T, NP, narrow_wpr<NP>()>(g, v, o, bh, n, st);
 }
 
 template <typename T>
