@@ -4,14 +4,14 @@
 // Reference semantics (src/NewtonInverse_cuda_kernel.cu):
 //   P = f32(mat) + 0.01 I                                       (:169, :320)
 //   alpha = 1.8 / (max_i sum_j P_ij)^2, signed row sums          (:82-120)
-//   V0 = alpha P; iters x V <- 2V - V(PV)   [3-buffer, n <= 112] (:181-248)
-//                          V <- 2V - (VP)V  [2-buffer, n = 128]  (:381-457)
+//   V0 = alpha P; iters x V <- 2V - V(PV)   [n <= 112]            (:181-248)
+//                          V <- 2V - (VP)V  [n = 128]             (:381-457)
 //   grad_mat = -(V^T G) V^T                                     (:469-573)
 // Matrices are zero-padded to NP = 16*ceil(n/16) (the reference's N_MAX
 // buckets, :677-688); the padding stays exactly zero through the iteration.
 //
-// Mapping: one workgroup per matrix, NP/16 waves; wave w owns output rows
-// [16w, 16w+16) and all NP/16 column tiles, one v_mfma_f32_16x16x4_f32
+// Mapping: one workgroup per matrix, WPR waves per 16-row strip; a wave owns
+// the strip's rows and NP/16/WPR column tiles, one v_mfma_f32_16x16x4_f32
 // accumulator (4 VGPRs) per 16x16 tile. MFMA 16x16x4 operand layout (wave64):
 //   A[i][k]: lane = i + 16k     B[k][j]: lane = j + 16k
 //   D[i][j]: lane = j + 16*(i/4), register i%4.
@@ -90,6 +90,32 @@ __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, cons
   }
 }
 
+// As mfma_rowstrip with X = P held in registers: pa[b][s] = P[16*strip + lane%16][16b + 4*(lane/16) + s],
+// the row-major A operand of k block b, step s; Y row-major in LDS.
+template <int NP, int WPR>
+__device__ __forceinline__ void mfma_rowstrip_areg(const float (&pa)[NP / 16][4], const float* __restrict__ Ys,
+                                                   int wave, int lane, v4f (&acc)[NP / 16 / WPR]) {
+  using L = NsLayout<NP, WPR>;
+  const int t0 = (wave % WPR) * L::TW;
+  const int li = lane & 15, lk = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < L::TW; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < L::NT; ++kb) {
+    const int k = 16 * kb + 4 * lk;
+    float b[L::TW][4];
+#pragma unroll
+    for (int t = 0; t < L::TW; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[t][s] = Ys[(k + s) * L::LS + 16 * (t0 + t) + li];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < L::TW; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[kb][s], b[t][s], acc[t], 0, 0, 0);
+  }
+}
+
 // Element (r) of this wave's tile t: row 16*strip + 4*(lane/16) + r, col 16*(t0 + t) + lane%16.
 template <int NP, int WPR>
 __device__ __forceinline__ void store_strip(float* __restrict__ Ds, int wave, int lane,
@@ -150,15 +176,18 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
   return 1.8f / (m * m);
 }
 
-template <typename T, int NP, bool THREE_BUF, int WPR = 1>
+// PV_FIRST: V <- 2V - V(PV) (the reference's order for n <= 112), P held in
+// registers as this wave's A operand after the set-up, so the LDS holds V and
+// T = PV only. Otherwise V <- 2V - (VP)V (its order for n = 128): LDS holds V
+// and P, P is overwritten by W = VP and reloaded each iteration.
+template <typename T, int NP, bool PV_FIRST, int WPR = 1>
 __global__ void __launch_bounds__(NP * 4 * WPR)
 newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
   using L = NsLayout<NP, WPR>;
   extern __shared__ __align__(16) float nsm[];
   __shared__ float red[16];
-  float* Ps = nsm;                 // P (2-buffer: P, then W = VP)
+  float* Ps = nsm;                 // P; then T = PV (PV_FIRST) or W = VP
   float* Vs = nsm + L::ELEMS;      // V
-  float* Ts = nsm + 2 * L::ELEMS;  // T = PV (3-buffer only)
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const T* Mg = mat + (size_t)blockIdx.x * n * n;
   T* Og = out + (size_t)blockIdx.x * n * n;
@@ -170,12 +199,22 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
   __syncthreads();
   const float alpha = compute_alpha<NP, WPR>(Ps, n, red);
   for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = Ps[e] * alpha;
-  __syncthreads();
 
   v4f acc[L::TW];
-  for (int it = 0; it < iters; ++it) {
-    if constexpr (THREE_BUF) {
-      mfma_rowstrip<NP, WPR, false, false>(Ps, Vs, wave, lane, acc);  // T = P V
+  if constexpr (PV_FIRST) {
+    float pa[L::NT][4];
+    {
+      const int i = 16 * (wave / WPR) + (lane & 15), kq = 4 * (lane >> 4);
+#pragma unroll
+      for (int kb = 0; kb < L::NT; ++kb) {
+        const float4 v = *reinterpret_cast<const float4*>(&Ps[i * L::LS + 16 * kb + kq]);
+        pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
+      }
+    }
+    __syncthreads();  // P fully read (registers) and V0 written before slot P becomes T
+    float* Ts = Ps;
+    for (int it = 0; it < iters; ++it) {
+      mfma_rowstrip_areg<NP, WPR>(pa, Vs, wave, lane, acc);           // T = P V
       store_strip<NP, WPR>(Ts, wave, lane, acc);
       __syncthreads();
       mfma_rowstrip<NP, WPR, false, false>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
@@ -184,13 +223,16 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
       if constexpr (WPR > 1) __syncthreads();
       update_strip<NP, WPR>(Vs, wave, lane, acc);                      // V = 2V - U
       __syncthreads();
-    } else {
+    }
+  } else {
+    __syncthreads();
+    for (int it = 0; it < iters; ++it) {
       mfma_rowstrip<NP, WPR, false, false>(Vs, Ps, wave, lane, acc);  // W = V P
-      __syncthreads();                                            // P reads done
+      __syncthreads();                                                 // P reads done
       store_strip<NP, WPR>(Ps, wave, lane, acc);
       __syncthreads();
       mfma_rowstrip<NP, WPR, false, false>(Ps, Vs, wave, lane, acc);  // U = W V
-      __syncthreads();                                            // V reads done
+      __syncthreads();                                                 // V reads done
       update_strip<NP, WPR>(Vs, wave, lane, acc);
       if (it + 1 < iters) load_P<T, NP, WPR>(Ps, Mg, n, false);        // padding of slot P is still zero
       __syncthreads();
@@ -602,7 +644,8 @@ int big_bwd(const T* g, const T* inv, T* out, int64_t bh, int n, float* ws, hipS
 
 int bucket(int64_t n) { return (int)((n + 15) / 16) * 16; }
 
-template <int NP> constexpr size_t fwd_lds(bool three) { return (three ? 3 : 2) * (size_t)NsLayout<NP>::ELEMS * 4; }
+// Two NP x (NP+4) fp32 matrices in either order (P, then T or W; and V).
+template <int NP> constexpr size_t fwd_lds() { return 2 * (size_t)NsLayout<NP>::ELEMS * 4; }
 
 template <typename Kern>
 int set_lds(Kern k, size_t bytes) {
@@ -622,18 +665,17 @@ template <int NP> constexpr int pick_wpr() {
 
 template <typename T, int NP, int WPR>
 int fwd_np_w(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
-  // Mirrors the reference's buffer choice: 3 buffers unless they do not fit.
-  const bool three = NP < 128 && fwd_lds<NP>(true) <= (size_t)max_lds_bytes();
-  if (three) {
+  // The reference's association order per bucket: V(PV) below 128, (VP)V at 128.
+  if (NP < 128) {
     auto k = newton_fwd_kernel<T, NP, true, WPR>;
-    int s = set_lds(k, fwd_lds<NP>(true));
+    int s = set_lds(k, fwd_lds<NP>());
     if (s) return s;
-    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(true), st, m, o, n, iters);
+    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(), st, m, o, n, iters);
   } else {
     auto k = newton_fwd_kernel<T, NP, false, WPR>;
-    int s = set_lds(k, fwd_lds<NP>(false));
+    int s = set_lds(k, fwd_lds<NP>());
     if (s) return s;
-    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(false), st, m, o, n, iters);
+    hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(), st, m, o, n, iters);
   }
   return check_launch("newton forward");
 }
