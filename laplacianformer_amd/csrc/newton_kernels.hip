@@ -129,6 +129,19 @@ __device__ __forceinline__ void store_strip(float* __restrict__ Ds, int wave, in
       Ds[(16 * strip + 4 * (lane >> 4) + r) * L::LS + 16 * (t0 + t) + (lane & 15)] = acc[t][r];
 }
 
+// Transposed store: Ds[j][i] = D[i][j] for this wave's tiles. A lane's 4 rows
+// are consecutive in the transposed row: one 16-byte write per tile (16 lanes of
+// a lane group on distinct bank groups, LS = 4 mod 16).
+template <int NP, int WPR>
+__device__ __forceinline__ void store_strip_t(float* __restrict__ Ds, int wave, int lane,
+                                              const v4f (&acc)[NP / 16 / WPR]) {
+  using L = NsLayout<NP, WPR>;
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
+#pragma unroll
+  for (int t = 0; t < L::TW; ++t)
+    *reinterpret_cast<v4f*>(&Ds[(16 * (t0 + t) + (lane & 15)) * L::LS + 16 * strip + 4 * (lane >> 4)]) = acc[t];
+}
+
 // V <- 2V - U on this wave's strip.
 template <int NP, int WPR>
 __device__ __forceinline__ void update_strip(float* __restrict__ Vs, int wave, int lane,
@@ -215,9 +228,9 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
     float* Ts = Ps;
     for (int it = 0; it < iters; ++it) {
       mfma_rowstrip_areg<NP, WPR>(pa, Vs, wave, lane, acc);           // T = P V
-      store_strip<NP, WPR>(Ts, wave, lane, acc);
+      store_strip_t<NP, WPR>(Ts, wave, lane, acc);                     // slot T holds T^T
       __syncthreads();
-      mfma_rowstrip<NP, WPR, false, false>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
+      mfma_rowstrip<NP, WPR, false, true>(Vs, Ts, wave, lane, acc);   // U = V T (own V rows only)
       // With WPR > 1 the waves of a strip read all of its V rows and each then
       // updates part of them: every read first.
       if constexpr (WPR > 1) __syncthreads();
