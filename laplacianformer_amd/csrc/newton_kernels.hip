@@ -263,20 +263,35 @@ newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __re
   using L = NsLayout<NP, WPR>;
   extern __shared__ __align__(16) float nsm[];
   float* Vs = nsm;
-  float* Gs = nsm + L::ELEMS;  // G, then S = V^T G
+  float* Gs = nsm + L::ELEMS;  // G^T, then S = V^T G
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const size_t off = (size_t)blockIdx.x * n * n;
-  if (n < NP)
+  if (n < NP) {
     for (int e = threadIdx.x; e < 2 * L::ELEMS; e += L::THREADS) nsm[e] = 0.f;
-  __syncthreads();
-  for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
-    const int i = e / n, j = e - i * n;
-    Vs[i * L::LS + j] = to_acc(inv[off + e]);
-    Gs[i * L::LS + j] = to_acc(gout[off + e]);
+    __syncthreads();
+    for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
+      const int i = e / n, j = e - i * n;
+      Vs[i * L::LS + j] = to_acc(inv[off + e]);
+      Gs[j * L::LS + i] = to_acc(gout[off + e]);
+    }
+  } else {
+    // Whole 4-element groups of a row (NP is a multiple of 16).
+    for (int e = threadIdx.x; e < NP * NP / 4; e += L::THREADS) {
+      const int i = e / (NP / 4), j = 4 * (e - i * (NP / 4));
+      float v[4], g[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[c] = to_acc(inv[off + (size_t)i * NP + j + c]);
+        g[c] = to_acc(gout[off + (size_t)i * NP + j + c]);
+      }
+      *reinterpret_cast<float4*>(&Vs[i * L::LS + j]) = float4{v[0], v[1], v[2], v[3]};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) Gs[(j + c) * L::LS + i] = g[c];
+    }
   }
   __syncthreads();
   v4f acc[L::TW];
-  mfma_rowstrip<NP, WPR, true, false>(Vs, Gs, wave, lane, acc);  // S = V^T G
+  mfma_rowstrip<NP, WPR, true, true>(Vs, Gs, wave, lane, acc);  // S = V^T G (B read from G^T)
   __syncthreads();
   store_strip<NP, WPR>(Gs, wave, lane, acc);
   __syncthreads();
