@@ -296,6 +296,21 @@ newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __re
   store_strip<NP, WPR>(Gs, wave, lane, acc);
   __syncthreads();
   mfma_rowstrip<NP, WPR, false, true>(Gs, Vs, wave, lane, acc);  // R = S V^T
+  if (n == NP) {
+    // Through LDS (slot V, free once every wave's products are done): whole
+    // rows leave as 4-element groups.
+    __syncthreads();
+    store_strip<NP, WPR>(Vs, wave, lane, acc);
+    __syncthreads();
+    for (int e = threadIdx.x; e < NP * NP / 4; e += L::THREADS) {
+      const int i = e / (NP / 4), j = 4 * (e - i * (NP / 4));
+      const float4 v = *reinterpret_cast<const float4*>(&Vs[i * L::LS + j]);
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) gmat[off + (size_t)i * NP + j + c] = from_acc<T>(-vv[c]);
+    }
+    return;
+  }
   const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
 #pragma unroll
   for (int t = 0; t < L::TW; ++t)
