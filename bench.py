@@ -234,20 +234,23 @@ def cpu_baseline(lap, ns, budget):
     }
 
 
-def _traffic(kernel_prefix):
-    """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary
-    (profiles/hbm_traffic.json, FETCH_SIZE/WRITE_SIZE scaled by a plain-copy calibration)."""
+def _traffic(*kernels):
+    """HBM bytes of one call made of the named kernel launches (exact names as rocprofv3 prints
+    them, without the argument list), from the committed counter summary (profiles/hbm_traffic.json,
+    FETCH_SIZE/WRITE_SIZE scaled by a plain-copy calibration); None if any is missing."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
             data = json.load(f)
     except (OSError, ValueError):
         return None
-    for name, v in data.get("kernels", {}).items():
-        if name.startswith(kernel_prefix):
-            return {"bytes": v["read_bytes"] + v["write_bytes"], "read_bytes": v["read_bytes"],
-                    "write_bytes": v["write_bytes"], "source": data.get("source")}
-    return None
+    table = data.get("kernels", {})
+    if not all(k in table for k in kernels):
+        return None
+    rd = sum(table[k]["read_bytes"] for k in kernels)
+    wr = sum(table[k]["write_bytes"] for k in kernels)
+    return {"bytes": rd + wr, "read_bytes": rd, "write_bytes": wr, "kernels": list(kernels),
+            "source": data.get("source")}
 
 
 def _cpu_model():
@@ -295,7 +298,8 @@ def main():
                                    "launches; fp32 vector peak)",
                          "achieved": bwd_tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                          "frac": bwd_tflops / PEAK_FP32_TFLOPS,
-                         "traffic": _traffic("lfamd::laplace_bwd_bcast_kernel<49, true, true>"),
+                         "traffic": _traffic("lfamd::laplace_bwd_bcast_kernel<49, true, true, 0>",
+                                             "lfamd::laplace_dk_reduce_cm_kernel"),
                          "algorithmic_bytes": 2 * (B_ * N_ * M_ + 2 * B_ * N_ * C_ + 2 * B_ * C_ * M_),
                          "work": f"{L1_FLOPS_BWD} flop per (i,j,d) triple x {T} triples per launch"},
             "kernels": {
