@@ -5,7 +5,9 @@ resident in HBM: LaplaceSubtraction forward + backward (grad_query and grad_key)
 at BASELINE config 2 (B=32 H=1 N=3136 M=49 d=64, fp16 storage, fp32 arithmetic).
 ``value`` is that step's throughput in G(i*j*d)/s (triples per second / 1e9).
 NewtonInverse forward + backward at BASELINE config 3 (1024 x 64x64 fp32,
-12 iterations) is timed the same way and reported under "newton".
+12 iterations) is timed the same way and reported under "newton"; the
+attention layer (config 5) under "layer" and the large-landmark stress case
+(config 4) under "config4".
 
 Per-kernel durations come from HIP events recorded on the stream the kernels
 run on (PyTorch's current stream). The CPU baseline is the C oracle
@@ -36,7 +38,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU timing (approx)")
-    p.add_argument("--only", choices=["laplace", "newton", "layer", "all"], default="all")
+    p.add_argument("--only", choices=["laplace", "newton", "layer", "cfg4", "all"], default="all")
     p.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                    help="after timing, run one plain device copy of MIB MiB (HBM counter calibration)")
     return p.parse_args()
@@ -167,6 +169,46 @@ def bench_layer(args, dev):
             "ms_per_step": wall, "l1_triples": T, "steps": steps}
 
 
+def bench_cfg4(args, dev):
+    """BASELINE config 4 (large-landmark stress): LaplaceSubtraction fwd + fused bwd at B=16 H=8
+    N=4096 M=256 d=64, bf16 storage (q, k ~ N(0, 0.5)); NewtonInverse fwd (16 it) + bwd on 128
+    matrices of 256 x 256 fp32 (the batched-GEMM path with its workspace)."""
+    import torch
+
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    B, H, N, M, C = 16, 8, 4096, 256, 64
+    q = gen((B, H, N, C), 1041, torch.bfloat16, 0.5).to(dev)
+    kT = gen((B, H, C, M), 1042, torch.bfloat16, 0.5).to(dev)
+    g = gen((B, H, N, M), 1043, torch.bfloat16).to(dev)
+    out = torch.empty((B, H, N, M), dtype=torch.bfloat16, device=dev)
+    dq, dk = torch.empty_like(q), torch.empty_like(kT)
+    steps = max(1, args.steps // 20)
+    wall, (t_f, t_b) = time_steps([lambda: L.LaplaceSubtraction_forward(q, kT, out),
+                                   lambda: L.LaplaceSubtraction_backward(g, q, kT, dq, dk)],
+                                  steps, max(1, args.warmup // 20))
+    T = B * H * N * M * C
+    n, nm, iters = 256, B * H, 16
+    kk = gen((nm, n, 64), 1044, torch.float32)
+    A = (torch.exp(-torch.cdist(kk, kk, p=1) / 8.0) + 1e-3 * torch.eye(n)).reshape(B, H, n, n).to(dev).contiguous()
+    G = gen((B, H, n, n), 1045, torch.float32).to(dev)
+    V, dA = torch.empty_like(A), torch.empty_like(A)
+    wall_n, (tn_f, tn_b) = time_steps([lambda: L.NewtonInverse_forward(A, V, iters),
+                                       lambda: L.NewtonInverse_backward(G, V, dA)], steps, max(1, args.warmup // 20))
+    fl_f, fl_b = nm * iters * 4 * n ** 3, nm * 4 * n ** 3
+    return {"workload": "BASELINE config 4: LaplaceSubtraction fwd+bwd B=16 H=8 N=4096 M=256 d=64 bf16; "
+                        "NewtonInverse 128 x 256x256 fp32, 16 it, fwd+bwd",
+            "l1": {"ms_per_step": wall, "value": T / (wall * 1e-3) / 1e9, "unit": "G(i*j*d)/s",
+                   "fwd_ms": t_f, "bwd_ms": t_b,
+                   "fwd_frac_fp32_peak": L1_FLOPS_FWD * T / (t_f * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+                   "bwd_frac_fp32_peak": L1_FLOPS_BWD * T / (t_b * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
+            "newton": {"ms_per_step": wall_n, "fwd_ms": tn_f, "bwd_ms": tn_b,
+                       "tflops": (fl_f + fl_b) / (wall_n * 1e-3) / 1e12,
+                       "frac_fp32_mfma_peak": (fl_f + fl_b) / (wall_n * 1e-3) / 1e12 / PEAK_FP32_TFLOPS},
+            "steps": steps}
+
+
 def cpu_baseline(lap, ns, budget):
     """C oracle (OpenMP) on a slice sample of config 2, scaled to the full workload,
     plus PyTorch CPU cdist fwd+bwd (fp32) and the bmm Newton loop."""
@@ -277,6 +319,7 @@ def main():
     lap = bench_laplace(args, dev) if args.only in ("laplace", "all") else None
     ns = bench_newton(args, dev) if args.only in ("newton", "all") else None
     layer = bench_layer(args, dev) if args.only in ("layer", "all") else None
+    cfg4 = bench_cfg4(args, dev) if args.only in ("cfg4", "all") else None
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
@@ -329,6 +372,8 @@ def main():
                          "config": {"workload": line["newton"]["workload"]}})
     if layer:
         line["layer"] = layer
+    if cfg4:
+        line["config4"] = cfg4
     if args.calib_copy:
         src = torch.empty(args.calib_copy << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
