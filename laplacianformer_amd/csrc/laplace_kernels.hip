@@ -873,6 +873,245 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward for M = CB * 32 columns (CB <= 8), fp16 / bf16 / fp32.
+//
+// A workgroup is RG row groups of CB waves; wave (g, b) of a group takes the
+// 32 columns [32b, 32b + 32) of every row batch (RB rows) of its group, with
+// its columns' key values and grad_key sums in registers, as the fp16 kernel
+// above does for all columns. A row's grad_query is the sum of the CB waves'
+// column-block partials: each wave leaves its partials in LDS (double-buffered
+// by batch parity), and after one workgroup barrier per batch each wave of the
+// group sums RB/CB of the batch's rows in column-block order (deterministic).
+// grad_key: the RG groups' sums in group order, then the workgroup partials
+// summed over the slice by the reduction kernel.
+//
+// Step y = (sgn(q - k) + 1)/2 at the full VALU rate: fp16 operands pre-scaled
+// by 2^24 (d = 0 or |d| >= 1, y = clamp(d/2 + 1/2)); bf16/fp32 by scaling the
+// difference twice by 2^100 (every nonzero fp32 difference is >= 2^-149, so
+// |d| * 2^200 >= 2^51; overflow to +-inf clamps correctly), five instructions
+// per triple instead of four.
+// ---------------------------------------------------------------------------
+constexpr int kMbMC = 32;  // columns per wave
+constexpr int kMbRB = 8;   // rows per batch
+
+template <typename T, int CB, bool DQ, bool DK>
+__global__ void __launch_bounds__(1024)
+laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, const T* __restrict__ key,
+                      T* __restrict__ dq, float* __restrict__ partial, int N, int C, int rowsPerWG) {
+  constexpr int MC = kMbMC, RB = kMbRB, M = CB * MC;
+  constexpr int MP = MC;                       // LDS row pitch of a staged batch (floats)
+  constexpr bool kF16 = std::is_same<T, f16s>::value;
+  constexpr int EPW = 4 / (int)sizeof(T) > 0 ? 4 / (int)sizeof(T) : 1;  // elements per 32-bit word
+  constexpr int GW = RB * MC / EPW;            // grad words of a batch (this wave's columns)
+  constexpr int NL = (GW + 63) / 64;           // words per lane
+  static_assert(GW % 64 == 0, "whole words per lane");
+  const int W = blockDim.x >> 6;
+  const int RG = W / CB;
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int cbk = wave % CB, grp = wave / CB;
+  const int bh = blockIdx.z, chb = blockIdx.y, x = blockIdx.x, nx = gridDim.x;
+  const int slice = bh * gridDim.y + chb;
+  const int c = chb * 64 + lane;
+  const bool cval = c < C;
+  const int cq = min(c, C - 1);
+  const int r0wg = x * rowsPerWG;
+  const int rowsWG = max(0, min(N, r0wg + rowsPerWG) - r0wg);
+  const int nb = (rowsWG + RB - 1) / RB;        // batches of the workgroup
+  const int rounds = (nb + RG - 1) / RG;        // batch t goes to group t % RG
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* big = reinterpret_cast<float*>(smem);  // key tile [M][64] at the start, then the
+                                                // grad_query partials [2][W][RB][64]
+  const int bigFloats = max(M * 64, 2 * W * RB * 64);
+  float* gsm = big + bigFloats + wave * (RB * MP + RB + RB * 64);  // this wave: [RB][MP] 2g,
+  float* gneg = gsm + RB * MP;                                      // [RB] -sum_j g,
+  float* qsm = gneg + RB;                                           // [RB][64] query values
+
+  const T* qb = query + (size_t)bh * N * C;
+  const T* kb = key + (size_t)bh * C * M;
+
+  // Next batch of this group: this wave's 32 columns of RB rows (clamped to the
+  // last valid row; rows past the batch are zeroed at staging) and RB query values.
+  uint32_t gpre[NL];
+  T qpre[RB];
+  int fnr = 0;
+  auto fetch = [&](int t) {
+    const int rb = r0wg + t * RB;
+    const int nr = min(RB, r0wg + rowsWG - rb);
+#pragma unroll
+    for (int s = 0; s < NL; ++s) {
+      const int w = lane + 64 * s;               // word of the batch block
+      const int r = min(w / (MC / EPW), nr - 1), jw = w - (w / (MC / EPW)) * (MC / EPW);
+      const T* src = gout + ((size_t)bh * N + rb + r) * M + cbk * MC + jw * EPW;
+      gpre[s] = *reinterpret_cast<const uint32_t*>(src);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) qpre[r] = qb[(size_t)min(rb + r, rb + nr - 1) * C + cq];
+    fnr = nr;
+  };
+  int t0 = grp;  // this group's first batch
+  if (t0 < nb) fetch(t0);
+
+  // Key tile (global [C][M], coalesced over j), scaled for fp16.
+  for (int t = threadIdx.x; t < 64 * M; t += blockDim.x) {
+    const int cl = t / M, j = t - cl * M;
+    const int cc = chb * 64 + cl;
+    const float v = cc < C ? to_acc(kb[(size_t)cc * M + j]) : 0.0f;
+    big[j * 64 + cl] = kF16 ? v * 16777216.0f : v;
+  }
+  __syncthreads();
+  float kreg[MC], dka[MC];
+#pragma unroll
+  for (int j = 0; j < MC; ++j) {
+    kreg[j] = big[(cbk * MC + j) * 64 + lane];
+    if (DK) dka[j] = 0.0f;
+  }
+  __syncthreads();  // the key tile's LDS becomes the partial buffers
+  float scl = 0x1p100f;
+  asm volatile("" : "+v"(scl));  // VGPR operand: an SGPR one would halve the issue rate
+  float hsum = 0.0f;  // lane j < MC: sum over this wave's rows of 2 g[i][j]
+
+  for (int round = 0; round < rounds; ++round) {
+    const int t = round * RG + grp;
+    const bool have = t < nb;                          // uniform per wave
+    const int nr = have ? fnr : 0;
+    float* dqp = big + ((round & 1) * W + wave) * RB * 64;  // this wave's partials of this batch
+    if (have) {
+      // Stage: 2g as fp32 [RB][MP], rows past nr zero.
+#pragma unroll
+      for (int s = 0; s < NL; ++s) {
+        const int w = lane + 64 * s;
+        const int r = w / (MC / EPW), jw = w - r * (MC / EPW);
+        const bool ok = r < nr;
+        if constexpr (EPW == 2) {
+          const float lo = std::is_same<T, f16s>::value
+                               ? (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[s] & 0xffffu))
+                               : __builtin_bit_cast(float, gpre[s] << 16);
+          const float hi = std::is_same<T, f16s>::value
+                               ? (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[s] >> 16))
+                               : __builtin_bit_cast(float, gpre[s] & 0xffff0000u);
+          gsm[r * MP + 2 * jw] = ok ? 2.0f * lo : 0.0f;
+          gsm[r * MP + 2 * jw + 1] = ok ? 2.0f * hi : 0.0f;
+        } else {
+          gsm[r * MP + jw] = ok ? 2.0f * __builtin_bit_cast(float, gpre[s]) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const float v = to_acc(qpre[r]);
+        qsm[r * 64 + lane] = kF16 ? v * 16777216.0f : v;
+      }
+      wave_sync();
+      if (DQ) {
+        const float4* rowp = reinterpret_cast<const float4*>(gsm + min(lane, RB - 1) * MP);
+        float4 v[MP / 4];
+#pragma unroll
+        for (int jq = 0; jq < MP / 4; ++jq) v[jq] = rowp[jq];
+        float sum = 0.0f;
+#pragma unroll
+        for (int jq = 0; jq < MP / 4; ++jq) sum += (v[jq].x + v[jq].y) + (v[jq].z + v[jq].w);
+        if (lane < RB) gneg[lane] = -0.5f * sum;
+      }
+      if (DK) {
+        float hv[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) hv[r] = gsm[r * MP + min(lane, MC - 1)];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) hsum += hv[r];
+      }
+      wave_sync();
+      if (t + RG < nb) fetch(t + RG);
+
+      // Row loop as in the fp16 kernel: grad values two 16-byte groups ahead,
+      // four partial sums per row, grad_key sums updated in place.
+      constexpr int NQ = MP / 4;
+      float qn = qsm[lane];
+      float accn = DQ ? gneg[0] : 0.0f;
+      float4 gq[2] = {reinterpret_cast<const float4*>(gsm)[0], reinterpret_cast<const float4*>(gsm)[1]};
+#pragma unroll 1
+      for (int r = 0; r < nr; ++r) {
+        const float4* g4 = reinterpret_cast<const float4*>(gsm + r * MP);
+        const float4* g4n = reinterpret_cast<const float4*>(gsm + min(r + 1, RB - 1) * MP);
+        const float qv = qn;
+        float acc[4] = {accn, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int jq = 0; jq < NQ; ++jq) {
+          const float4 gv = gq[jq & 1];
+          if (jq + 2 < NQ) gq[jq & 1] = g4[jq + 2];
+          else gq[jq & 1] = g4n[jq + 2 - NQ];
+          if (jq == NQ - 1) {
+            qn = qsm[min(r + 1, RB - 1) * 64 + lane];
+            if (DQ) accn = gneg[min(r + 1, RB - 1)];
+          }
+          const float gg[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int j = jq * 4 + u;
+            float y;
+            if constexpr (kF16) {
+              y = half_step(qv - kreg[j]);
+            } else {
+              const float e = (qv - kreg[j]) * scl;
+              y = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, scl, 0.5f), 0.0f, 1.0f);
+            }
+            if (DQ) acc[u] = fmaf(gg[u], y, acc[u]);
+            if (DK) {
+              dka[j] = fmaf(gg[u], y, dka[j]);
+              asm volatile("" : "+v"(dka[j]));  // update in place, not after the row
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (DQ) {
+          float total = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+          asm volatile("" : "+v"(total));
+          dqp[r * 64 + lane] = total;
+        }
+      }
+    }
+    if (DQ) {
+      // Every wave of the workgroup has written this batch's partials (and is
+      // done reading the partials of two batches ago, in the other buffer).
+      __syncthreads();
+      if (have) {
+        const int rb = r0wg + t * RB;
+        const float* gp = big + ((round & 1) * W + grp * CB) * RB * 64;  // the group's CB waves
+        for (int r = cbk; r < nr; r += CB) {
+          float sv = 0.0f;
+#pragma unroll
+          for (int b = 0; b < CB; ++b) sv += gp[(b * RB + r) * 64 + lane];
+          if (cval) dq[((size_t)bh * N + rb + r) * C + c] = from_acc<T>(sv);
+        }
+      }
+    }
+    if (have) wave_sync();
+  }
+
+  if (DK) {
+    // This wave's grad_key partial for its 32 columns, then the RG groups' sums in
+    // group order into red[M][64], written out as the workgroup's partial.
+    if (lane < MC) gsm[lane] = 0.5f * hsum;
+    wave_sync();
+#pragma unroll
+    for (int j = 0; j < MC; ++j) dka[j] = gsm[j] - dka[j];
+    __syncthreads();  // every wave is done with the partial buffers
+    float* red = big;
+    for (int g = 0; g < RG; ++g) {
+      if (grp == g) {
+#pragma unroll
+        for (int j = 0; j < MC; ++j) {
+          float* p = &red[(cbk * MC + j) * 64 + lane];
+          *p = g == 0 ? dka[j] : *p + dka[j];
+        }
+      }
+      __syncthreads();
+    }
+    float* out = partial + ((size_t)slice * nx + x) * 64 * M;
+    for (int tt = threadIdx.x; tt < 64 * M; tt += blockDim.x) out[tt] = red[tt];
+  }
+}
+
 // grad_key = sum over the workgroups of a slice of their partial sums, in
 // workgroup order (deterministic). One thread per (channel, column).
 template <typename T>
@@ -895,8 +1134,9 @@ laplace_dk_reduce_kernel(const typename AccOf<T>::type* __restrict__ partial, T*
 }
 
 // Same sum over column-major partials ([M][64] per workgroup, channel fastest).
+template <typename T = f16s>
 __global__ void __launch_bounds__(256)
-laplace_dk_reduce_cm_kernel(const float* __restrict__ partial, f16s* __restrict__ dk, int nx, int M, int C) {
+laplace_dk_reduce_cm_kernel(const float* __restrict__ partial, T* __restrict__ dk, int nx, int M, int C) {
   const int bh = blockIdx.z, cb = blockIdx.y;
   const int slice = bh * gridDim.y + cb;
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -908,7 +1148,7 @@ laplace_dk_reduce_cm_kernel(const float* __restrict__ partial, f16s* __restrict_
   float s = 0.0f;
 #pragma unroll 8
   for (int x = 0; x < nx; ++x) s += pb[(size_t)x * 64 * M];
-  dk[((size_t)bh * C + cc) * M + j] = from_acc<f16s>(s);
+  dk[((size_t)bh * C + cc) * M + j] = from_acc<T>(s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1180,9 +1420,10 @@ struct BcPlan {
   size_t lds, partialElems;
 };
 
+// (M = 64 runs faster on the column-block kernel below: 57 vs 62 us at B=32 N=3136.)
 bool bcast_bwd_ok(int dtype, const Dims& d, const void* g) {
   if (dtype != LFAMD_F16) return false;
-  if (!(d.M == 16 || d.M == 32 || d.M == 49 || d.M == 64)) return false;
+  if (!(d.M == 16 || d.M == 32 || d.M == 49)) return false;
   if ((d.N * d.M) % 2 != 0) return false;
   return (reinterpret_cast<uintptr_t>(g) & 3) == 0;
 }
@@ -1225,7 +1466,7 @@ int launch_bcast_bwd_mc(const void* g, const void* q, const void* k, void* dq, v
   int s = check_launch("laplace backward");
   if (s || !DK) return s;
   dim3 rgrid(ceil_div(64 * MC, 256), p.ncb, (unsigned)d.BH());
-  hipLaunchKernelGGL(laplace_dk_reduce_cm_kernel, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
+  hipLaunchKernelGGL(laplace_dk_reduce_cm_kernel<f16s>, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
                      static_cast<f16s*>(dk), p.nx, MC, (int)d.C);
   return check_launch("laplace backward_key reduction");
 }
@@ -1238,6 +1479,82 @@ int launch_bcast_bwd(const void* g, const void* q, const void* k, void* dq, void
     case 32: return launch_bcast_bwd_mc<32, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
     case 49: return launch_bcast_bwd_mc<49, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
     default: return launch_bcast_bwd_mc<64, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+  }
+}
+
+// ---- backward for M = 32 * CB (fp16 / bf16 / fp32) ----
+struct MbPlan {
+  int CB, RG, W, nx, ncb, rowsPerWG;
+  size_t lds, partialElems;
+};
+
+bool mb_bwd_ok(int dtype, const Dims& d, const void* g) {
+  if (!(dtype == LFAMD_F16 || dtype == LFAMD_BF16 || dtype == LFAMD_F32)) return false;
+  if (d.M % kMbMC != 0 || d.M < kMbMC || d.M > 8 * kMbMC) return false;
+  return (reinterpret_cast<uintptr_t>(g) & 3) == 0;
+}
+
+MbPlan plan_mb(const Dims& d, bool dkey) {
+  MbPlan p{};
+  p.ncb = ceil_div((int)d.C, 64);
+  p.CB = (int)d.M / kMbMC;
+  p.RG = std::max(1, 16 / p.CB);
+  p.W = p.CB * p.RG;
+  const int64_t slices = d.BH() * p.ncb;
+  const int N = (int)std::max<int64_t>(d.N, 1);
+  // One workgroup per CU when the slices allow it, each with at least one batch per row group.
+  int nx = (int)std::max<int64_t>(1, ceil_div(num_cus(), (int)std::min<int64_t>(slices, num_cus())));
+  nx = std::min(nx, std::max(1, N / (kMbRB * p.RG)));
+  p.rowsPerWG = round_up(ceil_div(N, nx), kMbRB);
+  p.nx = ceil_div(N, p.rowsPerWG);
+  const size_t bigFloats = std::max<size_t>((size_t)d.M * 64, (size_t)2 * p.W * kMbRB * 64);
+  p.lds = (bigFloats + (size_t)p.W * (kMbRB * kMbMC + kMbRB + kMbRB * 64)) * 4;
+  p.partialElems = dkey ? (size_t)slices * p.nx * 64 * (size_t)d.M : 0;
+  return p;
+}
+
+template <typename T, int CB, bool DQ, bool DK>
+int launch_mb_cb(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
+                 const MbPlan& p, hipStream_t st) {
+  auto kern = laplace_bwd_mb_kernel<T, CB, DQ, DK>;
+  if (p.lds > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)p.lds) != hipSuccess)
+    return fail(LFAMD_ERR_HIP, "laplace backward: hipFuncSetAttribute failed");
+  dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
+  hipLaunchKernelGGL(kern, grid, dim3(64 * p.W), p.lds, st, static_cast<const T*>(g), static_cast<const T*>(q),
+                     static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)d.N, (int)d.C,
+                     p.rowsPerWG);
+  int s = check_launch("laplace backward");
+  if (s || !DK) return s;
+  dim3 rgrid(ceil_div(64 * (int)d.M, 256), p.ncb, (unsigned)d.BH());
+  hipLaunchKernelGGL(laplace_dk_reduce_cm_kernel<T>, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
+                     static_cast<T*>(dk), p.nx, (int)d.M, (int)d.C);
+  return check_launch("laplace backward_key reduction");
+}
+
+template <typename T, bool DQ, bool DK>
+int launch_mb_t(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
+                const MbPlan& p, hipStream_t st) {
+  switch (p.CB) {
+    case 1: return launch_mb_cb<T, 1, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 2: return launch_mb_cb<T, 2, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 3: return launch_mb_cb<T, 3, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 4: return launch_mb_cb<T, 4, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 5: return launch_mb_cb<T, 5, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 6: return launch_mb_cb<T, 6, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 7: return launch_mb_cb<T, 7, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    default: return launch_mb_cb<T, 8, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+  }
+}
+
+template <bool DQ, bool DK>
+int launch_mb(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws,
+              const Dims& d, const MbPlan& p, hipStream_t st) {
+  switch (dtype) {
+    case LFAMD_F16: return launch_mb_t<f16s, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case LFAMD_BF16: return launch_mb_t<bf16s, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    default: return launch_mb_t<float, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
   }
 }
 
@@ -1329,6 +1646,14 @@ int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq,
     if (doDq) return launch_bcast_bwd<true, false>(g, q, k, dq, dk, ws, d, sp, st);
     return launch_bcast_bwd<false, true>(g, q, k, dq, dk, ws, d, sp, st);
   }
+  if (mb_bwd_ok(dtype, d, g)) {
+    const MbPlan mp = plan_mb(d, doDk);
+    if (doDk && (!ws || wsBytes < mp.partialElems * 4))
+      return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, mp.partialElems * 4, wsBytes);
+    if (doDq && doDk) return launch_mb<true, true>(dtype, g, q, k, dq, dk, ws, d, mp, st);
+    if (doDq) return launch_mb<true, false>(dtype, g, q, k, dq, dk, ws, d, mp, st);
+    return launch_mb<false, true>(dtype, g, q, k, dq, dk, ws, d, mp, st);
+  }
   const BwdPlan p = plan_bwd(d, doDq, doDk, acc, dtype == LFAMD_F16 ? 2 : acc);
   if (doDk) {
     const size_t need = p.partialElems * acc;
@@ -1391,6 +1716,8 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
   // Either backward path may run (the fp16 SGPR path also depends on pointer alignment).
   size_t bytes = plan_bwd(d, true, true, acc, dtype == LFAMD_F16 ? 2 : acc).partialElems * acc;
   if (dtype == LFAMD_F16) bytes = std::max(bytes, plan_bcast(d, true).partialElems * 4);
+  if (dtype != LFAMD_F64 && d.M % kMbMC == 0 && d.M <= 8 * kMbMC)
+    bytes = std::max(bytes, plan_mb(d, true).partialElems * 4);
   return bytes;
 }
 
