@@ -16,6 +16,9 @@
 //   A[i][k]: lane = i + 16k     B[k][j]: lane = j + 16k
 //   D[i][j]: lane = j + 16*(i/4), register i%4.
 #include <algorithm>
+#include <cstdint>
+#include <initializer_list>
+#include <type_traits>
 
 #include "lf_common.h"
 #include "lf_internal.h"
@@ -449,39 +452,53 @@ newton_bwd_f64_kernel(const double* __restrict__ gout, const double* __restrict_
 constexpr int kBgTile = 64;  // output tile per workgroup (4 waves, 32 x 32 each)
 constexpr int kBgK = 16;     // k per LDS stage
 
-// P = f32(mat) + 0.01 I and V0 = alpha P, padded to NP x NP with zeros; alpha
-// from the signed row sums in ascending j (one thread per row, as the
-// LDS-resident kernel does). One workgroup of NP threads per matrix.
+constexpr int kBgMaxNP = 256;  // largest padded size of the GEMM path
+constexpr int kInitRows = 16;  // rows per workgroup of the init kernel
+
+// P = f32(mat) + 0.01 I, zero-padded to NP x NP, and the signed row sums of P
+// in ascending j (one thread per row, as the LDS-resident kernel forms them)
+// into rowsum[m][i]; padding rows get -FLT_MAX so that they never give the max.
+// alpha = 1.8 / max_i(rowsum)^2 is formed by the kernels that apply it (V0 = alpha P
+// never goes to memory). Grid (NP/16 row blocks, matrices), 256 threads: the 16
+// rows pass through LDS, so both the matrix reads and the P writes are coalesced.
 template <typename T>
 __global__ void __launch_bounds__(256)
-newton_big_init_kernel(const T* __restrict__ mat, float* __restrict__ P, float* __restrict__ V, int n, int NP) {
-  __shared__ float red[4];
-  const int i = threadIdx.x;
-  const T* M = mat + (size_t)blockIdx.x * n * n;
-  float* Pm = P + (size_t)blockIdx.x * NP * NP;
-  float* Vm = V + (size_t)blockIdx.x * NP * NP;
-  float rowsum = -3.4e38f;
-  if (i < n) {
-    float sum = 0.0f;
-    for (int j = 0; j < n; ++j) {
-      const float p = to_acc(M[(size_t)i * n + j]) + (i == j ? 0.01f : 0.0f);
-      Pm[(size_t)i * NP + j] = p;
-      sum += p;
-    }
-    rowsum = sum;
+newton_big_init_kernel(const T* __restrict__ mat, float* __restrict__ P, float* __restrict__ rowsum, int n, int NP) {
+  __shared__ float rows[kInitRows][kBgMaxNP + 1];
+  const int r0 = blockIdx.x * kInitRows;
+  const size_t m = blockIdx.y;
+  const T* M = mat + m * n * n;
+  float* Pm = P + m * NP * NP;
+  for (int e = threadIdx.x; e < kInitRows * NP; e += blockDim.x) {
+    const int r = e / NP, j = e - r * NP, i = r0 + r;
+    float p = 0.0f;
+    if (i < n && j < n) p = to_acc(M[(size_t)i * n + j]) + (i == j ? 0.01f : 0.0f);
+    Pm[(size_t)i * NP + j] = p;
+    rows[r][j] = p;
   }
-  if (i < NP) {
-    for (int j = (i < n ? n : 0); j < NP; ++j) Pm[(size_t)i * NP + j] = 0.0f;
-  }
-  for (int off = 32; off > 0; off >>= 1) rowsum = fmaxf(rowsum, __shfl_xor(rowsum, off));
-  if ((i & 63) == 0) red[i >> 6] = rowsum;
   __syncthreads();
-  float m = red[0];
-  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = fmaxf(m, red[w]);
-  const float alpha = 1.8f / (m * m);
-  // Each thread scales the row it wrote itself (program order, no barrier needed).
-  if (i < NP)
-    for (int j = 0; j < NP; ++j) Vm[(size_t)i * NP + j] = alpha * Pm[(size_t)i * NP + j];
+  if (threadIdx.x < kInitRows) {
+    const int i = r0 + threadIdx.x;
+    float sum = -3.4e38f;
+    if (i < n) {
+      sum = 0.0f;
+      for (int j = 0; j < n; ++j) sum += rows[threadIdx.x][j];
+    }
+    rowsum[m * NP + i] = sum;
+  }
+}
+
+// alpha = 1.8 / (max of the NP row sums)^2, computed by every thread of a
+// 256-thread workgroup (contains one barrier).
+__device__ float big_alpha(const float* __restrict__ rs, int NP) {
+  __shared__ float red[4];
+  float v = -3.4e38f;
+  for (int i = threadIdx.x; i < NP; i += 256) v = fmaxf(v, rs[i]);
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  return 1.8f / (mx * mx);
 }
 
 // f32 copy of an n x n matrix, zero-padded to NP x NP.
@@ -495,29 +512,40 @@ newton_big_pack_kernel(const T* __restrict__ src, float* __restrict__ dst, int n
   dst[m * NP * NP + e] = (i < n && j < n) ? to_acc(src[m * n * n + (size_t)i * n + j]) : 0.0f;
 }
 
-// dst[i][j] = src[i][j] (i, j < n), rounded once to T; SIGN = -1 negates.
-template <typename T, int SIGN>
+// dst[i][j] = src[i][j] (i, j < n), rounded once to T; SIGN = -1 negates;
+// SCALED multiplies by alpha from the row sums (dst = V0 = alpha P).
+template <typename T, int SIGN, bool SCALED>
 __global__ void __launch_bounds__(256)
-newton_big_unpack_kernel(const float* __restrict__ src, T* __restrict__ dst, int n, int NP) {
+newton_big_unpack_kernel(const float* __restrict__ src, T* __restrict__ dst, const float* __restrict__ rowsum,
+                         int n, int NP) {
   const size_t m = blockIdx.y;
+  float scale = (float)SIGN;
+  if constexpr (SCALED) scale = big_alpha(rowsum + m * NP, NP);
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= n * n) return;
   const int i = e / n, j = e - i * n;
-  dst[m * n * n + e] = from_acc<T>(SIGN * src[m * NP * NP + (size_t)i * NP + j]);
+  dst[m * n * n + e] = from_acc<T>(scale * src[m * NP * NP + (size_t)i * NP + j]);
 }
 
-// Batched D = op(X) op(Y) over NP x NP fp32 matrices (row-major, matrix stride
-// NP*NP), op = transpose when TX / TY. MODE 0: D = XY; 1: D = 2E - XY. Grid: (NP/64)^2 tiles x matrices, flattened so that all tiles of a
-// matrix share blockIdx.x mod 8 (workgroups are dealt to the 8 XCDs round
-// robin, so a matrix's tiles share one L2). Both operands are staged k-major in
-// LDS ([k][64]): the MFMA operand reads (16 consecutive rows or columns per k)
-// are then conflict-free. Two LDS stages, one barrier per stage.
-template <bool TX, bool TY, int MODE>
+// Batched D = f(op(X) op(Y)) over NP x NP fp32 matrices (row-major, matrix
+// stride NP*NP), op = transpose when TX / TY. MODE 0: D = XY; 1: D = 2E - XY;
+// 2: D = -XY. SCALED multiplies the result by the matrix's alpha (from the
+// init kernel's row sums). Grid: (NP/64)^2 tiles x matrices, flattened so that
+// all tiles of a matrix share blockIdx.x mod 8 (workgroups are dealt to the 8
+// XCDs round robin, so a matrix's tiles share one L2). Both operands are staged
+// k-major in LDS ([k][64]) with the columns of row k XOR-swizzled by
+// 16 * ((k + k/4) mod 4): the 4 k rows of an MFMA operand read then fall on 4
+// different 16-bank groups, and so do the 4 rows of a transposing store
+// (conflict-free both ways, no padding). Two LDS stages, one
+// barrier per stage; global loads run two stages ahead of the MFMAs through
+// two register sets, so each load has two stages of MFMA work to land in.
+template <bool TX, bool TY, int MODE, bool SCALED>
 __global__ void __launch_bounds__(256)
 newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ E,
-                       float* __restrict__ D, int NP, int nMat) {
+                       const float* __restrict__ rowsum, float* __restrict__ D, int NP, int nMat) {
   __shared__ __align__(16) float As[2][kBgK][kBgTile];
   __shared__ __align__(16) float Bs[2][kBgK][kBgTile];
+  auto sw = [](int k) { return 16 * ((k + (k >> 2)) & 3); };
   const int nt = NP / kBgTile;
   const int tiles = nt * nt;
   // Inverse of the flattening: id = (m % 8) + 8 * (t + tiles * (m / 8)).
@@ -532,10 +560,11 @@ newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y,
   const float* Ym = Y + mo;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+  float alpha = 1.0f;
+  if constexpr (SCALED) alpha = big_alpha(rowsum + (size_t)m * NP, NP);
 
   // Global -> register staging of one k stage: 64 x 16 of op(X) and 16 x 64 of op(Y), one float4 each.
-  float4 ra, rb;
-  auto load = [&](int k0) {
+  auto load = [&](float4& ra, float4& rb, int k0) {
     if (TX) {  // A[i][k] = X[k][i]: 16 rows of X, 64 contiguous columns
       const int k = tid >> 4, iq = (tid & 15) * 4;
       ra = *reinterpret_cast<const float4*>(Xm + (size_t)(k0 + k) * NP + ti * kBgTile + iq);
@@ -551,20 +580,22 @@ newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y,
       rb = *reinterpret_cast<const float4*>(Ym + (size_t)(k0 + k) * NP + tj * kBgTile + jq);
     }
   };
-  auto store = [&](int b) {
+  auto store = [&](const float4& ra, const float4& rb, int b) {
     if (TX) {
       const int k = tid >> 4, iq = (tid & 15) * 4;
-      *reinterpret_cast<float4*>(&As[b][k][iq]) = ra;
+      *reinterpret_cast<float4*>(&As[b][k][iq ^ sw(k)]) = ra;
     } else {
       const int i = tid >> 2, kq = (tid & 3) * 4;
-      As[b][kq + 0][i] = ra.x; As[b][kq + 1][i] = ra.y; As[b][kq + 2][i] = ra.z; As[b][kq + 3][i] = ra.w;
+      As[b][kq + 0][i ^ sw(kq + 0)] = ra.x; As[b][kq + 1][i ^ sw(kq + 1)] = ra.y;
+      As[b][kq + 2][i ^ sw(kq + 2)] = ra.z; As[b][kq + 3][i ^ sw(kq + 3)] = ra.w;
     }
     if (TY) {
       const int j = tid >> 2, kq = (tid & 3) * 4;
-      Bs[b][kq + 0][j] = rb.x; Bs[b][kq + 1][j] = rb.y; Bs[b][kq + 2][j] = rb.z; Bs[b][kq + 3][j] = rb.w;
+      Bs[b][kq + 0][j ^ sw(kq + 0)] = rb.x; Bs[b][kq + 1][j ^ sw(kq + 1)] = rb.y;
+      Bs[b][kq + 2][j ^ sw(kq + 2)] = rb.z; Bs[b][kq + 3][j ^ sw(kq + 3)] = rb.w;
     } else {
       const int k = tid >> 4, jq = (tid & 15) * 4;
-      *reinterpret_cast<float4*>(&Bs[b][k][jq]) = rb;
+      *reinterpret_cast<float4*>(&Bs[b][k][jq ^ sw(k)]) = rb;
     }
   };
 
@@ -573,27 +604,38 @@ newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y,
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int c = 0; c < 2; ++c) acc[r][c] = v4f{0.f, 0.f, 0.f, 0.f};
-  const int nk = NP / kBgK;
-  load(0);
-  store(0);
-  __syncthreads();
   const int li = lane & 15, lk = lane >> 4;
-  for (int kc = 0; kc < nk; ++kc) {
-    const int b = kc & 1;
-    if (kc + 1 < nk) load((kc + 1) * kBgK);
+  auto compute = [&](int b) {
 #pragma unroll
     for (int ks = 0; ks < kBgK; ks += 4) {
       float a[2], bb[2];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) a[r] = As[b][ks + lk][wr + 16 * r + li];
+      for (int r = 0; r < 2; ++r) a[r] = As[b][ks + lk][(wr + 16 * r + li) ^ sw(ks + lk)];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) bb[c] = Bs[b][ks + lk][wc + 16 * c + li];
+      for (int c = 0; c < 2; ++c) bb[c] = Bs[b][ks + lk][(wc + 16 * c + li) ^ sw(ks + lk)];
 #pragma unroll
       for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int c = 0; c < 2; ++c) acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], bb[c], acc[r][c], 0, 0, 0);
     }
-    if (kc + 1 < nk) store(b ^ 1);
+  };
+
+  // nk = NP / 16 is a multiple of 4: stages go in pairs, even stages through
+  // LDS buffer 0 and register set 0, odd ones through buffer 1 and set 1.
+  const int nk = NP / kBgK;
+  float4 ra0, rb0, ra1, rb1;
+  load(ra0, rb0, 0);
+  load(ra1, rb1, kBgK);
+  store(ra0, rb0, 0);
+  __syncthreads();
+  for (int kc = 0; kc < nk; kc += 2) {
+    if (kc + 2 < nk) load(ra0, rb0, (kc + 2) * kBgK);
+    compute(0);
+    store(ra1, rb1, 1);
+    __syncthreads();
+    if (kc + 3 < nk) load(ra1, rb1, (kc + 3) * kBgK);
+    compute(1);
+    if (kc + 2 < nk) store(ra0, rb0, 0);
     __syncthreads();
   }
 
@@ -610,6 +652,8 @@ newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y,
         const size_t o = (size_t)i * NP + j;
         float v = acc[r][c][q];
         if (MODE == 1) v = 2.0f * Em[o] - v;
+        if (MODE == 2) v = -v;
+        if (SCALED) v = alpha * v;
         Dm[o] = v;
       }
 }
@@ -626,16 +670,34 @@ constexpr int kF64MaxN = 96;   // two fp64 96x97 buffers fill most of gfx950's 1
 int big_np(int64_t n) { return (int)((n + kBgTile - 1) / kBgTile) * kBgTile; }
 
 // fp32 NP x NP buffers per matrix the GEMM path uses: P, V, V', T (forward),
-// V, G, S (backward).
+// V, G, S (backward); then NP row sums per matrix (forward).
 constexpr int kBigBuffers = 4;
 size_t big_workspace_bytes(int64_t bh, int64_t n) {
   const size_t np = (size_t)big_np(n);
-  return (size_t)bh * kBigBuffers * np * np * 4;
+  return (size_t)bh * (kBigBuffers * np * np + np) * 4;
 }
 
 unsigned big_gemm_blocks(int np, int64_t bh) {
   const int tiles = (np / kBgTile) * (np / kBgTile);
   return (unsigned)(8 * tiles * ((bh + 7) / 8));  // matrices rounded up to a multiple of 8
+}
+
+// fp32 matrices with n == NP (and 16-byte aligned) already have the padded
+// layout: the GEMMs then read the caller's tensors and write the result in place
+// of the workspace copies (no pack / unpack pass).
+template <typename T>
+bool big_direct(int n, int np, std::initializer_list<const void*> ptrs) {
+  if (!std::is_same<T, float>::value || n != np) return false;
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) & 15) return false;
+  return true;
+}
+
+template <int MODE, bool SCALED, bool TX = false, bool TY = false>
+void big_gemm(const float* X, const float* Y, const float* E, const float* rowsum, float* D, int np, int64_t bh,
+              hipStream_t st) {
+  hipLaunchKernelGGL((newton_big_gemm_kernel<TX, TY, MODE, SCALED>), dim3(big_gemm_blocks(np, bh)), dim3(256), 0, st,
+                     X, Y, E, rowsum, D, np, (int)bh);
 }
 
 template <typename T>
@@ -646,20 +708,32 @@ int big_fwd(const T* mat, T* out, int64_t bh, int n, int iters, float* ws, hipSt
   float* Va = ws + (size_t)bh * mat_elems;
   float* Vb = ws + 2 * (size_t)bh * mat_elems;
   float* Tm = ws + 3 * (size_t)bh * mat_elems;
-  hipLaunchKernelGGL(newton_big_init_kernel<T>, dim3((unsigned)bh), dim3(np), 0, st, mat, P, Va, n, np);
+  float* rs = ws + 4 * (size_t)bh * mat_elems;
+  const bool direct = big_direct<T>(n, np, {out});
+  hipLaunchKernelGGL(newton_big_init_kernel<T>, dim3((unsigned)(np / kInitRows), (unsigned)bh), dim3(256), 0, st,
+                     mat, P, rs, n, np);
   int s = check_launch("newton forward init");
   if (s) return s;
-  const unsigned blocks = big_gemm_blocks(np, bh);
+  dim3 ug(ceil_div(n * n, 256), (unsigned)bh);
+  if (iters == 0) {  // V0 = alpha P
+    hipLaunchKernelGGL((newton_big_unpack_kernel<T, 1, true>), ug, dim3(256), 0, st, P, out, rs, n, np);
+    return check_launch("newton forward output");
+  }
   for (int it = 0; it < iters; ++it) {
-    hipLaunchKernelGGL((newton_big_gemm_kernel<false, false, 0>), dim3(blocks), dim3(256), 0, st, P, Va,
-                       static_cast<const float*>(nullptr), Tm, np, (int)bh);  // T = P V
-    hipLaunchKernelGGL((newton_big_gemm_kernel<false, false, 1>), dim3(blocks), dim3(256), 0, st, Va, Tm, Va, Vb,
-                       np, (int)bh);  // V' = 2V - V T
+    float* dst = (direct && it == iters - 1) ? reinterpret_cast<float*>(out) : Vb;
+    if (it == 0) {  // V0 = alpha P:  T = alpha (P P),  V1 = alpha (2P - P T)
+      big_gemm<0, true>(P, P, nullptr, rs, Tm, np, bh, st);
+      big_gemm<1, true>(P, Tm, P, rs, dst, np, bh, st);
+    } else {        // T = P V,  V' = 2V - V T
+      big_gemm<0, false>(P, Va, nullptr, nullptr, Tm, np, bh, st);
+      big_gemm<1, false>(Va, Tm, Va, nullptr, dst, np, bh, st);
+    }
     if ((s = check_launch("newton forward step"))) return s;
     std::swap(Va, Vb);
   }
-  dim3 ug(ceil_div(n * n, 256), (unsigned)bh);
-  hipLaunchKernelGGL((newton_big_unpack_kernel<T, 1>), ug, dim3(256), 0, st, Va, out, n, np);
+  if (direct) return LFAMD_OK;
+  hipLaunchKernelGGL((newton_big_unpack_kernel<T, 1, false>), ug, dim3(256), 0, st, Va, out,
+                     static_cast<const float*>(nullptr), n, np);
   return check_launch("newton forward output");
 }
 
@@ -667,21 +741,29 @@ template <typename T>
 int big_bwd(const T* g, const T* inv, T* out, int64_t bh, int n, float* ws, hipStream_t st) {
   const int np = big_np(n);
   const size_t mat_elems = (size_t)np * np;
+  float* S = ws + 2 * (size_t)bh * mat_elems;
+  // The second product reads V while it writes out: direct only when they do not overlap.
+  const size_t bytes = (size_t)bh * n * n * sizeof(T);
+  const uintptr_t o = reinterpret_cast<uintptr_t>(out), v = reinterpret_cast<uintptr_t>(inv);
+  const bool apart = o + bytes <= v || v + bytes <= o;
+  if (apart && big_direct<T>(n, np, {g, inv, out})) {  // S = V^T G,  out = -S V^T
+    const float* Vf = reinterpret_cast<const float*>(inv);
+    big_gemm<0, false, true, false>(Vf, reinterpret_cast<const float*>(g), nullptr, nullptr, S, np, bh, st);
+    big_gemm<2, false, false, true>(S, Vf, nullptr, nullptr, reinterpret_cast<float*>(out), np, bh, st);
+    return check_launch("newton backward products");
+  }
   float* Vf = ws;
   float* Gf = ws + (size_t)bh * mat_elems;
-  float* S = ws + 2 * (size_t)bh * mat_elems;
   dim3 pg(ceil_div(np * np, 256), (unsigned)bh);
   hipLaunchKernelGGL(newton_big_pack_kernel<T>, pg, dim3(256), 0, st, inv, Vf, n, np);
   hipLaunchKernelGGL(newton_big_pack_kernel<T>, pg, dim3(256), 0, st, g, Gf, n, np);
-  const unsigned blocks = big_gemm_blocks(np, bh);
-  hipLaunchKernelGGL((newton_big_gemm_kernel<true, false, 0>), dim3(blocks), dim3(256), 0, st, Vf, Gf,
-                     static_cast<const float*>(nullptr), S, np, (int)bh);  // S = V^T G
-  hipLaunchKernelGGL((newton_big_gemm_kernel<false, true, 0>), dim3(blocks), dim3(256), 0, st, S, Vf,
-                     static_cast<const float*>(nullptr), Gf, np, (int)bh);  // R = S V^T (into G's slot)
+  big_gemm<0, false, true, false>(Vf, Gf, nullptr, nullptr, S, np, bh, st);  // S = V^T G
+  big_gemm<2, false, false, true>(S, Vf, nullptr, nullptr, Gf, np, bh, st);  // -S V^T (into G's slot)
   int s = check_launch("newton backward products");
   if (s) return s;
   dim3 ug(ceil_div(n * n, 256), (unsigned)bh);
-  hipLaunchKernelGGL((newton_big_unpack_kernel<T, -1>), ug, dim3(256), 0, st, Gf, out, n, np);
+  hipLaunchKernelGGL((newton_big_unpack_kernel<T, 1, false>), ug, dim3(256), 0, st, Gf, out,
+                     static_cast<const float*>(nullptr), n, np);
   return check_launch("newton backward output");
 }
 

@@ -181,6 +181,36 @@ def test_newton_large_backward(gpu, dt, n):
     assert_newton_close(out, oracle.newton_backward(G, V, dt), dt, f"bwd {dt} n={n}", rtol=1e-5)
 
 
+def test_newton_large_backward_in_place_and_unaligned(gpu):
+    """fp32 n = 256 reads and writes the caller's tensors directly unless the output
+    overlaps the inverse or a pointer is not 16-byte aligned; every route gives the
+    same bits."""
+    import laplacianformer_amd as lf
+
+    n = 256
+    print("newton large backward aliasing / alignment", flush=True)
+    V = gen((2, 1, n, n), 41, "f32", scale=0.1).to(gpu)
+    G = gen((2, 1, n, n), 42, "f32").to(gpu)
+    L = lf.ext()
+    want = torch.empty_like(V)
+    L.NewtonInverse_backward(G, V, want)
+    got = V.clone()
+    L.NewtonInverse_backward(G, got, got)  # output written over the inverse
+    assert torch.equal(got, want)
+    buf = torch.empty(3 * V.numel() + 1, device=gpu)
+    Vu = buf[1:1 + V.numel()].view_as(V).copy_(V)  # 4-byte offset: not 16-byte aligned
+    Gu = buf[1 + V.numel():1 + 2 * V.numel()].view_as(G).copy_(G)
+    Ou = buf[1 + 2 * V.numel():].view_as(V)
+    L.NewtonInverse_backward(Gu, Vu, Ou)
+    assert torch.equal(Ou, want)
+    A = torch.from_numpy(gram(1, n, 32, seed=5)).float().reshape(1, 1, n, n).to(gpu)
+    fa = torch.empty_like(A)
+    L.NewtonInverse_forward(A, fa, 3)
+    fb = torch.empty(A.numel() + 1, device=gpu)[1:].view_as(A)
+    L.NewtonInverse_forward(A, fb, 3)
+    assert torch.equal(fa, fb)
+
+
 def test_newton_large_closed_form(gpu):
     """Diagonal A = c I at n = 256: X_k = (1 - (-0.8)^(2^k)) / (c + 0.01) * I, off-diagonal exactly 0."""
     import laplacianformer_amd as lf
