@@ -134,8 +134,9 @@ int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const flo
 
 /* Bytes of device workspace lfamd_newton_forward / lfamd_newton_backward need:
  * 0 for n <= 128 (matrices stay in LDS) and for fp64; for 128 < n <= 256 four
- * fp32 copies per matrix padded to 64*ceil(n/64) (the products run as batched
- * GEMMs). No reference counterpart (the reference stops at n = 128). */
+ * fp32 copies per matrix padded to NP = 64*ceil(n/64) plus NP row sums (the
+ * products run as batched GEMMs). No reference counterpart (the reference
+ * stops at n = 128). */
 size_t lfamd_newton_workspace_size(int dtype, int64_t batch_heads, int64_t n);
 
 /* Newton-Schulz inverse of P = mat + 0.01*I for each of the batch_heads n x n

@@ -449,7 +449,7 @@ newton_bwd_f64_kernel(const double* __restrict__ gout, const double* __restrict_
 // matrix cores over fp32 copies in a caller workspace, zero-padded to
 // NP = 64*ceil(n/64):  T = P V,  V' = 2V - V T  (the V(PV) order, ping-pong V).
 // ---------------------------------------------------------------------------
-constexpr int kBgTile = 64;  // output tile per workgroup (4 waves, 32 x 32 each)
+constexpr int kBgTile = 64;  // padding granule of NP (and the smallest workgroup tile side)
 constexpr int kBgK = 16;     // k per LDS stage
 
 constexpr int kBgMaxNP = 256;  // largest padded size of the GEMM path
@@ -530,100 +530,116 @@ newton_big_unpack_kernel(const float* __restrict__ src, T* __restrict__ dst, con
 // Batched D = f(op(X) op(Y)) over NP x NP fp32 matrices (row-major, matrix
 // stride NP*NP), op = transpose when TX / TY. MODE 0: D = XY; 1: D = 2E - XY;
 // 2: D = -XY. SCALED multiplies the result by the matrix's alpha (from the
-// init kernel's row sums). Grid: (NP/64)^2 tiles x matrices, flattened so that
+// init kernel's row sums). One TM x TN output tile per 4-wave workgroup (2 x 2
+// waves of TM/2 x TN/2). Grid: (NP/TM)(NP/TN) tiles x matrices, flattened so that
 // all tiles of a matrix share blockIdx.x mod 8 (workgroups are dealt to the 8
 // XCDs round robin, so a matrix's tiles share one L2). Both operands are staged
-// k-major in LDS ([k][64]) with the columns of row k XOR-swizzled by
+// k-major in LDS ([k][TM], [k][TN]) with the columns of row k XOR-swizzled by
 // 16 * ((k + k/4) mod 4): the 4 k rows of an MFMA operand read then fall on 4
 // different 16-bank groups, and so do the 4 rows of a transposing store
 // (conflict-free both ways, no padding). Two LDS stages, one
 // barrier per stage; global loads run two stages ahead of the MFMAs through
 // two register sets, so each load has two stages of MFMA work to land in.
-template <bool TX, bool TY, int MODE, bool SCALED>
+template <int TM, int TN, bool TX, bool TY, int MODE, bool SCALED>
 __global__ void __launch_bounds__(256)
 newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ E,
                        const float* __restrict__ rowsum, float* __restrict__ D, int NP, int nMat) {
-  __shared__ __align__(16) float As[2][kBgK][kBgTile];
-  __shared__ __align__(16) float Bs[2][kBgK][kBgTile];
+  static_assert(TM % 64 == 0 && TN % 64 == 0, "tile sides are multiples of 64");
+  constexpr int RT = TM / 32, CT = TN / 32;     // 16x16 accumulators per wave (2 x 2 waves)
+  constexpr int LA = TM / 64, LB = TN / 64;     // float4 staging loads per thread per operand
+  __shared__ __align__(16) float As[2][kBgK][TM];
+  __shared__ __align__(16) float Bs[2][kBgK][TN];
   auto sw = [](int k) { return 16 * ((k + (k >> 2)) & 3); };
-  const int nt = NP / kBgTile;
-  const int tiles = nt * nt;
+  const int ntm = NP / TM, ntn = NP / TN;
+  const int tiles = ntm * ntn;
   // Inverse of the flattening: id = (m % 8) + 8 * (t + tiles * (m / 8)).
   const int id = blockIdx.x;
   const int lo = id & 7, hi = id >> 3;
   const int t = hi % tiles, mg = hi / tiles;
   const int m = mg * 8 + lo;
   if (m >= nMat) return;  // whole workgroup
-  const int ti = t / nt, tj = t - ti * nt;
+  const int ti = t / ntn, tj = t - ti * ntn;
   const size_t mo = (size_t)m * NP * NP;
   const float* Xm = X + mo;
   const float* Ym = Y + mo;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+  const int wr = (wave >> 1) * (TM / 2), wc = (wave & 1) * (TN / 2);
   float alpha = 1.0f;
   if constexpr (SCALED) alpha = big_alpha(rowsum + (size_t)m * NP, NP);
 
-  // Global -> register staging of one k stage: 64 x 16 of op(X) and 16 x 64 of op(Y), one float4 each.
-  auto load = [&](float4& ra, float4& rb, int k0) {
-    if (TX) {  // A[i][k] = X[k][i]: 16 rows of X, 64 contiguous columns
-      const int k = tid >> 4, iq = (tid & 15) * 4;
-      ra = *reinterpret_cast<const float4*>(Xm + (size_t)(k0 + k) * NP + ti * kBgTile + iq);
-    } else {   // A[i][k] = X[i][k]: 64 rows of X, 16 contiguous columns
-      const int i = tid >> 2, kq = (tid & 3) * 4;
-      ra = *reinterpret_cast<const float4*>(Xm + (size_t)(ti * kBgTile + i) * NP + k0 + kq);
+  // Global -> register staging of one k stage: TM x 16 of op(X) and 16 x TN of op(Y).
+  auto load = [&](float4 (&ra)[LA], float4 (&rb)[LB], int k0) {
+#pragma unroll
+    for (int u = 0; u < LA; ++u) {
+      if (TX) {  // A[i][k] = X[k][i]: 16 rows of X, TM contiguous columns
+        const int e = tid + 256 * u, k = e / (TM / 4), iq = (e % (TM / 4)) * 4;
+        ra[u] = *reinterpret_cast<const float4*>(Xm + (size_t)(k0 + k) * NP + ti * TM + iq);
+      } else {   // A[i][k] = X[i][k]: TM rows of X, 16 contiguous columns
+        const int i = (tid >> 2) + 64 * u, kq = (tid & 3) * 4;
+        ra[u] = *reinterpret_cast<const float4*>(Xm + (size_t)(ti * TM + i) * NP + k0 + kq);
+      }
     }
-    if (TY) {  // B[k][j] = Y[j][k]
-      const int j = tid >> 2, kq = (tid & 3) * 4;
-      rb = *reinterpret_cast<const float4*>(Ym + (size_t)(tj * kBgTile + j) * NP + k0 + kq);
-    } else {   // B[k][j] = Y[k][j]
-      const int k = tid >> 4, jq = (tid & 15) * 4;
-      rb = *reinterpret_cast<const float4*>(Ym + (size_t)(k0 + k) * NP + tj * kBgTile + jq);
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      if (TY) {  // B[k][j] = Y[j][k]
+        const int j = (tid >> 2) + 64 * u, kq = (tid & 3) * 4;
+        rb[u] = *reinterpret_cast<const float4*>(Ym + (size_t)(tj * TN + j) * NP + k0 + kq);
+      } else {   // B[k][j] = Y[k][j]
+        const int e = tid + 256 * u, k = e / (TN / 4), jq = (e % (TN / 4)) * 4;
+        rb[u] = *reinterpret_cast<const float4*>(Ym + (size_t)(k0 + k) * NP + tj * TN + jq);
+      }
     }
   };
-  auto store = [&](const float4& ra, const float4& rb, int b) {
-    if (TX) {
-      const int k = tid >> 4, iq = (tid & 15) * 4;
-      *reinterpret_cast<float4*>(&As[b][k][iq ^ sw(k)]) = ra;
-    } else {
-      const int i = tid >> 2, kq = (tid & 3) * 4;
-      As[b][kq + 0][i ^ sw(kq + 0)] = ra.x; As[b][kq + 1][i ^ sw(kq + 1)] = ra.y;
-      As[b][kq + 2][i ^ sw(kq + 2)] = ra.z; As[b][kq + 3][i ^ sw(kq + 3)] = ra.w;
+  auto store = [&](const float4 (&ra)[LA], const float4 (&rb)[LB], int b) {
+#pragma unroll
+    for (int u = 0; u < LA; ++u) {
+      if (TX) {
+        const int e = tid + 256 * u, k = e / (TM / 4), iq = (e % (TM / 4)) * 4;
+        *reinterpret_cast<float4*>(&As[b][k][iq ^ sw(k)]) = ra[u];
+      } else {
+        const int i = (tid >> 2) + 64 * u, kq = (tid & 3) * 4;
+        As[b][kq + 0][i ^ sw(kq + 0)] = ra[u].x; As[b][kq + 1][i ^ sw(kq + 1)] = ra[u].y;
+        As[b][kq + 2][i ^ sw(kq + 2)] = ra[u].z; As[b][kq + 3][i ^ sw(kq + 3)] = ra[u].w;
+      }
     }
-    if (TY) {
-      const int j = tid >> 2, kq = (tid & 3) * 4;
-      Bs[b][kq + 0][j ^ sw(kq + 0)] = rb.x; Bs[b][kq + 1][j ^ sw(kq + 1)] = rb.y;
-      Bs[b][kq + 2][j ^ sw(kq + 2)] = rb.z; Bs[b][kq + 3][j ^ sw(kq + 3)] = rb.w;
-    } else {
-      const int k = tid >> 4, jq = (tid & 15) * 4;
-      *reinterpret_cast<float4*>(&Bs[b][k][jq ^ sw(k)]) = rb;
+#pragma unroll
+    for (int u = 0; u < LB; ++u) {
+      if (TY) {
+        const int j = (tid >> 2) + 64 * u, kq = (tid & 3) * 4;
+        Bs[b][kq + 0][j ^ sw(kq + 0)] = rb[u].x; Bs[b][kq + 1][j ^ sw(kq + 1)] = rb[u].y;
+        Bs[b][kq + 2][j ^ sw(kq + 2)] = rb[u].z; Bs[b][kq + 3][j ^ sw(kq + 3)] = rb[u].w;
+      } else {
+        const int e = tid + 256 * u, k = e / (TN / 4), jq = (e % (TN / 4)) * 4;
+        *reinterpret_cast<float4*>(&Bs[b][k][jq ^ sw(k)]) = rb[u];
+      }
     }
   };
 
-  v4f acc[2][2];
+  v4f acc[RT][CT];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < RT; ++r)
 #pragma unroll
-    for (int c = 0; c < 2; ++c) acc[r][c] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < CT; ++c) acc[r][c] = v4f{0.f, 0.f, 0.f, 0.f};
   const int li = lane & 15, lk = lane >> 4;
   auto compute = [&](int b) {
 #pragma unroll
     for (int ks = 0; ks < kBgK; ks += 4) {
-      float a[2], bb[2];
+      float a[RT], bb[CT];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) a[r] = As[b][ks + lk][(wr + 16 * r + li) ^ sw(ks + lk)];
+      for (int r = 0; r < RT; ++r) a[r] = As[b][ks + lk][(wr + 16 * r + li) ^ sw(ks + lk)];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) bb[c] = Bs[b][ks + lk][(wc + 16 * c + li) ^ sw(ks + lk)];
+      for (int c = 0; c < CT; ++c) bb[c] = Bs[b][ks + lk][(wc + 16 * c + li) ^ sw(ks + lk)];
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], bb[c], acc[r][c], 0, 0, 0);
+        for (int c = 0; c < CT; ++c) acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], bb[c], acc[r][c], 0, 0, 0);
     }
   };
 
   // nk = NP / 16 is a multiple of 4: stages go in pairs, even stages through
   // LDS buffer 0 and register set 0, odd ones through buffer 1 and set 1.
   const int nk = NP / kBgK;
-  float4 ra0, rb0, ra1, rb1;
+  float4 ra0[LA], rb0[LB], ra1[LA], rb1[LB];
   load(ra0, rb0, 0);
   load(ra1, rb1, kBgK);
   store(ra0, rb0, 0);
@@ -642,13 +658,13 @@ newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y,
   float* Dm = D + mo;
   const float* Em = MODE == 1 ? E + mo : nullptr;
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < RT; ++r)
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < CT; ++c)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int i = ti * kBgTile + wr + 16 * r + 4 * lk + q;
-        const int j = tj * kBgTile + wc + 16 * c + li;
+        const int i = ti * TM + wr + 16 * r + 4 * lk + q;
+        const int j = tj * TN + wc + 16 * c + li;
         const size_t o = (size_t)i * NP + j;
         float v = acc[r][c][q];
         if (MODE == 1) v = 2.0f * Em[o] - v;
@@ -677,8 +693,8 @@ size_t big_workspace_bytes(int64_t bh, int64_t n) {
   return (size_t)bh * (kBigBuffers * np * np + np) * 4;
 }
 
-unsigned big_gemm_blocks(int np, int64_t bh) {
-  const int tiles = (np / kBgTile) * (np / kBgTile);
+unsigned big_gemm_blocks(int np, int tm, int tn, int64_t bh) {
+  const int tiles = (np / tm) * (np / tn);
   return (unsigned)(8 * tiles * ((bh + 7) / 8));  // matrices rounded up to a multiple of 8
 }
 
@@ -693,11 +709,18 @@ bool big_direct(int n, int np, std::initializer_list<const void*> ptrs) {
   return true;
 }
 
+// Tiles: 128 x 64 for the forward's products (neither operand transposed) when
+// 128 divides NP, measured 10 % faster than 64 x 64 at 128 x 256^2; 64 x 64
+// otherwise (the backward's transposed products measured 15 % slower at 128 x 64).
 template <int MODE, bool SCALED, bool TX = false, bool TY = false>
 void big_gemm(const float* X, const float* Y, const float* E, const float* rowsum, float* D, int np, int64_t bh,
               hipStream_t st) {
-  hipLaunchKernelGGL((newton_big_gemm_kernel<TX, TY, MODE, SCALED>), dim3(big_gemm_blocks(np, bh)), dim3(256), 0, st,
-                     X, Y, E, rowsum, D, np, (int)bh);
+  if (!TX && !TY && np % 128 == 0)
+    hipLaunchKernelGGL((newton_big_gemm_kernel<128, 64, TX, TY, MODE, SCALED>),
+                       dim3(big_gemm_blocks(np, 128, 64, bh)), dim3(256), 0, st, X, Y, E, rowsum, D, np, (int)bh);
+  else
+    hipLaunchKernelGGL((newton_big_gemm_kernel<64, 64, TX, TY, MODE, SCALED>),
+                       dim3(big_gemm_blocks(np, 64, 64, bh)), dim3(256), 0, st, X, Y, E, rowsum, D, np, (int)bh);
 }
 
 template <typename T>
