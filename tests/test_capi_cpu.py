@@ -64,7 +64,7 @@ def test_argument_errors_without_device(lib):
     assert lib.lfamd_newton_backward(9, null, null, null, 4, 16, null, 0, null) == 2
     # 128 < n <= 256 needs the fp32 workspace; without one the call is rejected before any launch.
     ws = lib.lfamd_newton_workspace_size(0, 4, 200)
-    assert ws == 4 * 4 * 256 * 256 * 4
+    assert ws == 4 * (4 * 256 * 256 + 256) * 4  # per matrix: four padded fp32 copies + the row sums
     assert lib.lfamd_newton_workspace_size(0, 4, 128) == 0
     assert lib.lfamd_newton_workspace_size(3, 4, 90) == 0
     dummy = ctypes.c_void_p(16)
