@@ -14,7 +14,10 @@ distances accumulate in fp32 and are never rounded to it (an fp16 distance,
 ~70 at d = 64, would move exp(-dist/8) by ~0.4 %): the Laplacian kernels come
 out of the fused distance+exp op in fp32 (fp64 for fp64 inputs), and the
 products from there on run in that type. The result is returned in the input
-type.
+type. The products that stream the N-row matrices (K_qm . W with
+W = NewtonInverse(K_mm) . K_km^T V, and in the backward G . W^T, V . grad_kv^T,
+K_km . grad_kv) run on the HIP row-product kernel (inner and output widths
+<= 64); K_km^T V, K_qm^T G and the M x M products on the library GEMM.
 """
 from __future__ import annotations
 
@@ -22,7 +25,7 @@ import math
 
 import torch
 
-from .functional import laplace_kernel, newton_inverse
+from .functional import laplace_kernel, newton_inverse, tall_mix, tall_product
 
 
 def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor:
@@ -57,8 +60,8 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
     k_mm = laplace_kernel(km, km_cm, s)        # [B,H,M,M]
     k_km = laplace_kernel(k, km_cm, s)         # [B,H,N,M] = K_mk^T
     inv = newton_inverse(k_mm, iters)          # [B,H,M,M]
-    kv = torch.matmul(k_km.transpose(-1, -2), v.to(ct))  # [B,H,M,d], transposed fp32 operand
-    out = torch.matmul(k_qm, torch.matmul(inv, kv))
+    kv = tall_product(k_km, v)                 # [B,H,M,d] = K_km^T V
+    out = tall_mix(k_qm, torch.matmul(inv, kv))  # [B,H,N,d]
     return out.to(in_dtype)
 
 

@@ -1,0 +1,160 @@
+// mix_kernels.hip - the LaplacianFormer attention layer's output-heavy products
+// on gfx950 (no reference counterpart: the reference ships the two operators
+// only; these are the caller's matrix products around them).
+//
+//   C[s][n][q] = sum_{p < P} A[s][n][p] * B[s](q, p),   q < Q,  P, Q <= 64
+//
+// with A a tall [N, P] matrix per slice s (N in the thousands) and B a small
+// Q x P matrix addressed through element strides (so that both W and W^T are
+// read in place). The layer's K_qm . W, grad_out . W^T, V . grad_kv^T and
+// K_km . grad_kv are all of this form. With an inner dimension of at most 64
+// these products are HBM-bound (A in, C out: ~45 MB per product at config 5).
+// Each A value feeds Q multiply-adds, so a VALU kernel would read it from LDS
+// once per wave-wide FMA and be LDS-bound; the matrix cores take 4 k-steps of a
+// 16 x 16 tile per 16-byte operand read instead. A workgroup (4 waves) takes
+// 64-row tiles of A in turn (the next tile's loads in flight during the current
+// one's products): A rows and B staged in LDS (pitch 68 floats), wave w computes
+// rows [16w, 16w + 16) x all Q columns as four 16 x 16 v_mfma_f32_16x16x4_f32
+// accumulators, with the B operand (64 values per lane) in registers for the
+// whole tile and k permuted per lane (k = 16 kb + 4 (lane / 16) + step) so that
+// both operands are read as float4. fp32 products and sums throughout; tests
+// compare against an fp64 product within 1e-5 of sum |a| |b|.
+#include <algorithm>
+
+#include "lf_common.h"
+#include "lf_internal.h"
+
+namespace lfamd {
+
+typedef float v4f __attribute__((ext_vector_type(4)));  // one 16 x 16 MFMA accumulator per lane
+
+constexpr int kMixPMax = 64;   // largest inner / output width
+constexpr int kMixRows = 64;   // rows of A per workgroup
+constexpr int kMixLS = 68;     // LDS pitch (floats): lane-varying 16-byte reads without conflicts
+
+template <typename TA>
+__global__ void __launch_bounds__(256)
+mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int N, int P,
+                int Q, int64_t sq, int64_t sp, int64_t bStride) {
+  __shared__ __align__(16) float Bs[kMixPMax * kMixLS];  // Bs[q][p], zero outside Q x P
+  __shared__ __align__(16) float As[kMixRows * kMixLS];  // As[r][p], zero outside the rows and P
+  const int s = blockIdx.y;
+  const int tiles = (N + kMixRows - 1) / kMixRows;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float* Bm = B + (size_t)s * bStride;
+  const TA* As0 = A + (size_t)s * N * P;
+
+  // A tile t into registers: slot e = (row e / 64, column e % 64), zero outside.
+  float va[16];
+  auto loadA = [&](int t) {
+    const int n0 = t * kMixRows, rows = min(kMixRows, N - n0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = threadIdx.x + 256 * u, r = e >> 6, p = e & 63;
+      va[u] = (r < rows && p < P) ? to_acc(As0[(size_t)(n0 + r) * P + p]) : 0.0f;
+    }
+  };
+  int t = blockIdx.x;
+  if (t < tiles) loadA(t);  // in flight while B is staged
+
+  // B (4096 slots, 16 per thread), consecutive threads along its smaller stride
+  // (coalesced for W and for W^T); all loads issued before the stores.
+  {
+    const bool qFast = sq < sp;
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = threadIdx.x + 256 * u;
+      const int q = qFast ? (e & 63) : (e >> 6), p = qFast ? (e >> 6) : (e & 63);
+      v[u] = (q < Q && p < P) ? Bm[q * sq + p * sp] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = threadIdx.x + 256 * u;
+      const int q = qFast ? (e & 63) : (e >> 6), p = qFast ? (e >> 6) : (e & 63);
+      Bs[q * kMixLS + p] = v[u];
+    }
+  }
+  __syncthreads();
+  const int li = lane & 15, lg = lane >> 4;
+  float bq[4][4][4];  // [column tile c][k block kb][step]: B[k = 16 kb + 4 lg + step][16 c + li]
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 v = *reinterpret_cast<const float4*>(&Bs[(16 * c + li) * kMixLS + 16 * kb + 4 * lg]);
+      bq[c][kb][0] = v.x; bq[c][kb][1] = v.y; bq[c][kb][2] = v.z; bq[c][kb][3] = v.w;
+    }
+
+  // Tiles t, t + gridDim.x, ...: the next tile's rows are loaded while this one's
+  // products run.
+  for (; t < tiles; t += gridDim.x) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int e = threadIdx.x + 256 * u;
+      As[(e >> 6) * kMixLS + (e & 63)] = va[u];
+    }
+    __syncthreads();
+    if (t + (int)gridDim.x < tiles) loadA(t + gridDim.x);
+    v4f acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 v = *reinterpret_cast<const float4*>(&As[(16 * wave + li) * kMixLS + 16 * kb + 4 * lg]);
+      const float a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], bq[c][kb][st], acc[c], 0, 0, 0);
+    }
+    const int n0 = t * kMixRows, rows = min(kMixRows, N - n0);
+    float* Cm = C + ((size_t)s * N + n0) * Q;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * wave + 4 * lg + r, col = 16 * c + li;
+        if (row < rows && col < Q) Cm[(size_t)row * Q + col] = acc[c][r];
+      }
+    __syncthreads();  // every wave's reads of this tile are done before the next is stored
+  }
+}
+
+// Workgroups per slice: about two per CU over the whole grid (each loops over its
+// share of the slice's 64-row tiles; measured best of 1, 2, 4 and 16 per CU).
+template <typename TA>
+int launch_mix(const void* A, const float* B, float* C, int64_t slices, int64_t N, int P, int Q, int64_t sq,
+               int64_t sp, int64_t bStride, hipStream_t st) {
+  const int64_t tiles = (N + kMixRows - 1) / kMixRows;
+  const int64_t per = std::max<int64_t>(1, std::min<int64_t>(tiles, (2 * (int64_t)num_cus() + slices - 1) / slices));
+  dim3 grid((unsigned)per, (unsigned)slices);
+  hipLaunchKernelGGL(mix_rows_kernel<TA>, grid, dim3(256), 0, st, static_cast<const TA*>(A), B, C, (int)N, P, Q,
+                     sq, sp, bStride);
+  return check_launch("mix rows");
+}
+
+}  // namespace lfamd
+
+using namespace lfamd;
+
+extern "C" int lfamd_mix_rows(int dtype, const void* a, const float* b, float* c, int64_t slices, int64_t rows,
+                              int inner, int cols, int64_t b_col_stride, int64_t b_inner_stride,
+                              int64_t b_slice_stride, void* stream) {
+  if (dtype != LFAMD_F32 && dtype != LFAMD_F16 && dtype != LFAMD_BF16)
+    return fail(LFAMD_ERR_DTYPE, "mix rows: unsupported dtype %d", dtype);
+  if (slices < 0 || rows < 0 || inner < 1 || cols < 1 || slices > 65535 || rows > (int64_t)1 << 30)
+    return fail(LFAMD_ERR_ARG, "mix rows: bad sizes (slices=%lld rows=%lld inner=%d cols=%d)", (long long)slices,
+                (long long)rows, inner, cols);
+  if (inner > kMixPMax || cols > kMixPMax)
+    return fail(LFAMD_ERR_UNSUPPORTED, "mix rows: inner=%d, cols=%d exceed %d", inner, cols, kMixPMax);
+  if (slices == 0 || rows == 0) return ok();
+  if (!a || !b || !c) return fail(LFAMD_ERR_ARG, "mix rows: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case LFAMD_F32: return launch_mix<float>(a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
+    case LFAMD_F16: return launch_mix<f16s>(a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
+    default: return launch_mix<bf16s>(a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
+  }
+}

@@ -30,6 +30,10 @@ bool LaplaceKernel_forward_cuda(const at::Tensor query, const at::Tensor key, at
 bool LaplaceKernel_backward_cuda(const at::Tensor gradKernel, const at::Tensor kernel, const at::Tensor query,
                                  const at::Tensor key, std::optional<at::Tensor> gradQuery,
                                  std::optional<at::Tensor> gradKey, double scale);
+// LaplacianFormer attention layer's row products (no reference counterpart):
+// C[..., n, q] = sum_p A[..., n, p] * B[..., q, p] for a small B read through its
+// strides, inner and output widths <= 64 (lfamd_mix_rows).
+void MixRows_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c);
 #endif
 
 inline void LaplaceSubtraction_forward(const at::Tensor query, const at::Tensor key, at::Tensor output) {
@@ -94,6 +98,17 @@ inline bool LaplaceKernel_forward(const at::Tensor query, const at::Tensor key, 
   if (query.is_cuda() && key.is_cuda()) {
 #if defined(WITH_HIP)
     return LaplaceKernel_forward_cuda(query, key, output, scale);
+#else
+    AT_ERROR("Not compiled with GPU support");
+#endif
+  }
+  AT_ERROR("Not implemented on the CPU");
+}
+
+inline void MixRows(const at::Tensor a, const at::Tensor b, at::Tensor c) {
+  if (a.is_cuda() && b.is_cuda() && c.is_cuda()) {
+#if defined(WITH_HIP)
+    return MixRows_cuda(a, b, c);
 #else
     AT_ERROR("Not compiled with GPU support");
 #endif

@@ -59,6 +59,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("LaplaceKernel_backward", &LaplaceKernel_backward,
         "LaplaceKernel_backward (gradKernel, kernel, query, key, gradQuery, gradKey, scale): "
         "gradQuery / gradKey may be None; False where the fused path does not apply");
+  m.def("MixRows", &MixRows,
+        "MixRows (a, b, c): c[..., n, q] = sum_p a[..., n, p] * b[..., q, p] in float32, widths <= 64 "
+        "(the attention layer's products; b is read through its strides)");
 }
 
 }  // namespace laplace

@@ -121,6 +121,77 @@ class NewtonInverseFunction(torch.autograd.Function):
         return dmat, None
 
 
+_MIX_MAX = 64  # widest inner / output dimension of the HIP row-product kernel
+
+
+def _mixable(*widths: int) -> bool:
+    return all(0 < w <= _MIX_MAX for w in widths)
+
+
+def mix_rows(a: torch.Tensor, b_qp: torch.Tensor) -> torch.Tensor:
+    """c[..., n, q] = sum_p a[..., n, p] * b_qp[..., q, p] in float32 on the HIP
+    row-product kernel (a contiguous fp32/fp16/bf16, b_qp an fp32 view of any
+    strides whose batch dims collapse to one stride; widths <= 64)."""
+    c = torch.empty(a.shape[:-1] + (b_qp.shape[-2],), dtype=torch.float32, device=a.device)
+    ext().MixRows(a.contiguous(), b_qp.float(), c)
+    return c
+
+
+class TallMixFunction(torch.autograd.Function):
+    """C = A @ W for a tall A [..., N, P] and a small fp32 W [..., P, Q] (the
+    attention layer's K_qm . (V^-1 . kv)); both products of the backward that
+    stream A's rows (grad_A = G W^T) run on the row-product kernel, grad_W = A^T G
+    on the library GEMM."""
+
+    @staticmethod
+    def forward(ctx, a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        ctx.save_for_backward(a, w)
+        return mix_rows(a, w.transpose(-1, -2))
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        a, w = ctx.saved_tensors
+        g = g.float().contiguous()
+        ga = mix_rows(g, w).to(a.dtype) if ctx.needs_input_grad[0] else None
+        gw = torch.matmul(a.transpose(-1, -2).float(), g).to(w.dtype) if ctx.needs_input_grad[1] else None
+        return ga, gw
+
+
+class TallProductFunction(torch.autograd.Function):
+    """C = A^T @ B for tall A [..., N, P] (fp32) and B [..., N, Q] (any float
+    type, used as fp32) -> [..., P, Q] (the layer's K_km^T V); forward on the
+    library GEMM, both row-streaming backward products on the row-product kernel:
+    grad_A = B G^T, grad_B = A G."""
+
+    @staticmethod
+    def forward(ctx, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        ctx.save_for_backward(a, b)
+        return torch.matmul(a.transpose(-1, -2), b.float())
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        a, b = ctx.saved_tensors
+        g = g.float().contiguous()
+        ga = mix_rows(b, g).to(a.dtype) if ctx.needs_input_grad[0] else None
+        gb = mix_rows(a, g.transpose(-1, -2)).to(b.dtype) if ctx.needs_input_grad[1] else None
+        return ga, gb
+
+
+def tall_mix(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """a @ w for tall a [..., N, P] and small fp32 w [..., P, Q]; the HIP row-product
+    kernel where P, Q <= 64 and a is fp32/fp16/bf16, torch.matmul elsewhere."""
+    if a.dtype != torch.float64 and _mixable(a.shape[-1], w.shape[-1]):
+        return TallMixFunction.apply(a, w)
+    return torch.matmul(a, w)
+
+
+def tall_product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T @ b for tall a [..., N, P] and b [..., N, Q] (b used in a's type)."""
+    if a.dtype != torch.float64 and _mixable(a.shape[-1], b.shape[-1]):
+        return TallProductFunction.apply(a, b)
+    return torch.matmul(a.transpose(-1, -2), b.to(a.dtype))
+
+
 def laplace_subtraction(query: torch.Tensor, key: torch.Tensor, key_layout: str = "cm") -> torch.Tensor:
     """Pairwise L1 distance with autograd.
 
