@@ -6,6 +6,7 @@ HIP kernels behind the C ABI of ``include/laplacianformer_amd.h``.
 """
 from ._lib import EXT_PATH, LIB_PATH, capi, check, dtype_code, ext
 from .attention import LaplacianAttention, laplacian_attention
+from .graphs import GraphedStep
 from .functional import (LaplaceKernelFunction, LaplaceSubtractionFunction, NewtonInverseFunction,
                          TallMixFunction, TallProductFunction, laplace_kernel, laplace_subtraction, mix_rows,
                          newton_inverse, tall_mix, tall_product)
@@ -14,5 +15,5 @@ __all__ = [
     "EXT_PATH", "LIB_PATH", "capi", "check", "dtype_code", "ext", "LaplaceKernelFunction",
     "LaplaceSubtractionFunction", "NewtonInverseFunction", "LaplacianAttention", "laplace_kernel",
     "laplace_subtraction", "laplacian_attention", "newton_inverse", "TallMixFunction", "TallProductFunction",
-    "mix_rows", "tall_mix", "tall_product",
+    "mix_rows", "tall_mix", "tall_product", "GraphedStep",
 ]
