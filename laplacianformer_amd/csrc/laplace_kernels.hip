@@ -249,7 +249,8 @@ template <typename T> struct FwdOut<T, kEpiExp> { using type = float; };
 template <typename T, int JB, int R, int EPI = kEpiDist>
 __global__ void __launch_bounds__(1024)
 laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
-                         typename FwdOut<T, EPI>::type* __restrict__ out, int N, int M, int C, float scale) {
+                         typename FwdOut<T, EPI>::type* __restrict__ out, int N, int Mg, int Mtot, int C,
+                         float scale) {
   using O = typename FwdOut<T, EPI>::type;
   constexpr int JBS = fb_pitch(JB);
   constexpr int NG = JBS / 4;
@@ -261,9 +262,13 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
   // partial last blocks (N not a multiple of 64R) after all of them, so the
   // workgroups dispatched last, onto CUs that already hold their share, are
   // the short ones.
+  // Column groups are the fastest grid index, so that the groups of one row
+  // block run next to each other and share its query rows in L2.
+  const int CG = (Mtot + Mg - 1) / Mg;
+  const int cg = blockIdx.x % CG;
   const int nFull = N / (64 * R);
   const int BH = gridDim.y;
-  const int id = blockIdx.y * gridDim.x + blockIdx.x;
+  const int id = blockIdx.y * (gridDim.x / CG) + blockIdx.x / CG;
   int bh, blk;
   if (id < BH * nFull) {
     bh = id / nFull;
@@ -274,6 +279,11 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
   }
   const int i0 = blk * 64 * R;
   const int rows = min(64 * R, N - i0);
+  // Column group cg: columns [cb0, cb0 + M) of the Mtot (the row stride
+  // of key and output); one group covers all columns unless the tiles of all of
+  // them would keep the workgroup to one per CU.
+  const int cb0 = cg * Mg;
+  const int M = min(Mg, Mtot - cb0);
   const int KP = W * JBS;              // key tile pitch (floats per channel)
   const int QV = C / EV;               // 16-byte vectors per query row
   const int QP = QV + 1;               // query tile pitch in vectors (padding: fewer bank conflicts)
@@ -290,12 +300,12 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
     qsm[row * QP + v] = qsrc[u];
   }
   // Key tile, fp32, zero outside [0, M); channel c staged by wave c % W.
-  const T* kb = key + (size_t)bh * C * M;
+  const T* kb = key + (size_t)bh * C * Mtot + cb0;
   for (int c = wave; c < C; c += W) {
     for (int t = lane; t < KP; t += 64) {
       const int w = t / JBS, jj = t - w * JBS;
       const int col = w * JB + jj;
-      ksm[c * KP + t] = (jj < JB && col < M) ? to_acc(kb[(size_t)c * M + col]) : 0.0f;
+      ksm[c * KP + t] = (jj < JB && col < M) ? to_acc(kb[(size_t)c * Mtot + col]) : 0.0f;
     }
   }
   __syncthreads();
@@ -379,10 +389,26 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
       }
     }
   __syncthreads();
+  constexpr int OV = 16 / (int)sizeof(O);  // output elements per 16-byte vector
+  O* dst = out + ((size_t)bh * N + i0) * Mtot + cb0;
+  if (M != Mtot) {  // a column group: rows of M elements, Mtot apart
+    if ((M % OV) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (Mtot % OV) == 0) {
+      const int vr = M / OV;
+      const uint4* src4 = reinterpret_cast<const uint4*>(otile);
+      for (int t = threadIdx.x; t < rows * vr; t += blockDim.x) {
+        const int r = t / vr;
+        reinterpret_cast<uint4*>(dst + (size_t)r * Mtot)[t - r * vr] = src4[t];
+      }
+    } else {
+      for (int t = threadIdx.x; t < rows * M; t += blockDim.x) {
+        const int r = t / M;
+        dst[(size_t)r * Mtot + (t - r * M)] = otile[t];
+      }
+    }
+    return;
+  }
   // Rows [i0, i0 + rows) are one contiguous span of rows*M elements.
   const int n = rows * M;
-  constexpr int OV = 16 / (int)sizeof(O);  // output elements per 16-byte vector
-  O* dst = out + ((size_t)bh * N + i0) * M;
   int done = 0;
   if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
     const int nv = n / OV;
@@ -1305,13 +1331,32 @@ template <> constexpr int dtype_of<double>() { return LFAMD_F64; }
 // LDS of the broadcast forward: fp32 key tile [C][W*JBS], then the query tile
 // [64R][C/EV + 1] 16-byte vectors, which the output tile [64R][M] (elements of
 // out_bytes) reuses.
-size_t fb_lds_bytes(int dtype, const Dims& d, size_t out_bytes) {
+size_t fb_lds_bytes_g(int dtype, const Dims& d, size_t out_bytes, int mg) {
   const int jb = pick_fb_jb(d.M);
-  const int W = ceil_div((int)d.M, jb);
+  const int W = ceil_div(mg, jb);
   const size_t es = dtype_size(dtype);
   const size_t qtile = (size_t)64 * kFbR * (d.C * es / 16 + 1) * 16;
-  const size_t otile = (size_t)64 * kFbR * d.M * out_bytes;
+  const size_t otile = (size_t)64 * kFbR * mg * out_bytes;
   return (size_t)W * d.C * fb_pitch(jb) * 4 + std::max(qtile, otile);
+}
+
+// Columns per workgroup: all M, or half of them (a multiple of the per-wave
+// block) when the tiles of all M would leave room for only one workgroup per CU
+// and there are row blocks for several rounds of the chip, or when all M do not
+// fit one workgroup's LDS at all (fp32 output at M = 256). Config 4 (bf16,
+// M = 256, 4096 row blocks): 662 -> 560 us; with a single round of row blocks
+// the split measured slower (31 -> 34 us at 256 blocks), so it is not taken there.
+int fb_group_cols(int dtype, const Dims& d, size_t out_bytes) {
+  const int jb = pick_fb_jb(d.M);
+  const int half = ceil_div(ceil_div((int)d.M, 2), jb) * jb;
+  const int64_t blocks = (int64_t)ceil_div((int)d.N, 64 * kFbR) * d.BH();
+  const size_t full = fb_lds_bytes_g(dtype, d, out_bytes, (int)d.M), lim = (size_t)max_lds_bytes();
+  if (half < d.M && (full > lim || (2 * full > lim && blocks >= 4 * (int64_t)num_cus()))) return half;
+  return (int)d.M;
+}
+
+size_t fb_lds_bytes(int dtype, const Dims& d, size_t out_bytes) {
+  return fb_lds_bytes_g(dtype, d, out_bytes, fb_group_cols(dtype, d, out_bytes));
 }
 
 // Broadcast forward: a non-fp64 type, C % 8 == 0, 16-byte aligned query,
@@ -1325,16 +1370,17 @@ bool fwd_bcast_ok(int dtype, const Dims& d, const void* q, size_t out_bytes) {
 template <typename T, int JB, int EPI>
 int launch_fwd_bcast_jb(const void* q, const void* k, void* o, const Dims& d, float scale, hipStream_t st) {
   using O = typename FwdOut<T, EPI>::type;
-  const int W = ceil_div((int)d.M, JB);
-  const size_t lds = fb_lds_bytes(dtype_of<T>(), d, sizeof(O));
+  const int mg = fb_group_cols(dtype_of<T>(), d, sizeof(O));
+  const int W = ceil_div(mg, JB);
+  const size_t lds = fb_lds_bytes_g(dtype_of<T>(), d, sizeof(O), mg);
   auto kern = laplace_fwd_bcast_kernel<T, JB, kFbR, EPI>;
   if (lds > 65536 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds) != hipSuccess)
     return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
-  dim3 grid(ceil_div((int)d.N, 64 * kFbR), (unsigned)d.BH());
+  dim3 grid(ceil_div((int)d.N, 64 * kFbR) * ceil_div((int)d.M, mg), (unsigned)d.BH());
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, st, static_cast<const T*>(q), static_cast<const T*>(k),
-                     static_cast<O*>(o), (int)d.N, (int)d.M, (int)d.C, scale);
+                     static_cast<O*>(o), (int)d.N, mg, (int)d.M, (int)d.C, scale);
   return check_launch("laplace forward");
 }
 

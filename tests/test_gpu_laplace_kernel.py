@@ -23,6 +23,8 @@ FWD_SHAPES = [
     (1, 2, 100, 100, 40),
     (1, 1, 129, 128, 64),
     (2, 1, 3136, 49, 64),
+    (1, 1, 129, 256, 64),   # fp32 output tiles of all 256 columns exceed the LDS: two column groups
+    (2, 1, 70, 240, 64),    # column groups of 128 and 112
 ]
 # Fused-backward shapes: fp16, M in {16, 32, 49, 64}; odd N * M and single rows included.
 BWD_SHAPES = [
@@ -117,10 +119,10 @@ def test_kernel_unsupported_reports_false(gpu):
     k3 = gen((1, 1, 16, 50), 6, "f16").to(gpu)  # M = 50
     kern3 = torch.rand((1, 1, 10, 50), device=gpu)
     assert L.LaplaceKernel_backward(kern3, kern3, q3, k3, torch.empty_like(q3), None, 0.5) is False
-    # M = 256: the fp32 output tile of 128 rows plus the key tile exceed one workgroup's LDS.
+    # M = 257: beyond the broadcast forward's 256 columns.
     q4 = gen((1, 1, 129, 64), 7, "f16").to(gpu)
-    k4 = gen((1, 1, 64, 256), 8, "f16").to(gpu)
-    assert L.LaplaceKernel_forward(q4, k4, torch.empty((1, 1, 129, 256), device=gpu), 0.5) is False
+    k4 = gen((1, 1, 64, 257), 8, "f16").to(gpu)
+    assert L.LaplaceKernel_forward(q4, k4, torch.empty((1, 1, 129, 257), device=gpu), 0.5) is False
     with pytest.raises(RuntimeError):
         L.LaplaceKernel_forward(q2, k2, torch.empty((1, 1, 10, 49), dtype=torch.float16, device=gpu), 0.5)
 
