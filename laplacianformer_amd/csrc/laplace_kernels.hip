@@ -632,7 +632,8 @@ laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
 }
 
 // ---------------------------------------------------------------------------
-// fp16 backward, every per-triple instruction at the full VALU rate.
+// Backward with every key column in registers (M in {16, 32, 49} for fp16,
+// {16, 49} for fp32 / bf16), every per-triple instruction at the full VALU rate.
 //
 // With q' = 2^24 q and k' = 2^24 k (exact for fp16 values, whose nonzero
 // differences are at least 2^-24), d = q' - k' is 0 or at least 1 in magnitude,
@@ -640,7 +641,10 @@ laplace_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ query,
 //   grad_query[i,c] = sum_j (2 g_ij) y_ijc - sum_j g_ij
 //   grad_key[c,j]   = sum_i g_ij - sum_i (2 g_ij) y_ijc
 // Per triple: v_sub, v_fma+clamp, two v_fma, all with VGPR operands (an SGPR
-// operand, v_med3 or v_fma_mix would issue at half rate on gfx950).
+// operand, v_med3 or v_fma_mix would issue at half rate on gfx950). fp32 and
+// bf16 scale the difference twice by 2^100 instead (every nonzero fp32
+// difference is at least 2^-149, so |d| 2^200 >= 2^51; overflow to +-inf clamps
+// correctly): one v_mul more per triple.
 //
 // Lane = channel, key' and the grad_key sums of the MC columns in registers.
 // Each wave owns a row range and stages its grad rows, scaled by 2, in a private
@@ -697,15 +701,18 @@ __host__ __device__ constexpr int bcast_pitch(int mc) { return (mc + 7) & ~7; }
 // the distance's gradient g = -s * gK * K is formed while a batch is staged.
 enum BwdGrad { kGradF16 = 0, kGradKernel = 1 };
 
-template <int MC, bool DQ, bool DK, int GSRC = kGradF16>
+template <typename T, int MC, bool DQ, bool DK, int GSRC = kGradF16>
 __global__ void __launch_bounds__(64 * bcast_max_waves(MC))
-laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict__ gkern,
-                         const float* __restrict__ kern, float gscale, const f16s* __restrict__ query,
-                         const f16s* __restrict__ key, f16s* __restrict__ dq, f16s* __restrict__ dk,
+laplace_bwd_bcast_kernel(const T* __restrict__ gout, const float* __restrict__ gkern,
+                         const float* __restrict__ kern, float gscale, const T* __restrict__ query,
+                         const T* __restrict__ key, T* __restrict__ dq, T* __restrict__ dk,
                          float* __restrict__ partial, int N, int C, int rowsPerWave) {
   constexpr int RB = kBcRB;
   constexpr int MP = bcast_pitch(MC);            // LDS row pitch (floats)
-  constexpr int GD = GSRC == kGradF16 ? RB * MC / 2 : RB * MC;  // grad words of a full batch
+  constexpr bool kF16 = std::is_same<T, f16s>::value;
+  constexpr int EPW = sizeof(T) == 2 ? 2 : 1;    // grad elements per 32-bit word
+  static_assert(GSRC == kGradF16 || kF16, "the kernel-gradient source is instantiated for fp16 only");
+  constexpr int GD = GSRC == kGradF16 ? RB * MC / EPW : RB * MC;  // grad words of a full batch
   constexpr int NL = (GD + 63) / 64;             // words per lane per batch
   const int W = blockDim.x >> 6;
   const int wave = uniform(threadIdx.x >> 6);
@@ -725,19 +732,19 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
   float* hsm = gneg + RB;
   float* qsm = hsm + MP;
 
-  const f16s* qb = query + (size_t)bh * N * C;
+  const T* qb = query + (size_t)bh * N * C;
   const uint32_t* gw = reinterpret_cast<const uint32_t*>(gout + (size_t)bh * N * MC);
-  const f16s* kb = key + (size_t)bh * C * MC;
+  const T* kb = key + (size_t)bh * C * MC;
 
   uint32_t gpre[NL];
   float kpre[GSRC == kGradKernel ? NL : 1];
   const float gscale2 = -2.0f * gscale;  // 2 * (-s * gK) * K == (-2s * gK) * K exactly
   int kwords = 0;                        // valid words of the fetched kernel-gradient batch
-  uint16_t qpre[RB];
+  T qpre[RB];
   auto fetch = [&](int rb) {
     if constexpr (GSRC == kGradF16) {
-      const int words = min(RB, rowEnd - rb) * MC / 2;
-      const uint32_t* src = gw + (size_t)rb * MC / 2;
+      const int words = min(RB, rowEnd - rb) * MC / EPW;
+      const uint32_t* src = gw + (size_t)rb * MC / EPW;
 #pragma unroll
       for (int t = 0; t < NL; ++t) {
         const int e = lane + 64 * t;
@@ -758,7 +765,7 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
       kwords = words;
     }
 #pragma unroll
-    for (int r = 0; r < RB; ++r) qpre[r] = (cval && rb + r < rowEnd) ? qb[(size_t)(rb + r) * C + c].bits : 0;
+    for (int r = 0; r < RB; ++r) qpre[r] = (cval && rb + r < rowEnd) ? qb[(size_t)(rb + r) * C + c] : T{};
   };
   // The first batch's loads are in flight while the key tile is staged.
   if (rowBeg < rowEnd) fetch(rowBeg);
@@ -766,7 +773,7 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
   for (int t = threadIdx.x; t < 64 * MC; t += blockDim.x) {
     const int cl = t & 63, j = t >> 6;
     const int cc = cb * 64 + cl;
-    ksm[j * 64 + cl] = cc < C ? to_acc(kb[(size_t)cc * MC + j]) * 16777216.0f : 0.0f;
+    ksm[j * 64 + cl] = cc < C ? to_acc(kb[(size_t)cc * MC + j]) * (kF16 ? 16777216.0f : 1.0f) : 0.0f;
   }
   __syncthreads();
   float kreg[MC], dka[MC];
@@ -776,20 +783,41 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
     if (DK) dka[j] = 0.0f;
   }
   float hsum = 0.0f;  // lane j < MC: sum over this wave's rows of g[i][j]
+  // fp32 / bf16: the difference is scaled twice by 2^100 (a VGPR operand: an
+  // SGPR one would halve the issue rate) before the clamped half step.
+  float scl = 0x1p100f;
+  asm volatile("" : "+v"(scl));
 
   for (int rb = rowBeg; rb < rowEnd; rb += RB) {
     const int nr = min(RB, rowEnd - rb);  // uniform
     // Stage this batch: 2g as fp32, row-major [RB][MP] (exact for fp16 g; for the
     // kernel gradient g = -s * gK * K, rounded once, then doubled exactly).
-    if constexpr (GSRC == kGradF16) {
+    if constexpr (GSRC == kGradF16 && EPW == 2) {
 #pragma unroll
       for (int t = 0; t < NL; ++t) {
         const int e = 2 * (lane + 64 * t);
         if (e < RB * MC) {
           const int r0 = e / MC, j0 = e - r0 * MC;
           const int r1 = (e + 1) / MC, j1 = e + 1 - r1 * MC;
-          gsm[r0 * MP + j0] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] & 0xffffu));
-          gsm[r1 * MP + j1] = 2.0f * (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] >> 16));
+          float lo, hi;
+          if constexpr (kF16) {
+            lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] & 0xffffu));
+            hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(gpre[t] >> 16));
+          } else {  // bf16
+            lo = __builtin_bit_cast(float, gpre[t] << 16);
+            hi = __builtin_bit_cast(float, gpre[t] & 0xffff0000u);
+          }
+          gsm[r0 * MP + j0] = 2.0f * lo;
+          gsm[r1 * MP + j1] = 2.0f * hi;
+        }
+      }
+    } else if constexpr (GSRC == kGradF16) {  // fp32: one element per word
+#pragma unroll
+      for (int t = 0; t < NL; ++t) {
+        const int e = lane + 64 * t;
+        if (e < RB * MC) {
+          const int r = e / MC, j = e - r * MC;
+          gsm[r * MP + j] = 2.0f * __builtin_bit_cast(float, gpre[t]);
         }
       }
     } else {
@@ -804,7 +832,7 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
       }
     }
 #pragma unroll
-    for (int r = 0; r < RB; ++r) qsm[r * 64 + lane] = (float)__builtin_bit_cast(_Float16, qpre[r]) * 16777216.0f;
+    for (int r = 0; r < RB; ++r) qsm[r * 64 + lane] = to_acc(qpre[r]) * (kF16 ? 16777216.0f : 1.0f);
     wave_sync();
     // Row sums (lane r) for grad_query and column sums (lane j) for grad_key.
     // Rows past nr are zero in the batch. All reads of a sum are issued before
@@ -867,7 +895,13 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
         for (int t = 0; t < 4; ++t) {
           const int j = jq * 4 + t;
           if (j < MC) {
-            const float y = half_step(qv - kreg[j]);
+            float y;
+            if constexpr (kF16) {
+              y = half_step(qv - kreg[j]);
+            } else {
+              const float e = (qv - kreg[j]) * scl;
+              y = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, scl, 0.5f), 0.0f, 1.0f);
+            }
             if (DQ) acc[t] = fmaf(gg[t], y, acc[t]);
             if (DK) {
               dka[j] = fmaf(gg[t], y, dka[j]);
@@ -882,7 +916,7 @@ laplace_bwd_bcast_kernel(const f16s* __restrict__ gout, const float* __restrict_
         // Materialise the sum here: sunk into the store's branch, the
         // accumulation would keep every column's step value live.
         asm volatile("" : "+v"(total));
-        if (cval) dq[((size_t)bh * N + rb + r) * C + c] = from_acc<f16s>(total);
+        if (cval) dq[((size_t)bh * N + rb + r) * C + c] = from_acc<T>(total);
       }
     }
     wave_sync();
@@ -1467,10 +1501,16 @@ struct BcPlan {
 };
 
 // (M = 64 runs faster on the column-block kernel below: 57 vs 62 us at B=32 N=3136.)
+// fp32 / bf16 with M = 32 (a column block) run the column-block kernel.
 bool bcast_bwd_ok(int dtype, const Dims& d, const void* g) {
-  if (dtype != LFAMD_F16) return false;
-  if (!(d.M == 16 || d.M == 32 || d.M == 49)) return false;
-  if ((d.N * d.M) % 2 != 0) return false;
+  if (dtype == LFAMD_F16) {
+    if (!(d.M == 16 || d.M == 32 || d.M == 49)) return false;
+  } else if (dtype == LFAMD_F32 || dtype == LFAMD_BF16) {
+    if (!(d.M == 16 || d.M == 49)) return false;
+  } else {
+    return false;
+  }
+  if (dtype != LFAMD_F32 && (d.N * d.M) % 2 != 0) return false;
   return (reinterpret_cast<uintptr_t>(g) & 3) == 0;
 }
 
@@ -1501,31 +1541,47 @@ struct KernGrad {
   float scale = 0.0f;
 };
 
-template <int MC, bool DQ, bool DK, int GSRC = kGradF16>
+template <typename T, int MC, bool DQ, bool DK, int GSRC = kGradF16>
 int launch_bcast_bwd_mc(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
                         const BcPlan& p, hipStream_t st, KernGrad kg = {}) {
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
-  hipLaunchKernelGGL((laplace_bwd_bcast_kernel<MC, DQ, DK, GSRC>), grid, dim3(64 * p.W), p.lds, st,
-                     static_cast<const f16s*>(g), kg.gk, kg.kv, kg.scale, static_cast<const f16s*>(q),
-                     static_cast<const f16s*>(k), static_cast<f16s*>(dq), static_cast<f16s*>(dk),
+  hipLaunchKernelGGL((laplace_bwd_bcast_kernel<T, MC, DQ, DK, GSRC>), grid, dim3(64 * p.W), p.lds, st,
+                     static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
+                     static_cast<const T*>(k), static_cast<T*>(dq), static_cast<T*>(dk),
                      static_cast<float*>(ws), (int)d.N, (int)d.C, p.rowsPerWave);
   int s = check_launch("laplace backward");
   if (s || !DK) return s;
   dim3 rgrid(ceil_div(64 * MC, 256), p.ncb, (unsigned)d.BH());
-  hipLaunchKernelGGL(laplace_dk_reduce_cm_kernel<f16s>, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
-                     static_cast<f16s*>(dk), p.nx, MC, (int)d.C);
+  hipLaunchKernelGGL(laplace_dk_reduce_cm_kernel<T>, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
+                     static_cast<T*>(dk), p.nx, MC, (int)d.C);
   return check_launch("laplace backward_key reduction");
 }
 
-template <bool DQ, bool DK, int GSRC = kGradF16>
-int launch_bcast_bwd(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                     const BcPlan& p, hipStream_t st, KernGrad kg = {}) {
-  switch (d.M) {
-    case 16: return launch_bcast_bwd_mc<16, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
-    case 32: return launch_bcast_bwd_mc<32, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
-    case 49: return launch_bcast_bwd_mc<49, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
-    default: return launch_bcast_bwd_mc<64, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+template <typename T, bool DQ, bool DK, int GSRC = kGradF16>
+int launch_bcast_bwd_t(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
+                       const BcPlan& p, hipStream_t st, KernGrad kg) {
+  if constexpr (std::is_same<T, f16s>::value) {
+    switch (d.M) {
+      case 16: return launch_bcast_bwd_mc<T, 16, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+      case 32: return launch_bcast_bwd_mc<T, 32, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+      case 49: return launch_bcast_bwd_mc<T, 49, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+      default: return launch_bcast_bwd_mc<T, 64, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    }
+  } else {
+    if (d.M == 16) return launch_bcast_bwd_mc<T, 16, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    return launch_bcast_bwd_mc<T, 49, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
   }
+}
+
+// The kernel-gradient source (fp32 gK and K) is fp16-only.
+template <bool DQ, bool DK, int GSRC = kGradF16>
+int launch_bcast_bwd(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws,
+                     const Dims& d, const BcPlan& p, hipStream_t st, KernGrad kg = {}) {
+  if constexpr (GSRC == kGradF16) {
+    if (dtype == LFAMD_F32) return launch_bcast_bwd_t<float, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    if (dtype == LFAMD_BF16) return launch_bcast_bwd_t<bf16s, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+  }
+  return launch_bcast_bwd_t<f16s, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
 }
 
 // ---- backward for M = 32 * CB (fp16 / bf16 / fp32) ----
@@ -1688,9 +1744,9 @@ int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq,
     const BcPlan sp = plan_bcast(d, doDk);
     if (doDk && (!ws || wsBytes < sp.partialElems * 4))
       return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, sp.partialElems * 4, wsBytes);
-    if (doDq && doDk) return launch_bcast_bwd<true, true>(g, q, k, dq, dk, ws, d, sp, st);
-    if (doDq) return launch_bcast_bwd<true, false>(g, q, k, dq, dk, ws, d, sp, st);
-    return launch_bcast_bwd<false, true>(g, q, k, dq, dk, ws, d, sp, st);
+    if (doDq && doDk) return launch_bcast_bwd<true, true>(dtype, g, q, k, dq, dk, ws, d, sp, st);
+    if (doDq) return launch_bcast_bwd<true, false>(dtype, g, q, k, dq, dk, ws, d, sp, st);
+    return launch_bcast_bwd<false, true>(dtype, g, q, k, dq, dk, ws, d, sp, st);
   }
   if (mb_bwd_ok(dtype, d, g)) {
     const MbPlan mp = plan_mb(d, doDk);
@@ -1759,9 +1815,9 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
   if (!valid_dtype(dtype) || check_dims(d, "workspace") || d.BH() == 0 || d.N == 0 || d.M == 0 || d.C == 0)
     return 0;
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
-  // Either backward path may run (the fp16 SGPR path also depends on pointer alignment).
+  // Any of the backward paths may run (which one also depends on pointer alignment).
   size_t bytes = plan_bwd(d, true, true, acc, dtype == LFAMD_F16 ? 2 : acc).partialElems * acc;
-  if (dtype == LFAMD_F16) bytes = std::max(bytes, plan_bcast(d, true).partialElems * 4);
+  if (dtype != LFAMD_F64) bytes = std::max(bytes, plan_bcast(d, true).partialElems * 4);
   if (dtype != LFAMD_F64 && d.M % kMbMC == 0 && d.M <= 8 * kMbMC)
     bytes = std::max(bytes, plan_mb(d, true).partialElems * 4);
   return bytes;
@@ -1830,10 +1886,10 @@ int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const flo
                 workspace_bytes);
   const KernGrad kg{grad_kernel, kernel, scale};
   if (doDq && doDk)
-    return launch_bcast_bwd<true, true, kGradKernel>(nullptr, query, key, grad_query, grad_key, workspace, d, sp, st, kg);
+    return launch_bcast_bwd<true, true, kGradKernel>(LFAMD_F16, nullptr, query, key, grad_query, grad_key, workspace, d, sp, st, kg);
   if (doDq)
-    return launch_bcast_bwd<true, false, kGradKernel>(nullptr, query, key, grad_query, nullptr, workspace, d, sp, st, kg);
-  return launch_bcast_bwd<false, true, kGradKernel>(nullptr, query, key, nullptr, grad_key, workspace, d, sp, st, kg);
+    return launch_bcast_bwd<true, false, kGradKernel>(LFAMD_F16, nullptr, query, key, grad_query, nullptr, workspace, d, sp, st, kg);
+  return launch_bcast_bwd<false, true, kGradKernel>(LFAMD_F16, nullptr, query, key, nullptr, grad_key, workspace, d, sp, st, kg);
 }
 
 int lfamd_laplace_reduce_forward(int dtype, const void* query, const void* key,

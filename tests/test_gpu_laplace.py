@@ -26,6 +26,11 @@ SHAPES = [
     (2, 1, 77, 32, 64),
     (1, 2, 200, 96, 48),
     (1, 1, 33, 128, 130),
+    # Register-resident columns (M = 16, 49) for every type: odd N * M (fp32 only there),
+    # several channel blocks, a single row.
+    (2, 1, 131, 16, 80),
+    (1, 1, 7, 49, 64),
+    (1, 2, 1, 49, 128),
 ]
 DTYPES = ["f32", "f16", "bf16", "f64"]
 
