@@ -26,14 +26,14 @@ FWD_SHAPES = [
     (1, 1, 129, 256, 64),   # fp32 output tiles of all 256 columns exceed the LDS: two column groups
     (2, 1, 70, 240, 64),    # column groups of 128 and 112
 ]
-# Fused-backward shapes: fp16, M in {16, 32, 49, 64}; odd N * M and single rows included.
+# Fused-backward shapes: fp16, M in {16, 32, 49}; odd N * M and single rows included.
 BWD_SHAPES = [
     (2, 2, 196, 49, 32),
     (1, 1, 1, 49, 64),
     (1, 1, 7, 49, 64),
     (1, 2, 131, 16, 80),
     (2, 1, 200, 32, 64),
-    (1, 1, 97, 64, 130),
+    (1, 1, 97, 32, 130),
     (2, 1, 3136, 49, 64),
 ]
 
@@ -119,6 +119,11 @@ def test_kernel_unsupported_reports_false(gpu):
     k3 = gen((1, 1, 16, 50), 6, "f16").to(gpu)  # M = 50
     kern3 = torch.rand((1, 1, 10, 50), device=gpu)
     assert L.LaplaceKernel_backward(kern3, kern3, q3, k3, torch.empty_like(q3), None, 0.5) is False
+    # M = 64: the composed path (the register-resident kernel would spill).
+    q5 = gen((1, 1, 10, 16), 9, "f16").to(gpu)
+    k5 = gen((1, 1, 16, 64), 10, "f16").to(gpu)
+    kern5 = torch.rand((1, 1, 10, 64), device=gpu)
+    assert L.LaplaceKernel_backward(kern5, kern5, q5, k5, torch.empty_like(q5), None, 0.5) is False
     # M = 257: beyond the broadcast forward's 256 columns.
     q4 = gen((1, 1, 129, 64), 7, "f16").to(gpu)
     k4 = gen((1, 1, 64, 257), 8, "f16").to(gpu)
