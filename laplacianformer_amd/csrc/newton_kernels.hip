@@ -543,7 +543,7 @@ newton_big_unpack_kernel(const float* __restrict__ src, T* __restrict__ dst, con
 template <int TM, int TN, bool TX, bool TY, int MODE, bool SCALED>
 __global__ void __launch_bounds__(256)
 newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ E,
-                       const float* __restrict__ rowsum, float* __restrict__ D, int NP, int nMat) {
+                       const float* __restrict__ rowsum, float* __restrict__ D, int NP, int K, int nMat) {
   static_assert(TM % 64 == 0 && TN % 64 == 0, "tile sides are multiples of 64");
   constexpr int RT = TM / 32, CT = TN / 32;     // 16x16 accumulators per wave (2 x 2 waves)
   constexpr int LA = TM / 64, LB = TN / 64;     // float4 staging loads per thread per operand
@@ -636,9 +636,11 @@ newton_big_gemm_kernel(const float* __restrict__ X, const float* __restrict__ Y,
     }
   };
 
-  // nk = NP / 16 is a multiple of 4: stages go in pairs, even stages through
-  // LDS buffer 0 and register set 0, odd ones through buffer 1 and set 1.
-  const int nk = NP / kBgK;
+  // The products run over k < K = 32 * ceil(n / 32) <= NP (columns and rows from n
+  // on are zero padding and contribute nothing). nk = K / 16 is even: stages go in
+  // pairs, even stages through LDS buffer 0 and register set 0, odd ones through
+  // buffer 1 and set 1.
+  const int nk = K / kBgK;
   float4 ra0[LA], rb0[LB], ra1[LA], rb1[LB];
   load(ra0, rb0, 0);
   load(ra1, rb1, kBgK);
@@ -713,14 +715,15 @@ bool big_direct(int n, int np, std::initializer_list<const void*> ptrs) {
 // 128 divides NP, measured 10 % faster than 64 x 64 at 128 x 256^2; 64 x 64
 // otherwise (the backward's transposed products measured 15 % slower at 128 x 64).
 template <int MODE, bool SCALED, bool TX = false, bool TY = false>
-void big_gemm(const float* X, const float* Y, const float* E, const float* rowsum, float* D, int np, int64_t bh,
-              hipStream_t st) {
+void big_gemm(const float* X, const float* Y, const float* E, const float* rowsum, float* D, int np, int n,
+              int64_t bh, hipStream_t st) {
+  const int K = std::min(np, (n + 31) / 32 * 32);
   if (!TX && !TY && np % 128 == 0)
     hipLaunchKernelGGL((newton_big_gemm_kernel<128, 64, TX, TY, MODE, SCALED>),
-                       dim3(big_gemm_blocks(np, 128, 64, bh)), dim3(256), 0, st, X, Y, E, rowsum, D, np, (int)bh);
+                       dim3(big_gemm_blocks(np, 128, 64, bh)), dim3(256), 0, st, X, Y, E, rowsum, D, np, K, (int)bh);
   else
     hipLaunchKernelGGL((newton_big_gemm_kernel<64, 64, TX, TY, MODE, SCALED>),
-                       dim3(big_gemm_blocks(np, 64, 64, bh)), dim3(256), 0, st, X, Y, E, rowsum, D, np, (int)bh);
+                       dim3(big_gemm_blocks(np, 64, 64, bh)), dim3(256), 0, st, X, Y, E, rowsum, D, np, K, (int)bh);
 }
 
 template <typename T>
@@ -745,11 +748,11 @@ int big_fwd(const T* mat, T* out, int64_t bh, int n, int iters, float* ws, hipSt
   for (int it = 0; it < iters; ++it) {
     float* dst = (direct && it == iters - 1) ? reinterpret_cast<float*>(out) : Vb;
     if (it == 0) {  // V0 = alpha P:  T = alpha (P P),  V1 = alpha (2P - P T)
-      big_gemm<0, true>(P, P, nullptr, rs, Tm, np, bh, st);
-      big_gemm<1, true>(P, Tm, P, rs, dst, np, bh, st);
+      big_gemm<0, true>(P, P, nullptr, rs, Tm, np, n, bh, st);
+      big_gemm<1, true>(P, Tm, P, rs, dst, np, n, bh, st);
     } else {        // T = P V,  V' = 2V - V T
-      big_gemm<0, false>(P, Va, nullptr, nullptr, Tm, np, bh, st);
-      big_gemm<1, false>(Va, Tm, Va, nullptr, dst, np, bh, st);
+      big_gemm<0, false>(P, Va, nullptr, nullptr, Tm, np, n, bh, st);
+      big_gemm<1, false>(Va, Tm, Va, nullptr, dst, np, n, bh, st);
     }
     if ((s = check_launch("newton forward step"))) return s;
     std::swap(Va, Vb);
@@ -771,8 +774,8 @@ int big_bwd(const T* g, const T* inv, T* out, int64_t bh, int n, float* ws, hipS
   const bool apart = o + bytes <= v || v + bytes <= o;
   if (apart && big_direct<T>(n, np, {g, inv, out})) {  // S = V^T G,  out = -S V^T
     const float* Vf = reinterpret_cast<const float*>(inv);
-    big_gemm<0, false, true, false>(Vf, reinterpret_cast<const float*>(g), nullptr, nullptr, S, np, bh, st);
-    big_gemm<2, false, false, true>(S, Vf, nullptr, nullptr, reinterpret_cast<float*>(out), np, bh, st);
+    big_gemm<0, false, true, false>(Vf, reinterpret_cast<const float*>(g), nullptr, nullptr, S, np, n, bh, st);
+    big_gemm<2, false, false, true>(S, Vf, nullptr, nullptr, reinterpret_cast<float*>(out), np, n, bh, st);
     return check_launch("newton backward products");
   }
   float* Vf = ws;
@@ -780,8 +783,8 @@ int big_bwd(const T* g, const T* inv, T* out, int64_t bh, int n, float* ws, hipS
   dim3 pg(ceil_div(np * np, 256), (unsigned)bh);
   hipLaunchKernelGGL(newton_big_pack_kernel<T>, pg, dim3(256), 0, st, inv, Vf, n, np);
   hipLaunchKernelGGL(newton_big_pack_kernel<T>, pg, dim3(256), 0, st, g, Gf, n, np);
-  big_gemm<0, false, true, false>(Vf, Gf, nullptr, nullptr, S, np, bh, st);  // S = V^T G
-  big_gemm<2, false, false, true>(S, Vf, nullptr, nullptr, Gf, np, bh, st);  // -S V^T (into G's slot)
+  big_gemm<0, false, true, false>(Vf, Gf, nullptr, nullptr, S, np, n, bh, st);  // S = V^T G
+  big_gemm<2, false, false, true>(S, Vf, nullptr, nullptr, Gf, np, n, bh, st);  // -S V^T (into G's slot)
   int s = check_launch("newton backward products");
   if (s) return s;
   dim3 ug(ceil_div(n * n, 256), (unsigned)bh);
