@@ -1494,7 +1494,7 @@ BwdPlan plan_bwd(const Dims& d, bool dq, bool dkey, size_t accBytes, size_t gByt
   return p;
 }
 
-// Plan of the fp16 broadcast backward: 3 waves per SIMD resident (4 for M <= 16).
+// Plan of the register-resident-column backward: 3 waves per SIMD resident (4 for M <= 16).
 struct BcPlan {
   int W, nx, rowsPerWave, ncb;
   size_t lds, partialElems;
