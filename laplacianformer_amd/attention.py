@@ -28,8 +28,9 @@ import torch
 from .functional import laplace_kernel, newton_inverse, tall_mix, tall_product
 
 
-def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor:
-    """pool x pool average pooling of k [B,H,N,d] over its gh x gw token grid -> [B,H,M,d]."""
+def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """pool x pool average pooling of k [B,H,N,d] over its gh x gw token grid -> [B,H,M,d],
+    accumulated and returned in ``dtype`` (default: k's type) without a converted copy of k."""
     B, H, N, d = k.shape
     gh, gw = grid
     if gh * gw != N or gh % pool or gw % pool:
@@ -37,7 +38,7 @@ def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int) -> torch.Tensor
     # A mean over the two in-window axes of a view: its backward is a broadcast,
     # cheaper than avg_pool2d's on this channel-last layout.
     x = k.reshape(B, H, gh // pool, pool, gw // pool, pool, d)
-    return x.mean(dim=(3, 5)).reshape(B, H, -1, d)
+    return x.mean(dim=(3, 5), dtype=dtype).reshape(B, H, -1, d)
 
 
 def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid: tuple[int, int] | None = None,
@@ -53,7 +54,7 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
         side = math.isqrt(N)
         grid = (side, side)
     ct = torch.float64 if q.dtype == torch.float64 else torch.float32
-    km = landmarks(k.to(ct), grid, pool).to(in_dtype)
+    km = landmarks(k, grid, pool, dtype=ct).to(in_dtype)
     km_cm = km.transpose(-1, -2).contiguous()  # [B,H,d,M]: the reference's key layout
     s = 1.0 / math.sqrt(d)
     k_qm = laplace_kernel(q, km_cm, s)         # [B,H,N,M]
