@@ -86,3 +86,43 @@ def test_graphed_operators_match_eager(gpu):
         torch.cuda.synchronize()
         for i, (got, want) in enumerate(zip(outs, ref)):
             assert torch.equal(got, want), (rep, i)
+
+
+def test_operators_on_concurrent_streams(gpu):
+    """Two problems launched on two streams at once (each operator takes the calling
+    stream and a workspace of its own) give the same bits as one after the other."""
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    print("operators on two streams", flush=True)
+    probs = []
+    for i in range(2):
+        q = gen((8, 1, 3136, 64), 300 + i, "f16").to(gpu)
+        k = gen((8, 1, 64, 49), 310 + i, "f16").to(gpu)
+        go = gen((8, 1, 3136, 49), 320 + i, "f16").to(gpu)
+        A = (torch.rand(16, 1, 256, 256, generator=torch.Generator().manual_seed(330 + i)) / 256).to(gpu)
+        A = A + A.transpose(-1, -2) + torch.eye(256, device=gpu)
+        probs.append((q, k, go, A))
+
+    def run(p):
+        q, k, go, A = p
+        o = [torch.empty_like(go), torch.empty_like(q), torch.empty_like(k), torch.empty_like(A)]
+        L.LaplaceSubtraction_forward(q, k, o[0])
+        L.LaplaceSubtraction_backward(go, q, k, o[1], o[2])
+        L.NewtonInverse_forward(A, o[3], 16)
+        return o
+
+    ref = [run(p) for p in probs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    got = [None, None]
+    for rep in range(3):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                got[i] = run(probs[i])
+        torch.cuda.synchronize()
+        for i in range(2):
+            for j, (a, b) in enumerate(zip(got[i], ref[i])):
+                assert torch.equal(a, b), (rep, i, j)

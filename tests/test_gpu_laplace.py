@@ -273,3 +273,36 @@ def test_golden_config1(gpu):
     assert_l1_close(dq2, z["dq"], "f32", "fixture dq", np.broadcast_to(ga.sum(3, keepdims=True), dq2.shape))
     assert_l1_close(dk2, np.swapaxes(z["dk_mc"], -1, -2), "f32", "fixture dk",
                     np.broadcast_to(ga.sum(2, keepdims=True), dk2.shape))
+
+
+def test_laplace_beyond_2pow31_elements(gpu):
+    """Output and grad_output with more than 2^31 elements (fp16, N = 2^23 + 128, M = 256,
+    C = 8): 64-bit indexing everywhere. grad_output is zero except for sampled rows at the
+    start, middle and end, so grad_key depends on those rows only and every gradient is
+    checked exactly against the oracle; forward rows at the same places bit for bit."""
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    N, M, C = (1 << 23) + 128, 256, 8
+    assert N * M > 2 ** 31
+    print("laplace beyond 2^31 elements", flush=True)
+    q = gen((1, 1, N, C), 2031, "f16")
+    k = gen((1, 1, C, M), 2032, "f16")
+    rows = [0, 1, 63, N // 2, N // 2 + 5, N - 129, N - 2, N - 1]
+    gs = gen((1, 1, len(rows), M), 2033, "f16")
+    qd, kd = q.to(gpu), k.to(gpu)
+    gd = torch.zeros((1, 1, N, M), dtype=torch.float16, device=gpu)
+    gd[0, 0, rows] = gs[0, 0].to(gpu)
+    out = torch.empty((1, 1, N, M), dtype=torch.float16, device=gpu)
+    dq = torch.empty_like(qd)
+    dk = torch.empty_like(kd)
+    L.LaplaceSubtraction_forward(qd, kd, out)
+    L.LaplaceSubtraction_backward(gd, qd, kd, dq, dk)
+    torch.cuda.synchronize()
+    qs = q[:, :, rows]
+    assert_bitwise(out[:, :, rows], oracle.laplace_forward(qs, k, "f16"), "f16", "forward rows")
+    refs = l1_refs(qs, k, gs, "f16")
+    check_l1(out[:, :, rows], dq[:, :, rows], dk, refs, "f16", "sampled rows ")
+    zero_rows = torch.ones(N, dtype=torch.bool)
+    zero_rows[rows] = False
+    assert not dq[0, 0][zero_rows.to(gpu)].any(), "grad_query of rows with zero grad_output"
