@@ -934,7 +934,8 @@ laplace_bwd_bcast_kernel(const T* __restrict__ gout, const float* __restrict__ g
 }
 
 // ---------------------------------------------------------------------------
-// Backward for M = CB * 32 columns (CB <= 8), fp16 / bf16 / fp32.
+// Backward for 17 <= M <= 256 columns in CB = ceil(M / 32) blocks of 32, fp16 /
+// bf16 / fp32 (the last block zero-padded when M is not a multiple of 32).
 //
 // A workgroup is RG row groups of CB waves; wave (g, b) of a group takes the
 // 32 columns [32b, 32b + 32) of every row batch (RB rows) of its group, with
@@ -958,7 +959,10 @@ constexpr int kMbRB = 8;   // rows per batch
 template <typename T, int CB, bool DQ, bool DK>
 __global__ void __launch_bounds__(1024)
 laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, const T* __restrict__ key,
-                      T* __restrict__ dq, float* __restrict__ partial, int N, int C, int rowsPerWG) {
+                      T* __restrict__ dq, float* __restrict__ partial, int N, int C, int rowsPerWG, int Mt) {
+  // M = CB * 32 columns in registers and LDS; the tensors have Mt <= M columns (the
+  // last block is partial when Mt is not a multiple of 32: its columns from Mt on
+  // have zero grad and key, so they add nothing and are not stored).
   constexpr int MC = kMbMC, RB = kMbRB, M = CB * MC;
   constexpr int MP = MC;                       // LDS row pitch of a staged batch (floats)
   constexpr bool kF16 = std::is_same<T, f16s>::value;
@@ -989,7 +993,7 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
   float* qsm = gneg + RB;                                           // [RB][64] query values
 
   const T* qb = query + (size_t)bh * N * C;
-  const T* kb = key + (size_t)bh * C * M;
+  const T* kb = key + (size_t)bh * C * Mt;
 
   // Next batch of this group: this wave's 32 columns of RB rows (clamped to the
   // last valid row; rows past the batch are zeroed at staging) and RB query values.
@@ -1003,8 +1007,9 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
     for (int s = 0; s < NL; ++s) {
       const int w = lane + 64 * s;               // word of the batch block
       const int r = min(w / (MC / EPW), nr - 1), jw = w - (w / (MC / EPW)) * (MC / EPW);
-      const T* src = gout + ((size_t)bh * N + rb + r) * M + cbk * MC + jw * EPW;
-      gpre[s] = *reinterpret_cast<const uint32_t*>(src);
+      const int col = cbk * MC + jw * EPW;  // Mt is even for 16-bit types: a word is all in or all out
+      const T* src = gout + ((size_t)bh * N + rb + r) * Mt + min(col, Mt - EPW);
+      gpre[s] = col < Mt ? *reinterpret_cast<const uint32_t*>(src) : 0u;
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r) qpre[r] = qb[(size_t)min(rb + r, rb + nr - 1) * C + cq];
@@ -1017,7 +1022,7 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
   for (int t = threadIdx.x; t < 64 * M; t += blockDim.x) {
     const int cl = t / M, j = t - cl * M;
     const int cc = chb * 64 + cl;
-    const float v = cc < C ? to_acc(kb[(size_t)cc * M + j]) : 0.0f;
+    const float v = (cc < C && j < Mt) ? to_acc(kb[(size_t)cc * Mt + j]) : 0.0f;
     big[j * 64 + cl] = kF16 ? v * 16777216.0f : v;
   }
   __syncthreads();
@@ -1167,8 +1172,8 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
       }
       __syncthreads();
     }
-    float* out = partial + ((size_t)slice * nx + x) * 64 * M;
-    for (int tt = threadIdx.x; tt < 64 * M; tt += blockDim.x) out[tt] = red[tt];
+    float* out = partial + ((size_t)slice * nx + x) * 64 * Mt;
+    for (int tt = threadIdx.x; tt < 64 * Mt; tt += blockDim.x) out[tt] = red[tt];
   }
 }
 
@@ -1583,22 +1588,25 @@ int launch_bcast_bwd(int dtype, const void* g, const void* q, const void* k, voi
   return launch_bcast_bwd_t<f16s, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
 }
 
-// ---- backward for M = 32 * CB (fp16 / bf16 / fp32) ----
+// ---- backward for 17 <= M <= 256 in column blocks of 32 (fp16 / bf16 / fp32) ----
 struct MbPlan {
   int CB, RG, W, nx, ncb, rowsPerWG;
   size_t lds, partialElems;
 };
 
+// Any 17 <= M <= 256 (even for 16-bit types, so that every grad row starts on a
+// 4-byte word); a last column block of fewer than 32 columns is zero-padded.
 bool mb_bwd_ok(int dtype, const Dims& d, const void* g) {
   if (!(dtype == LFAMD_F16 || dtype == LFAMD_BF16 || dtype == LFAMD_F32)) return false;
-  if (d.M % kMbMC != 0 || d.M < kMbMC || d.M > 8 * kMbMC) return false;
+  if (d.M < 17 || d.M > 8 * kMbMC) return false;
+  if (dtype != LFAMD_F32 && d.M % 2 != 0) return false;
   return (reinterpret_cast<uintptr_t>(g) & 3) == 0;
 }
 
 MbPlan plan_mb(const Dims& d, bool dkey) {
   MbPlan p{};
   p.ncb = ceil_div((int)d.C, 64);
-  p.CB = (int)d.M / kMbMC;
+  p.CB = ceil_div((int)d.M, kMbMC);
   p.RG = std::max(1, 16 / p.CB);
   p.W = p.CB * p.RG;
   const int64_t slices = d.BH() * p.ncb;
@@ -1608,7 +1616,7 @@ MbPlan plan_mb(const Dims& d, bool dkey) {
   nx = std::min(nx, std::max(1, N / (kMbRB * p.RG)));
   p.rowsPerWG = round_up(ceil_div(N, nx), kMbRB);
   p.nx = ceil_div(N, p.rowsPerWG);
-  const size_t bigFloats = std::max<size_t>((size_t)d.M * 64, (size_t)2 * p.W * kMbRB * 64);
+  const size_t bigFloats = std::max<size_t>((size_t)p.CB * kMbMC * 64, (size_t)2 * p.W * kMbRB * 64);
   p.lds = (bigFloats + (size_t)p.W * (kMbRB * kMbMC + kMbRB + kMbRB * 64)) * 4;
   p.partialElems = dkey ? (size_t)slices * p.nx * 64 * (size_t)d.M : 0;
   return p;
@@ -1625,7 +1633,7 @@ int launch_mb_cb(const void* g, const void* q, const void* k, void* dq, void* dk
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
   hipLaunchKernelGGL(kern, grid, dim3(64 * p.W), p.lds, st, static_cast<const T*>(g), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)d.N, (int)d.C,
-                     p.rowsPerWG);
+                     p.rowsPerWG, (int)d.M);
   int s = check_launch("laplace backward");
   if (s || !DK) return s;
   dim3 rgrid(ceil_div(64 * (int)d.M, 256), p.ncb, (unsigned)d.BH());
@@ -1819,7 +1827,7 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
   // Any of the backward paths may run (which one also depends on pointer alignment).
   size_t bytes = plan_bwd(d, true, true, acc, dtype == LFAMD_F16 ? 2 : acc).partialElems * acc;
   if (dtype != LFAMD_F64) bytes = std::max(bytes, plan_bcast(d, true).partialElems * 4);
-  if (dtype != LFAMD_F64 && d.M % kMbMC == 0 && d.M <= 8 * kMbMC)
+  if (dtype != LFAMD_F64 && d.M >= 17 && d.M <= 8 * kMbMC)
     bytes = std::max(bytes, plan_mb(d, true).partialElems * 4);
   return bytes;
 }

@@ -79,7 +79,7 @@ def test_laplace_parity(gpu, shape, dt):
     assert torch.equal(dq.cpu(), dq2.cpu()), "grad_query differs between the separate and fused entry points"
 
 
-@pytest.mark.parametrize("M", [49, 64, 256])
+@pytest.mark.parametrize("M", [49, 64, 196, 256])
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 def test_laplace_integer_ties(gpu, dt, M):
     """Integer inputs: every sum is exact and ties (sgn(0) = 0) are frequent."""
