@@ -346,8 +346,8 @@ def main():
                                    "launches; fp32 vector peak)",
                          "achieved": bwd_tflops, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                          "frac": bwd_tflops / PEAK_FP32_TFLOPS,
-                         "traffic": _traffic("lfamd::laplace_bwd_bcast_kernel<49, true, true, 0>",
-                                             "lfamd::laplace_dk_reduce_cm_kernel"),
+                         "traffic": _traffic("lfamd::laplace_bwd_bcast_kernel<lfamd::f16s, 49, true, true, 0>",
+                                             "lfamd::laplace_dk_reduce_cm_kernel<lfamd::f16s>"),
                          "algorithmic_bytes": 2 * (B_ * N_ * M_ + 2 * B_ * N_ * C_ + 2 * B_ * C_ * M_),
                          "work": f"{L1_FLOPS_BWD} flop per (i,j,d) triple x {T} triples per launch"},
             "kernels": {
