@@ -1007,9 +1007,18 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
     for (int s = 0; s < NL; ++s) {
       const int w = lane + 64 * s;               // word of the batch block
       const int r = min(w / (MC / EPW), nr - 1), jw = w - (w / (MC / EPW)) * (MC / EPW);
-      const int col = cbk * MC + jw * EPW;  // Mt is even for 16-bit types: a word is all in or all out
-      const T* src = gout + ((size_t)bh * N + rb + r) * Mt + min(col, Mt - EPW);
-      gpre[s] = col < Mt ? *reinterpret_cast<const uint32_t*>(src) : 0u;
+      const int col = cbk * MC + jw * EPW;
+      const T* rowp = gout + ((size_t)bh * N + rb + r) * Mt;
+      if constexpr (EPW == 2) {
+        if (Mt & 1) {  // odd row length: rows do not start on 4-byte words, two 16-bit loads
+          const uint32_t lo = col < Mt ? rowp[min(col, Mt - 1)].bits : 0u;
+          const uint32_t hi = col + 1 < Mt ? rowp[min(col + 1, Mt - 1)].bits : 0u;
+          gpre[s] = lo | (hi << 16);
+          continue;
+        }
+      }
+      // Even row length (or fp32): a word is all in or all out of the row.
+      gpre[s] = col < Mt ? *reinterpret_cast<const uint32_t*>(rowp + min(col, Mt - EPW)) : 0u;
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r) qpre[r] = qb[(size_t)min(rb + r, rb + nr - 1) * C + cq];
@@ -1594,13 +1603,14 @@ struct MbPlan {
   size_t lds, partialElems;
 };
 
-// Any 17 <= M <= 256 (even for 16-bit types, so that every grad row starts on a
-// 4-byte word); a last column block of fewer than 32 columns is zero-padded.
+// Any 17 <= M <= 256; a last column block of fewer than 32 columns is
+// zero-padded. (16-bit grad rows of odd length are fetched element by element.)
 bool mb_bwd_ok(int dtype, const Dims& d, const void* g) {
   if (!(dtype == LFAMD_F16 || dtype == LFAMD_BF16 || dtype == LFAMD_F32)) return false;
   if (d.M < 17 || d.M > 8 * kMbMC) return false;
-  if (dtype != LFAMD_F32 && d.M % 2 != 0) return false;
-  return (reinterpret_cast<uintptr_t>(g) & 3) == 0;
+  // Word loads need 4-byte rows; odd 16-bit rows are read element by element.
+  const bool elementwise = dtype != LFAMD_F32 && d.M % 2 != 0;
+  return (reinterpret_cast<uintptr_t>(g) & (elementwise ? 1 : 3)) == 0;
 }
 
 MbPlan plan_mb(const Dims& d, bool dkey) {

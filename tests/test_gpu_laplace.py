@@ -31,6 +31,9 @@ SHAPES = [
     (2, 1, 131, 16, 80),
     (1, 1, 7, 49, 64),
     (1, 2, 1, 49, 128),
+    # Odd M beyond the register-resident set: column blocks with 16-bit rows of odd length.
+    (1, 2, 77, 81, 64),
+    (2, 1, 50, 225, 40),
 ]
 DTYPES = ["f32", "f16", "bf16", "f64"]
 
