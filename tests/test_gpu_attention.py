@@ -119,3 +119,12 @@ def test_attention_module(gpu):
     assert y.shape == x.shape and torch.isfinite(x.grad).all()
     with pytest.raises(ValueError):
         lf.LaplacianAttention(63, 2)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_attention_first_stage_grid(gpu, dtype):
+    """A first-stage grid: 56x56 tokens pooled 4x4 -> M = 196 landmarks (fused forward with
+    column groups, composed backward on the column-block kernel with a partial last block,
+    NewtonInverse on the batched-GEMM path at n = 196, library products for widths > 64)."""
+    print(f"attention 56x56 grid {dtype}", flush=True)
+    _run(gpu, 2, 1, (56, 56), 32, dtype, seed=70, iters=12)
