@@ -121,7 +121,7 @@ int lfamd_laplace_kernel_forward(int dtype, const void* query, const void* key, 
  * `kernel` is this op's forward output, `grad_kernel` its gradient, both fp32
  * [B,H,N,M]. Either of grad_query / grad_key may be NULL to skip it; grad_key
  * needs the workspace lfamd_laplace_backward_workspace_size reports. Fused path:
- * LFAMD_F16 with M in {16, 32, 49}; LFAMD_ERR_UNSUPPORTED elsewhere. No single
+ * LFAMD_F16 with 16 <= M <= 256; LFAMD_ERR_UNSUPPORTED elsewhere. No single
  * reference counterpart (replaces the composition around
  * laplace::LaplaceSubtraction_backward_{query,key}_cuda, reference src/wrapper.cpp:84-88). */
 int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const float* kernel,

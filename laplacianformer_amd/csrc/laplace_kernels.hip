@@ -956,17 +956,21 @@ laplace_bwd_bcast_kernel(const T* __restrict__ gout, const float* __restrict__ g
 constexpr int kMbMC = 32;  // columns per wave
 constexpr int kMbRB = 8;   // rows per batch
 
-template <typename T, int CB, bool DQ, bool DK>
+template <typename T, int CB, bool DQ, bool DK, int GSRC = kGradF16>
 __global__ void __launch_bounds__(1024)
 laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, const T* __restrict__ key,
-                      T* __restrict__ dq, float* __restrict__ partial, int N, int C, int rowsPerWG, int Mt) {
+                      T* __restrict__ dq, float* __restrict__ partial, int N, int C, int rowsPerWG, int Mt,
+                      const float* __restrict__ gkern, const float* __restrict__ kern, float gscale) {
   // M = CB * 32 columns in registers and LDS; the tensors have Mt <= M columns (the
   // last block is partial when Mt is not a multiple of 32: its columns from Mt on
   // have zero grad and key, so they add nothing and are not stored).
   constexpr int MC = kMbMC, RB = kMbRB, M = CB * MC;
   constexpr int MP = MC;                       // LDS row pitch of a staged batch (floats)
   constexpr bool kF16 = std::is_same<T, f16s>::value;
-  constexpr int EPW = 4 / (int)sizeof(T) > 0 ? 4 / (int)sizeof(T) : 1;  // elements per 32-bit word
+  // Grad elements per fetched 32-bit word: 2 for 16-bit grads, 1 for fp32 grads and
+  // for the kernel-gradient source (fp32 gK and K, g = -s * gK * K formed at staging).
+  static_assert(GSRC == kGradF16 || std::is_same<T, f16s>::value, "kernel-gradient source: fp16 only");
+  constexpr int EPW = GSRC == kGradKernel ? 1 : (4 / (int)sizeof(T) > 0 ? 4 / (int)sizeof(T) : 1);
   constexpr int GW = RB * MC / EPW;            // grad words of a batch (this wave's columns)
   constexpr int NL = (GW + 63) / 64;           // words per lane
   static_assert(GW % 64 == 0, "whole words per lane");
@@ -998,6 +1002,8 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
   // Next batch of this group: this wave's 32 columns of RB rows (clamped to the
   // last valid row; rows past the batch are zeroed at staging) and RB query values.
   uint32_t gpre[NL];
+  float kpre[GSRC == kGradKernel ? NL : 1];
+  const float gscale2 = -2.0f * gscale;  // 2 * (-s * gK) * K == (-2s * gK) * K exactly
   T qpre[RB];
   int fnr = 0;
   auto fetch = [&](int t) {
@@ -1008,6 +1014,12 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
       const int w = lane + 64 * s;               // word of the batch block
       const int r = min(w / (MC / EPW), nr - 1), jw = w - (w / (MC / EPW)) * (MC / EPW);
       const int col = cbk * MC + jw * EPW;
+      if constexpr (GSRC == kGradKernel) {
+        const size_t o = ((size_t)bh * N + rb + r) * Mt + min(col, Mt - 1);
+        gpre[s] = col < Mt ? __builtin_bit_cast(uint32_t, gkern[o]) : 0u;
+        kpre[s] = col < Mt ? kern[o] : 0.0f;
+        continue;
+      }
       const T* rowp = gout + ((size_t)bh * N + rb + r) * Mt;
       if constexpr (EPW == 2) {
         if (Mt & 1) {  // odd row length: rows do not start on 4-byte words, two 16-bit loads
@@ -1067,6 +1079,8 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
                                : __builtin_bit_cast(float, gpre[s] & 0xffff0000u);
           gsm[r * MP + 2 * jw] = ok ? 2.0f * lo : 0.0f;
           gsm[r * MP + 2 * jw + 1] = ok ? 2.0f * hi : 0.0f;
+        } else if constexpr (GSRC == kGradKernel) {
+          gsm[r * MP + jw] = ok ? (gscale2 * __builtin_bit_cast(float, gpre[s])) * kpre[s] : 0.0f;
         } else {
           gsm[r * MP + jw] = ok ? 2.0f * __builtin_bit_cast(float, gpre[s]) : 0.0f;
         }
@@ -1632,10 +1646,10 @@ MbPlan plan_mb(const Dims& d, bool dkey) {
   return p;
 }
 
-template <typename T, int CB, bool DQ, bool DK>
+template <typename T, int CB, bool DQ, bool DK, int GSRC = kGradF16>
 int launch_mb_cb(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                 const MbPlan& p, hipStream_t st) {
-  auto kern = laplace_bwd_mb_kernel<T, CB, DQ, DK>;
+                 const MbPlan& p, hipStream_t st, KernGrad kg = {}) {
+  auto kern = laplace_bwd_mb_kernel<T, CB, DQ, DK, GSRC>;
   if (p.lds > 65536 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)p.lds) != hipSuccess)
@@ -1643,7 +1657,7 @@ int launch_mb_cb(const void* g, const void* q, const void* k, void* dq, void* dk
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
   hipLaunchKernelGGL(kern, grid, dim3(64 * p.W), p.lds, st, static_cast<const T*>(g), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)d.N, (int)d.C,
-                     p.rowsPerWG, (int)d.M);
+                     p.rowsPerWG, (int)d.M, kg.gk, kg.kv, kg.scale);
   int s = check_launch("laplace backward");
   if (s || !DK) return s;
   dim3 rgrid(ceil_div(64 * (int)d.M, 256), p.ncb, (unsigned)d.BH());
@@ -1652,18 +1666,18 @@ int launch_mb_cb(const void* g, const void* q, const void* k, void* dq, void* dk
   return check_launch("laplace backward_key reduction");
 }
 
-template <typename T, bool DQ, bool DK>
+template <typename T, bool DQ, bool DK, int GSRC = kGradF16>
 int launch_mb_t(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
-                const MbPlan& p, hipStream_t st) {
+                const MbPlan& p, hipStream_t st, KernGrad kg = {}) {
   switch (p.CB) {
-    case 1: return launch_mb_cb<T, 1, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 2: return launch_mb_cb<T, 2, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 3: return launch_mb_cb<T, 3, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 4: return launch_mb_cb<T, 4, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 5: return launch_mb_cb<T, 5, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 6: return launch_mb_cb<T, 6, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    case 7: return launch_mb_cb<T, 7, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
-    default: return launch_mb_cb<T, 8, DQ, DK>(g, q, k, dq, dk, ws, d, p, st);
+    case 1: return launch_mb_cb<T, 1, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 2: return launch_mb_cb<T, 2, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 3: return launch_mb_cb<T, 3, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 4: return launch_mb_cb<T, 4, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 5: return launch_mb_cb<T, 5, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 6: return launch_mb_cb<T, 6, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    case 7: return launch_mb_cb<T, 7, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
+    default: return launch_mb_cb<T, 8, DQ, DK, GSRC>(g, q, k, dq, dk, ws, d, p, st, kg);
   }
 }
 
@@ -1677,11 +1691,12 @@ int launch_mb(int dtype, const void* g, const void* q, const void* k, void* dq, 
   }
 }
 
-// The fused kernel-gradient backward runs on the fp16 broadcast path only.
-// M = 64 is left to the composed path: with 64 key columns and their sums in
-// registers this kernel spills (94 us against 87 us composed at B=32 N=3136).
+// The fused kernel-gradient backward (fp16): M in {16, 32, 49} on the
+// register-resident-column kernel, any other 17 <= M <= 256 on the column-block
+// kernel (the former spills at M = 64: 94 us there against 87 us composed).
+bool kernel_bwd_bcast(const Dims& d) { return d.M == 16 || d.M == 32 || d.M == 49; }
 bool kernel_bwd_ok(int dtype, const Dims& d) {
-  return dtype == LFAMD_F16 && (d.M == 16 || d.M == 32 || d.M == 49);
+  return dtype == LFAMD_F16 && (kernel_bwd_bcast(d) || (d.M >= 17 && d.M <= 8 * kMbMC));
 }
 
 template <typename T, int JB, bool DQ, bool DK>
@@ -1899,11 +1914,22 @@ int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const flo
                 (long long)d.N, (long long)d.M);
   if (!grad_kernel || !kernel || !query || !key) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const KernGrad kg{grad_kernel, kernel, scale};
+  if (!kernel_bwd_bcast(d)) {
+    const MbPlan mp = plan_mb(d, doDk);
+    if (doDk && (!workspace || workspace_bytes < mp.partialElems * 4))
+      return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, mp.partialElems * 4,
+                  workspace_bytes);
+    if (doDq && doDk)
+      return launch_mb_t<f16s, true, true, kGradKernel>(nullptr, query, key, grad_query, grad_key, workspace, d, mp, st, kg);
+    if (doDq)
+      return launch_mb_t<f16s, true, false, kGradKernel>(nullptr, query, key, grad_query, nullptr, workspace, d, mp, st, kg);
+    return launch_mb_t<f16s, false, true, kGradKernel>(nullptr, query, key, nullptr, grad_key, workspace, d, mp, st, kg);
+  }
   const BcPlan sp = plan_bcast(d, doDk);
   if (doDk && (!workspace || workspace_bytes < sp.partialElems * 4))
     return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, sp.partialElems * 4,
                 workspace_bytes);
-  const KernGrad kg{grad_kernel, kernel, scale};
   if (doDq && doDk)
     return launch_bcast_bwd<true, true, kGradKernel>(LFAMD_F16, nullptr, query, key, grad_query, grad_key, workspace, d, sp, st, kg);
   if (doDq)

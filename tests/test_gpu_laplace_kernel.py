@@ -26,7 +26,8 @@ FWD_SHAPES = [
     (1, 1, 129, 256, 64),   # fp32 output tiles of all 256 columns exceed the LDS: two column groups
     (2, 1, 70, 240, 64),    # column groups of 128 and 112
 ]
-# Fused-backward shapes: fp16, M in {16, 32, 49}; odd N * M and single rows included.
+# Fused-backward shapes: fp16, M in {16, 32, 49} (register-resident columns) and other
+# 17 <= M <= 256 (column blocks, partial last block included); odd N * M and single rows.
 BWD_SHAPES = [
     (2, 2, 196, 49, 32),
     (1, 1, 1, 49, 64),
@@ -35,6 +36,9 @@ BWD_SHAPES = [
     (2, 1, 200, 32, 64),
     (1, 1, 97, 32, 130),
     (2, 1, 3136, 49, 64),
+    (1, 2, 150, 64, 64),
+    (1, 1, 77, 81, 40),
+    (2, 1, 130, 196, 64),
 ]
 
 
@@ -115,14 +119,10 @@ def test_kernel_unsupported_reports_false(gpu):
     dq = torch.full_like(q2, 7.0)
     assert L.LaplaceKernel_backward(kern, kern, q2, k2, dq, None, 0.5) is False  # fp32: no fused backward
     assert bool((dq == 7.0).all())
-    q3 = gen((1, 1, 10, 16), 5, "f16").to(gpu)
-    k3 = gen((1, 1, 16, 50), 6, "f16").to(gpu)  # M = 50
-    kern3 = torch.rand((1, 1, 10, 50), device=gpu)
-    assert L.LaplaceKernel_backward(kern3, kern3, q3, k3, torch.empty_like(q3), None, 0.5) is False
-    # M = 64: the composed path (the register-resident kernel would spill).
+    # M = 8: below both fused backward paths.
     q5 = gen((1, 1, 10, 16), 9, "f16").to(gpu)
-    k5 = gen((1, 1, 16, 64), 10, "f16").to(gpu)
-    kern5 = torch.rand((1, 1, 10, 64), device=gpu)
+    k5 = gen((1, 1, 16, 8), 10, "f16").to(gpu)
+    kern5 = torch.rand((1, 1, 10, 8), device=gpu)
     assert L.LaplaceKernel_backward(kern5, kern5, q5, k5, torch.empty_like(q5), None, 0.5) is False
     # M = 257: beyond the broadcast forward's 256 columns.
     q4 = gen((1, 1, 129, 64), 7, "f16").to(gpu)
