@@ -85,7 +85,9 @@ def test_argument_errors_without_device(lib):
     assert lib.lfamd_laplace_kernel_forward(1, null, null, null, 0, 1, 4, 49, 64, 0.5, null) == 0  # empty
     kb = lib.lfamd_laplace_kernel_backward
     assert kb(0, null, null, null, null, dummy, null, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 3  # fp32
-    assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 50, 64, 0.5, null, 0, null) == 3  # M = 50
+    assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 8, 64, 0.5, null, 0, null) == 3  # M = 8
+    assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 257, 64, 0.5, null, 0, null) == 3  # M = 257
+    assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 50, 64, 0.5, null, 0, null) == 1  # M = 50: null
     assert kb(1, null, null, null, null, dummy, null, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 1  # null
     assert kb(1, null, null, null, null, null, dummy, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 1  # ws
     assert b"workspace" in lib.lfamd_last_error() or b"null" in lib.lfamd_last_error()
