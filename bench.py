@@ -140,8 +140,27 @@ def bench_newton(args, dev):
     flops_bwd = nm * 4 * n ** 3
     P = A.double() + 0.01 * torch.eye(n, device=dev, dtype=torch.float64)
     resid = torch.linalg.matrix_norm(P @ V.double() - torch.eye(n, device=dev, dtype=torch.float64)).mean().item()
+    # The same op at the configuration-1 (ViT stage 1) landmark shape: B*H = 32 Gram matrices
+    # exp(-L1(k, k) / sqrt(d)) + 1e-3 I of 49 landmarks, d = 64, 10 iterations. One workgroup per
+    # matrix occupies 32 of the chip's CUs, so the whole-chip MFMA fraction is bounded by 32/CUs;
+    # the per-occupied-CU fraction is reported beside it.
+    nm1, n1, it1 = 32, 49, 10
+    k1 = gen((nm1, 1, n1, 64), 1021, torch.float32).to(dev)
+    d1 = torch.empty((nm1, 1, n1, n1), device=dev)
+    L.LaplaceSubtraction_forward(k1, k1.transpose(-1, -2).contiguous(), d1)
+    A1 = (torch.exp(-d1 / 8.0) + 1e-3 * torch.eye(n1, device=dev)).contiguous()
+    G1 = gen((nm1, 1, n1, n1), 1031, torch.float32).to(dev)
+    V1 = torch.empty_like(A1)
+    dA1 = torch.empty_like(A1)
+    wall1, (t1_fwd, t1_bwd) = time_steps([lambda: L.NewtonInverse_forward(A1, V1, it1),
+                                          lambda: L.NewtonInverse_backward(G1, V1, dA1)], args.steps, args.warmup)
+    P1 = A1.double() + 0.01 * torch.eye(n1, device=dev, dtype=torch.float64)
+    resid1 = torch.linalg.matrix_norm(P1 @ V1.double() - torch.eye(n1, device=dev, dtype=torch.float64)).mean().item()
+    stage1 = {"wall_ms": wall1, "fwd_ms": t1_fwd, "bwd_ms": t1_bwd, "flops_fwd": nm1 * it1 * 4 * n1 ** 3,
+              "flops_bwd": nm1 * 4 * n1 ** 3, "n_mats": nm1, "n": n1, "iters": it1, "residual_fro_mean": resid1}
     return {"wall_ms": wall, "fwd_ms": t_fwd, "bwd_ms": t_bwd, "flops_fwd": flops_fwd, "flops_bwd": flops_bwd,
-            "residual_fro_mean": resid, "A": A.cpu(), "G": G.cpu(), "n_mats": nm, "n": n, "iters": iters}
+            "residual_fro_mean": resid, "A": A.cpu(), "G": G.cpu(), "n_mats": nm, "n": n, "iters": iters,
+            "stage1": stage1}
 
 
 def bench_layer(args, dev):
@@ -371,6 +390,18 @@ def main():
             "fwd": {"ms": ns["fwd_ms"], "tflops": tf_f, "frac": tf_f / PEAK_FP32_TFLOPS},
             "bwd": {"ms": ns["bwd_ms"], "tflops": tf_b, "frac": tf_b / PEAK_FP32_TFLOPS},
             "residual_fro_mean": ns["residual_fro_mean"],
+        }
+        s1 = ns["stage1"]
+        tf1 = (s1["flops_fwd"] + s1["flops_bwd"]) / (s1["wall_ms"] * 1e-3) / 1e12
+        cus = props.multi_processor_count
+        line["newton"]["stage1"] = {
+            "workload": "BASELINE config 1 landmark shape: NewtonInverse fwd (10 it) + bwd, 32 x 49x49 fp32 "
+                        "(one workgroup per matrix: 32 CUs occupied)",
+            "ms_per_step": s1["wall_ms"], "fwd_ms": s1["fwd_ms"], "bwd_ms": s1["bwd_ms"], "tflops": tf1,
+            "frac_fp32_mfma_peak": tf1 / PEAK_FP32_TFLOPS,
+            "frac_per_occupied_cu": tf1 / (PEAK_FP32_TFLOPS * s1["n_mats"] / cus),
+            "flops": "4 n^3 per iteration + 4 n^3 backward, n = 49 (algorithmic; the kernels pad to 64)",
+            "residual_fro_mean": s1["residual_fro_mean"],
         }
         if not lap:
             line.update({"value": tf, "unit": "TFLOP/s", "ms_per_step": ns["wall_ms"],
