@@ -246,6 +246,78 @@ enum FwdEpi { kEpiDist = 0, kEpiExp = 1 };
 template <typename T, int EPI> struct FwdOut { using type = T; };
 template <typename T> struct FwdOut<T, kEpiExp> { using type = float; };
 
+// Channel sums of the broadcast forward for the first RR of a lane's R row sets
+// (RR = 1 for a block of at most 64 rows: the second set would be idle lanes that
+// still cost every instruction). acc[r][j] accumulates |q - k| over c ascending.
+template <typename T, int JB, int R, int RR>
+__device__ __forceinline__ void fb_sums(float (&acc)[R][JB], const uint4* qsm, const float* ksm, int rows,
+                                        int wave, int lane, int KP, int QP, int C) {
+  constexpr int JBS = fb_pitch(JB);
+  constexpr int NG = JBS / 4;
+  constexpr int EV = 16 / (int)sizeof(T);
+  constexpr int NVC = kFbKC / EV;
+  // Rows past the block's end read row 0 of the tile (their results are not stored).
+  const uint4* qrow[RR];
+#pragma unroll
+  for (int r = 0; r < RR; ++r) qrow[r] = qsm + (r * 64 + lane < rows ? r * 64 + lane : 0) * QP;
+  const float4* kw = reinterpret_cast<const float4*>(ksm + wave * JBS);
+  const int KP4 = KP / 4;
+  const int nChunks = C / kFbKC;
+  // Key values one channel ahead and query vectors one chunk ahead of the
+  // arithmetic; a compiler memory barrier per channel keeps it from hoisting a
+  // whole chunk's reads (registers).
+  uint4 qv[RR][NVC];
+#pragma unroll
+  for (int r = 0; r < RR; ++r)
+#pragma unroll
+    for (int v = 0; v < NVC; ++v) qv[r][v] = qrow[r][v];
+  float4 kcur[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) kcur[g] = kw[g];
+  for (int kc = 0; kc < nChunks; ++kc) {
+    uint4 qn[RR][NVC];
+    const int kn = min(kc + 1, nChunks - 1);
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int v = 0; v < NVC; ++v) qn[r][v] = qrow[r][kn * NVC + v];
+#pragma unroll
+    for (int cc = 0; cc < kFbKC; ++cc) {
+      const int cnext = min(kc * kFbKC + cc + 1, C - 1);
+      float4 knext[NG];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        knext[g] = kw[cnext * KP4 + g];
+        // Use the padding lane too, so the read stays one ds_read_b128 (a
+        // narrower split, e.g. b96 + b32, costs more LDS cycles than b128).
+        asm volatile("" ::"v"(knext[g].w));
+      }
+      float qf[RR];
+#pragma unroll
+      for (int r = 0; r < RR; ++r) qf[r] = elem_f32<T>(qv[r][cc / EV], cc % EV);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float k4[4] = {kcur[g].x, kcur[g].y, kcur[g].z, kcur[g].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (g * 4 + t < JB) {
+#pragma unroll
+            for (int r = 0; r < RR; ++r) acc[r][g * 4 + t] += fabsf(qf[r] - k4[t]);
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < NG; ++g) kcur[g] = knext[g];
+      asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int v = 0; v < NVC; ++v) qv[r][v] = qn[r][v];
+  }
+
+}
+
 template <typename T, int JB, int R, int EPI = kEpiDist>
 __global__ void __launch_bounds__(1024)
 laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
@@ -315,65 +387,10 @@ laplace_fwd_bcast_kernel(const T* __restrict__ query, const T* __restrict__ key,
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < JB; ++j) acc[r][j] = 0.0f;
-  // Rows past the block's end read row 0 of the tile (their results are not stored).
-  const uint4* qrow[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) qrow[r] = qsm + (r * 64 + lane < rows ? r * 64 + lane : 0) * QP;
-  const float4* kw = reinterpret_cast<const float4*>(ksm + wave * JBS);
-  const int KP4 = KP / 4;
-  const int nChunks = C / kFbKC;
-  // Key values one channel ahead and query vectors one chunk ahead of the
-  // arithmetic; a compiler memory barrier per channel keeps it from hoisting a
-  // whole chunk's reads (registers).
-  uint4 qv[R][NVC];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int v = 0; v < NVC; ++v) qv[r][v] = qrow[r][v];
-  float4 kcur[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) kcur[g] = kw[g];
-  for (int kc = 0; kc < nChunks; ++kc) {
-    uint4 qn[R][NVC];
-    const int kn = min(kc + 1, nChunks - 1);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int v = 0; v < NVC; ++v) qn[r][v] = qrow[r][kn * NVC + v];
-#pragma unroll
-    for (int cc = 0; cc < kFbKC; ++cc) {
-      const int cnext = min(kc * kFbKC + cc + 1, C - 1);
-      float4 knext[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        knext[g] = kw[cnext * KP4 + g];
-        // Use the padding lane too, so the read stays one ds_read_b128 (a
-        // narrower split, e.g. b96 + b32, costs more LDS cycles than b128).
-        asm volatile("" ::"v"(knext[g].w));
-      }
-      float qf[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) qf[r] = elem_f32<T>(qv[r][cc / EV], cc % EV);
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const float k4[4] = {kcur[g].x, kcur[g].y, kcur[g].z, kcur[g].w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (g * 4 + t < JB) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r][g * 4 + t] += fabsf(qf[r] - k4[t]);
-          }
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < NG; ++g) kcur[g] = knext[g];
-      asm volatile("" ::: "memory");
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int v = 0; v < NVC; ++v) qv[r][v] = qn[r][v];
-  }
+  if (R > 1 && rows <= 64)
+    fb_sums<T, JB, R, 1>(acc, qsm, ksm, rows, wave, lane, KP, QP, C);
+  else
+    fb_sums<T, JB, R, R>(acc, qsm, ksm, rows, wave, lane, KP, QP, C);
 
   __syncthreads();  // every wave is done with the query tile, which becomes the output tile
 #pragma unroll
