@@ -41,6 +41,27 @@ def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int, dtype: torch.dt
     return x.mean(dim=(3, 5), dtype=dtype).reshape(B, H, -1, d)
 
 
+class _PooledLandmarks(torch.autograd.Function):
+    """landmarks(k, grid, pool, acc) rounded to k's type, with a backward that forms
+    grad_k = (grad_km / pool^2) broadcast over each pool x pool patch in k's type in
+    one copy (autograd's mean backward would expand in the accumulation type, divide,
+    then cast: two passes over an fp32 [B,H,N,d] tensor). Same values: the
+    division is done in the accumulation type and rounded once to k's type."""
+
+    @staticmethod
+    def forward(ctx, k: torch.Tensor, grid: tuple[int, int], pool: int, acc: torch.dtype) -> torch.Tensor:
+        ctx.shape, ctx.grid, ctx.pool, ctx.acc = k.shape, grid, pool, acc
+        return landmarks(k, grid, pool, dtype=acc).to(k.dtype)
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        B, H, N, d = ctx.shape
+        gh, gw = ctx.grid
+        p = ctx.pool
+        gs = (g.to(ctx.acc) / (p * p)).to(g.dtype).reshape(B, H, gh // p, 1, gw // p, 1, d)
+        return gs.expand(B, H, gh // p, p, gw // p, p, d).reshape(B, H, N, d), None, None, None
+
+
 def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid: tuple[int, int] | None = None,
                         pool: int = 4, iters: int = 10) -> torch.Tensor:
     """LaplacianFormer attention of q, k, v [B,H,N,d] (autograd through the HIP ops).
@@ -54,7 +75,7 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
         side = math.isqrt(N)
         grid = (side, side)
     ct = torch.float64 if q.dtype == torch.float64 else torch.float32
-    km = landmarks(k, grid, pool, dtype=ct).to(in_dtype)
+    km = _PooledLandmarks.apply(k, grid, pool, ct)
     km_cm = km.transpose(-1, -2).contiguous()  # [B,H,d,M]: the reference's key layout
     s = 1.0 / math.sqrt(d)
     k_qm = laplace_kernel(q, km_cm, s)         # [B,H,N,M]
