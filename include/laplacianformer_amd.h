@@ -166,14 +166,15 @@ int lfamd_newton_is_supported(int64_t n);
 /* ---- Attention-layer products ------------------------------------------- */
 
 /* c[s][n][q] = sum_{p < inner} a[s][n][p] * b[s*b_slice_stride + q*b_col_stride + p*b_inner_stride]
- * for s < slices, n < rows, q < cols; fp32 arithmetic and output, `a` of element type `dtype`
- * (F32, F16 or BF16), a and c contiguous [slices][rows][inner] / [slices][rows][cols], b fp32
+ * for s < slices, n < rows, q < cols; fp32 arithmetic, `a` of element type `dtype` and c of
+ * element type `c_dtype` (each F32, F16 or BF16; c is the fp32 sum rounded once),
+ * a and c contiguous [slices][rows][inner] / [slices][rows][cols], b fp32
  * addressed through the element strides (W and W^T are both read in place). inner, cols <= 64;
  * LFAMD_ERR_UNSUPPORTED beyond. No reference counterpart: these are the LaplacianFormer
  * attention layer's products around the two operators (K_qm.W, grad.W^T, V.grad_kv^T,
  * K_km.grad_kv), which the reference leaves to its caller. */
-int lfamd_mix_rows(int dtype, const void* a, const float* b, float* c, int64_t slices, int64_t rows,
-                   int inner, int cols, int64_t b_col_stride, int64_t b_inner_stride,
+int lfamd_mix_rows(int dtype, const void* a, const float* b, int c_dtype, void* c, int64_t slices,
+                   int64_t rows, int inner, int cols, int64_t b_col_stride, int64_t b_inner_stride,
                    int64_t b_slice_stride, void* stream);
 
 /* ---- Runtime ------------------------------------------------------------ */

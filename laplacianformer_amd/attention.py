@@ -83,7 +83,7 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
     k_km = laplace_kernel(k, km_cm, s)         # [B,H,N,M] = K_mk^T
     inv = newton_inverse(k_mm, iters)          # [B,H,M,M]
     kv = tall_product(k_km, v)                 # [B,H,M,d] = K_km^T V
-    out = tall_mix(k_qm, torch.matmul(inv, kv))  # [B,H,N,d]
+    out = tall_mix(k_qm, torch.matmul(inv, kv), in_dtype)  # [B,H,N,d]
     return out.to(in_dtype)
 
 

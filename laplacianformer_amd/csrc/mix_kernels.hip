@@ -11,7 +11,8 @@
 // these products are HBM-bound (A in, C out: ~45 MB per product at config 5).
 // Each A value feeds Q multiply-adds, so a VALU kernel would read it from LDS
 // once per wave-wide FMA and be LDS-bound; the matrix cores take 4 k-steps of a
-// 16 x 16 tile per 16-byte operand read instead. A workgroup (4 waves) takes
+// 16 x 16 tile per 16-byte operand read instead. C is written in fp32, fp16 or
+// bf16 (one rounding of the fp32 sum). A workgroup (4 waves) takes
 // 64-row tiles of A in turn (the next tile's loads in flight during the current
 // one's products): A rows and B staged in LDS (pitch 68 floats), wave w computes
 // rows [16w, 16w + 16) x all Q columns as four 16 x 16 v_mfma_f32_16x16x4_f32
@@ -32,9 +33,9 @@ constexpr int kMixPMax = 64;   // largest inner / output width
 constexpr int kMixRows = 64;   // rows of A per workgroup
 constexpr int kMixLS = 68;     // LDS pitch (floats): lane-varying 16-byte reads without conflicts
 
-template <typename TA>
+template <typename TA, typename TC>
 __global__ void __launch_bounds__(256)
-mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int N, int P,
+mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __restrict__ C, int N, int P,
                 int Q, int64_t sq, int64_t sp, int64_t bStride) {
   __shared__ __align__(16) float Bs[kMixPMax * kMixLS];  // Bs[q][p], zero outside Q x P
   __shared__ __align__(16) float As[kMixRows * kMixLS];  // As[r][p], zero outside the rows and P
@@ -110,13 +111,13 @@ mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, float* __
           acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], bq[c][kb][st], acc[c], 0, 0, 0);
     }
     const int n0 = t * kMixRows, rows = min(kMixRows, N - n0);
-    float* Cm = C + ((size_t)s * N + n0) * Q;
+    TC* Cm = C + ((size_t)s * N + n0) * Q;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * wave + 4 * lg + r, col = 16 * c + li;
-        if (row < rows && col < Q) Cm[(size_t)row * Q + col] = acc[c][r];
+        if (row < rows && col < Q) Cm[(size_t)row * Q + col] = from_acc<TC>(acc[c][r]);
       }
     __syncthreads();  // every wave's reads of this tile are done before the next is stored
   }
@@ -124,14 +125,14 @@ mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, float* __
 
 // Workgroups per slice: about two per CU over the whole grid (each loops over its
 // share of the slice's 64-row tiles; measured best of 1, 2, 4 and 16 per CU).
-template <typename TA>
-int launch_mix(const void* A, const float* B, float* C, int64_t slices, int64_t N, int P, int Q, int64_t sq,
+template <typename TA, typename TC>
+int launch_mix(const void* A, const float* B, void* C, int64_t slices, int64_t N, int P, int Q, int64_t sq,
                int64_t sp, int64_t bStride, hipStream_t st) {
   const int64_t tiles = (N + kMixRows - 1) / kMixRows;
   const int64_t per = std::max<int64_t>(1, std::min<int64_t>(tiles, (2 * (int64_t)num_cus() + slices - 1) / slices));
   dim3 grid((unsigned)per, (unsigned)slices);
-  hipLaunchKernelGGL(mix_rows_kernel<TA>, grid, dim3(256), 0, st, static_cast<const TA*>(A), B, C, (int)N, P, Q,
-                     sq, sp, bStride);
+  hipLaunchKernelGGL((mix_rows_kernel<TA, TC>), grid, dim3(256), 0, st, static_cast<const TA*>(A), B,
+                     static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
   return check_launch("mix rows");
 }
 
@@ -139,11 +140,23 @@ int launch_mix(const void* A, const float* B, float* C, int64_t slices, int64_t 
 
 using namespace lfamd;
 
-extern "C" int lfamd_mix_rows(int dtype, const void* a, const float* b, float* c, int64_t slices, int64_t rows,
-                              int inner, int cols, int64_t b_col_stride, int64_t b_inner_stride,
+template <typename TA>
+int launch_mix_c(int c_dtype, const void* a, const float* b, void* c, int64_t slices, int64_t rows, int inner,
+                 int cols, int64_t sq, int64_t sp, int64_t bStride, hipStream_t st) {
+  switch (c_dtype) {
+    case LFAMD_F32: return launch_mix<TA, float>(a, b, c, slices, rows, inner, cols, sq, sp, bStride, st);
+    case LFAMD_F16: return launch_mix<TA, f16s>(a, b, c, slices, rows, inner, cols, sq, sp, bStride, st);
+    default: return launch_mix<TA, bf16s>(a, b, c, slices, rows, inner, cols, sq, sp, bStride, st);
+  }
+}
+
+extern "C" int lfamd_mix_rows(int dtype, const void* a, const float* b, int c_dtype, void* c, int64_t slices,
+                              int64_t rows, int inner, int cols, int64_t b_col_stride, int64_t b_inner_stride,
                               int64_t b_slice_stride, void* stream) {
   if (dtype != LFAMD_F32 && dtype != LFAMD_F16 && dtype != LFAMD_BF16)
     return fail(LFAMD_ERR_DTYPE, "mix rows: unsupported dtype %d", dtype);
+  if (c_dtype != LFAMD_F32 && c_dtype != LFAMD_F16 && c_dtype != LFAMD_BF16)
+    return fail(LFAMD_ERR_DTYPE, "mix rows: unsupported output dtype %d", c_dtype);
   if (slices < 0 || rows < 0 || inner < 1 || cols < 1 || slices > 65535 || rows > (int64_t)1 << 30)
     return fail(LFAMD_ERR_ARG, "mix rows: bad sizes (slices=%lld rows=%lld inner=%d cols=%d)", (long long)slices,
                 (long long)rows, inner, cols);
@@ -153,8 +166,8 @@ extern "C" int lfamd_mix_rows(int dtype, const void* a, const float* b, float* c
   if (!a || !b || !c) return fail(LFAMD_ERR_ARG, "mix rows: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case LFAMD_F32: return launch_mix<float>(a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
-    case LFAMD_F16: return launch_mix<f16s>(a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
-    default: return launch_mix<bf16s>(a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
+    case LFAMD_F32: return launch_mix_c<float>(c_dtype, a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
+    case LFAMD_F16: return launch_mix_c<f16s>(c_dtype, a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
+    default: return launch_mix_c<bf16s>(c_dtype, a, b, c, slices, rows, inner, cols, b_col_stride, b_inner_stride, b_slice_stride, st);
   }
 }

@@ -173,7 +173,7 @@ void LaplaceSubtraction_reduce_forward_cuda(const at::Tensor query, const at::Te
 void MixRows_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c) {
   TORCH_CHECK(a.dim() >= 2 && b.dim() == a.dim() && c.dim() == a.dim(), "mix_rows: a, b, c need the same rank >= 2");
   TORCH_CHECK(a.is_contiguous() && c.is_contiguous(), "mix_rows: a and c must be contiguous");
-  TORCH_CHECK(b.scalar_type() == at::kFloat && c.scalar_type() == at::kFloat, "mix_rows: b and c must be float32");
+  TORCH_CHECK(b.scalar_type() == at::kFloat, "mix_rows: b must be float32");
   TORCH_CHECK(a.device() == b.device() && a.device() == c.device(), "mix_rows: tensors on different devices");
   const int nd = (int)a.dim();
   const int64_t N = a.size(nd - 2), P = a.size(nd - 1), Q = b.size(nd - 2);
@@ -187,9 +187,9 @@ void MixRows_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c) {
     else TORCH_CHECK(b.stride(i) == bSlice * S, "mix_rows: b's batch dims do not collapse to one stride");
     S *= a.size(i);
   }
-  const int dt = detail::abi_dtype(a, "mix_rows");
+  const int dt = detail::abi_dtype(a, "mix_rows"), ct = detail::abi_dtype(c, "mix_rows");
   at::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
-  detail::check_status(lfamd_mix_rows(dt, a.data_ptr(), b.data_ptr<float>(), c.data_ptr<float>(), S, N, (int)P,
+  detail::check_status(lfamd_mix_rows(dt, a.data_ptr(), b.data_ptr<float>(), ct, c.data_ptr(), S, N, (int)P,
                                       (int)Q, b.stride(nd - 2), b.stride(nd - 1), bSlice, detail::stream_of(a)));
 }
 

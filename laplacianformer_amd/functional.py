@@ -128,11 +128,12 @@ def _mixable(*widths: int) -> bool:
     return all(0 < w <= _MIX_MAX for w in widths)
 
 
-def mix_rows(a: torch.Tensor, b_qp: torch.Tensor) -> torch.Tensor:
-    """c[..., n, q] = sum_p a[..., n, p] * b_qp[..., q, p] in float32 on the HIP
-    row-product kernel (a contiguous fp32/fp16/bf16, b_qp an fp32 view of any
-    strides whose batch dims collapse to one stride; widths <= 64)."""
-    c = torch.empty(a.shape[:-1] + (b_qp.shape[-2],), dtype=torch.float32, device=a.device)
+def mix_rows(a: torch.Tensor, b_qp: torch.Tensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """c[..., n, q] = sum_p a[..., n, p] * b_qp[..., q, p], summed in float32 on the
+    HIP row-product kernel and returned in ``out_dtype`` (fp32/fp16/bf16, one
+    rounding); a contiguous fp32/fp16/bf16, b_qp an fp32 view of any strides whose
+    batch dims collapse to one stride; widths <= 64."""
+    c = torch.empty(a.shape[:-1] + (b_qp.shape[-2],), dtype=out_dtype, device=a.device)
     ext().MixRows(a.contiguous(), b_qp.float(), c)
     return c
 
@@ -144,17 +145,17 @@ class TallMixFunction(torch.autograd.Function):
     on the library GEMM."""
 
     @staticmethod
-    def forward(ctx, a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    def forward(ctx, a: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
         ctx.save_for_backward(a, w)
-        return mix_rows(a, w.transpose(-1, -2))
+        return mix_rows(a, w.transpose(-1, -2), out_dtype)
 
     @staticmethod
     def backward(ctx, g: torch.Tensor):
         a, w = ctx.saved_tensors
-        g = g.float().contiguous()
-        ga = mix_rows(g, w).to(a.dtype) if ctx.needs_input_grad[0] else None
-        gw = torch.matmul(a.transpose(-1, -2).float(), g).to(w.dtype) if ctx.needs_input_grad[1] else None
-        return ga, gw
+        g = g.contiguous()
+        ga = mix_rows(g, w, a.dtype) if ctx.needs_input_grad[0] else None
+        gw = torch.matmul(a.transpose(-1, -2).float(), g.float()).to(w.dtype) if ctx.needs_input_grad[1] else None
+        return ga, gw, None
 
 
 class TallProductFunction(torch.autograd.Function):
@@ -172,17 +173,20 @@ class TallProductFunction(torch.autograd.Function):
     def backward(ctx, g: torch.Tensor):
         a, b = ctx.saved_tensors
         g = g.float().contiguous()
-        ga = mix_rows(b, g).to(a.dtype) if ctx.needs_input_grad[0] else None
-        gb = mix_rows(a, g.transpose(-1, -2)).to(b.dtype) if ctx.needs_input_grad[1] else None
+        ga = mix_rows(b, g, a.dtype) if ctx.needs_input_grad[0] else None
+        gb = mix_rows(a, g.transpose(-1, -2), b.dtype) if ctx.needs_input_grad[1] else None
         return ga, gb
 
 
-def tall_mix(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """a @ w for tall a [..., N, P] and small fp32 w [..., P, Q]; the HIP row-product
-    kernel where P, Q <= 64 and a is fp32/fp16/bf16, torch.matmul elsewhere."""
-    if a.dtype != torch.float64 and _mixable(a.shape[-1], w.shape[-1]):
-        return TallMixFunction.apply(a, w)
-    return torch.matmul(a, w)
+def tall_mix(a: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """a @ w for tall a [..., N, P] and small fp32 w [..., P, Q], returned in ``out_dtype``
+    (default w's type); the HIP row-product kernel where P, Q <= 64, a is fp32/fp16/bf16
+    and out_dtype is one of those, torch.matmul elsewhere."""
+    out_dtype = out_dtype or w.dtype
+    if (a.dtype != torch.float64 and out_dtype != torch.float64 and w.dtype != torch.float64
+            and _mixable(a.shape[-1], w.shape[-1])):
+        return TallMixFunction.apply(a, w, out_dtype)
+    return torch.matmul(a, w).to(out_dtype)
 
 
 def tall_product(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

@@ -68,10 +68,11 @@ def test_argument_errors_without_device(lib):
     assert lib.lfamd_newton_workspace_size(0, 4, 128) == 0
     assert lib.lfamd_newton_workspace_size(3, 4, 90) == 0
     # Row products: dtype, width and pointer checks happen before any launch.
-    assert lib.lfamd_mix_rows(3, null, null, null, 2, 10, 49, 64, 1, 64, 3136, null) == 2  # no fp64
-    assert lib.lfamd_mix_rows(0, null, null, null, 2, 10, 65, 64, 1, 64, 4160, null) == 3  # inner > 64
-    assert lib.lfamd_mix_rows(0, null, null, null, 2, 10, 49, 64, 1, 64, 3136, null) == 1  # null pointers
-    assert lib.lfamd_mix_rows(0, null, null, null, 0, 10, 49, 64, 1, 64, 3136, null) == 0  # nothing to do
+    assert lib.lfamd_mix_rows(3, null, null, 0, null, 2, 10, 49, 64, 1, 64, 3136, null) == 2  # no fp64
+    assert lib.lfamd_mix_rows(0, null, null, 0, null, 2, 10, 65, 64, 1, 64, 4160, null) == 3  # inner > 64
+    assert lib.lfamd_mix_rows(0, null, null, 0, null, 2, 10, 49, 64, 1, 64, 3136, null) == 1  # null pointers
+    assert lib.lfamd_mix_rows(0, null, null, 0, null, 0, 10, 49, 64, 1, 64, 3136, null) == 0  # nothing to do
+    assert lib.lfamd_mix_rows(0, null, null, 3, null, 2, 10, 49, 64, 1, 64, 3136, null) == 2  # fp64 output
     dummy = ctypes.c_void_p(16)
     assert lib.lfamd_newton_forward(0, dummy, dummy, 4, 200, 3, null, 0, null) == 1
     assert b"workspace" in lib.lfamd_last_error()

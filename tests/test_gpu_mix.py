@@ -41,6 +41,20 @@ def test_mix_rows(gpu, dt, shape):
     _check(c2, a, wq, "a @ wq^T")
 
 
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("out", [torch.float16, torch.bfloat16])
+def test_mix_rows_output_type(gpu, dt, out):
+    """A 16-bit output is the fp32 result rounded once (bit-identical to casting it)."""
+    import laplacianformer_amd as lf
+
+    print(f"mix rows output {dt} -> {out}", flush=True)
+    a = gen((2, 3, 333, 49), 21, dt).to(gpu)
+    w = gen((2, 3, 64, 49), 22, "f32").to(gpu)
+    c = lf.mix_rows(a, w, out)
+    assert c.dtype == out
+    assert torch.equal(c, lf.mix_rows(a, w).to(out))
+
+
 def test_mix_rows_rejects(gpu):
     import laplacianformer_amd as lf
 
