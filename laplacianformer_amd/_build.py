@@ -25,7 +25,8 @@ LIB_PATH = os.path.join(PKG_DIR, "liblfamd.so")
 EXT_NAME = "Laplace_subtraction_cuda"
 EXT_PATH = os.path.join(PKG_DIR, EXT_NAME + ".so")
 
-HIP_SOURCES = ["laplace_kernels.hip", "newton_kernels.hip", "mix_kernels.hip", "lf_runtime.hip"]
+HIP_SOURCES = ["laplace_kernels.hip", "laplace_bwd2.hip", "newton_kernels.hip", "mix_kernels.hip",
+               "lf_runtime.hip"]
 TORCH_SOURCES = ["wrapper.cpp", "LaplaceSubtraction_hip.cpp", "NewtonInverse_hip.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -61,8 +62,14 @@ def _torch_paths():
     return inc, libdir, abi
 
 
+def generate(verbose=False):
+    """Writes csrc/l1_asm_gen.h from csrc/gen_l1_asm.py (unchanged files are left alone)."""
+    _run([sys.executable, os.path.join(CSRC, "gen_l1_asm.py"), os.path.join(CSRC, "l1_asm_gen.h")], verbose)
+
+
 def build_hip(verbose=False, jobs=4):
     os.makedirs(BUILD_DIR, exist_ok=True)
+    generate(verbose)
     objs = []
     cmds = []
     for src in HIP_SOURCES:

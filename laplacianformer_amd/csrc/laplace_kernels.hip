@@ -1791,6 +1791,9 @@ int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq,
   }
   if (!g || !q || !k || (doDq && !dq) || (doDk && !dk)) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
+  if (b2_ok(dtype, d.BH(), d.N, d.M, d.C))
+    return b2_launch(dtype, g, q, k, doDq ? dq : nullptr, doDk ? dk : nullptr, ws, wsBytes, d.BH(), d.N, d.M, d.C,
+                     st, who);
   if (bcast_bwd_ok(dtype, d, g)) {
     const BcPlan sp = plan_bcast(d, doDk);
     if (doDk && (!ws || wsBytes < sp.partialElems * 4))
@@ -1871,6 +1874,7 @@ size_t lfamd_laplace_backward_workspace_size(int dtype, int64_t batch, int64_t h
   if (dtype != LFAMD_F64) bytes = std::max(bytes, plan_bcast(d, true).partialElems * 4);
   if (dtype != LFAMD_F64 && d.M >= 17 && d.M <= 8 * kMbMC)
     bytes = std::max(bytes, plan_mb(d, true).partialElems * 4);
+  if (b2_ok(dtype, d.BH(), d.N, d.M, d.C)) bytes = std::max(bytes, b2_workspace_elems(d.BH(), d.N, d.M, d.C) * 4);
   return bytes;
 }
 

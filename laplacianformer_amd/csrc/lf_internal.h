@@ -24,6 +24,12 @@ int max_lds_bytes();
 // Compute units of the current device (cached per device; 256 if unknown).
 int num_cus();
 
+// Column-split fused backward of 16-bit LaplaceSubtraction (laplace_bwd2.hip).
+bool b2_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C);
+size_t b2_workspace_elems(int64_t BH, int64_t N, int64_t M, int64_t C);
+int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, size_t wsBytes,
+              int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who);
+
 inline bool valid_dtype(int dt) {
   return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;
 }
