@@ -19,20 +19,26 @@
 //
 // Mapping. A workgroup is 8 waves (2 per SIMD: the register file holds two of
 // these waves, and the SIMD issues two VALU instructions per 4 cycles only from
-// an even number of waves). One channel block of 64 channels per workgroup;
-// lane (h, p), h = lane / 32, p = lane % 32, owns channels 2p and 2p + 1 and the
-// key columns [h * JC, h * JC + JC), JC = ceil(M / 2). Its key terms and grad_key
-// sums stay in registers; the grad rows are staged in LDS (2g as fp32, the two
-// halves of a row 16-byte aligned, the row sum in slot JC of each half) and read
-// back as 16-byte wave-wide reads with two addresses, each feeding 24 VALU
-// instructions (two channels x four columns x three). The row loop itself is the
-// generated asm block of l1_asm_gen.h (register map chosen to avoid VGPR bank
-// clashes, grad rows of the next batch loaded during the current one).
+// an even number of waves), one per CU, and takes a contiguous range of at most
+// 512 rows of one (b, h) slice and one channel block of 64 channels. Lane
+// (h, p), h = lane / 32, p = lane % 32, owns channels 2p and 2p + 1 and the key
+// columns of parity h (column 2j + h, j < JC = ceil(M / 2)); its key terms and
+// grad_key sums stay in registers.
 //
-// grad_key: each wave's partial (column sums of g minus the accumulated 2g y) is
-// summed over the workgroup's waves in LDS in a fixed order and written per
-// workgroup channel-major; laplace_dk_reduce_t_kernel sums the workgroups of a
-// slice in workgroup order. Results are deterministic.
+// The workgroup stages its grad rows in LDS in one pass: 4-byte loads, all in
+// flight at once, scattered as 2g in fp32 to row r, half h = col % 2, slot
+// col / 2 (so consecutive lanes write consecutive LDS words), each half 16-byte
+// aligned with the row sum of g in slot JC. Each wave then adds the row sums and
+// column sums of its own rows and runs its row loop: the generated asm block of
+// l1_asm_gen.h, in which every 16-byte wave-wide grad read (two addresses, one
+// per half) feeds 24 VALU instructions (two channels x four columns x three),
+// the register map is chosen for the co-issue of the SIMD's two waves, and
+// query rows are prefetched four rows ahead.
+//
+// grad_key: per wave, half its column sums of 2g minus its accumulated 2g y,
+// summed over the waves in LDS in wave order; the workgroup partials of a slice
+// are summed in workgroup order by laplace_dk_reduce_t_kernel. Results are
+// deterministic.
 #include <algorithm>
 
 #include "lf_common.h"
@@ -43,27 +49,30 @@ namespace lfamd {
 
 namespace {
 
-constexpr int kB2Waves = 8;   // waves per workgroup (2 per SIMD)
-constexpr int kB2RB = 8;      // grad rows per staged batch (the asm block's RB)
-constexpr int kB2Bufs = 4;    // LDS accumulators of the workgroup grad_key reduction
-
-template <typename T> struct B2Traits;
-template <> struct B2Traits<f16s> { static constexpr bool bf16 = false; };
-template <> struct B2Traits<bf16s> { static constexpr bool bf16 = true; };
+constexpr int kB2Waves = 8;     // waves per workgroup (2 per SIMD)
+constexpr int kB2Unroll = 4;    // rows per iteration of the asm row loop (its query prefetch depth)
+constexpr int kB2MaxRows = 512;  // most grad rows of one workgroup (staged in LDS at once)
+constexpr int kB2Threads = 64 * kB2Waves;
 
 // Layout constants shared by the kernel and the host plan.
 struct B2Shape {
-  int M, JC, EPL, XV, HP, PITCH, NKK;
+  int M, JC, HP, PITCH, NKK;
   __host__ __device__ constexpr B2Shape(int m)
-      : M(m), JC((m + 1) / 2), EPL((m + 7) / 8), XV(m / ((m + 7) / 8)), HP((((m + 1) / 2) + 1 + 3) / 4 * 4),
-        PITCH(2 * ((((m + 1) / 2) + 1 + 3) / 4 * 4)), NKK((2 * ((m + 1) / 2) + 3) / 4) {}
-  // Per-wave staging slot: RB rows plus one row the read-ahead may touch, plus a
-  // 64-byte scratch area for the writes of lanes without a real destination.
-  __host__ __device__ constexpr int slot_bytes() const { return ((kB2RB + 1) * PITCH) * 4 + 64; }
-  __host__ __device__ constexpr int kk_bytes() const { return NKK * 64 * 16; }
-  __host__ __device__ constexpr int red_bytes() const { return kB2Bufs * M * 65 * 4; }
+      : M(m), JC((m + 1) / 2), HP((((m + 1) / 2) + 1 + 3) / 4 * 4), PITCH(2 * ((((m + 1) / 2) + 1 + 3) / 4 * 4)),
+        NKK((2 * ((m + 1) / 2) + 3) / 4) {}
+  // LDS: the waves' column sums of 2g [kB2Waves][M] | key-term table
+  // [NKK][65][4] (lane-major 16-byte groups, one spare group per table row so
+  // that the scatter into it spreads over the banks) | staged rows
+  // [kB2MaxRows + 1][PITCH]. After the row loops the waves' grad_key sums
+  // ([kB2Waves][M][65], channel fastest, padded) overwrite the table and rows.
+  __host__ __device__ constexpr int colsum_bytes() const { return (kB2Waves * M * 4 + 15) / 16 * 16; }
+  __host__ __device__ constexpr int kk_off() const { return colsum_bytes(); }
+  __host__ __device__ constexpr int rows_off() const { return kk_off() + NKK * 65 * 16; }
+  __host__ __device__ constexpr int red_bytes() const { return kB2Waves * M * 65 * 4; }
   __host__ __device__ constexpr int lds_bytes() const {
-    return kk_bytes() + kB2Waves * slot_bytes() > red_bytes() ? kk_bytes() + kB2Waves * slot_bytes() : red_bytes();
+    return rows_off() + (kB2MaxRows + 1) * PITCH * 4 > colsum_bytes() + red_bytes()
+               ? rows_off() + (kB2MaxRows + 1) * PITCH * 4
+               : colsum_bytes() + red_bytes();
   }
 };
 
@@ -73,24 +82,26 @@ __device__ __forceinline__ float tmap16(uint16_t bits) {
   return __builtin_bit_cast(float, (uint32_t)(0x4a808000 + t));
 }
 
+template <typename T> __device__ __forceinline__ float g2f(uint16_t b);
+template <> __device__ __forceinline__ float g2f<f16s>(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+template <> __device__ __forceinline__ float g2f<bf16s>(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
 // Dispatch to the generated row loops (grad_query and grad_key together or alone).
 template <typename T, int M, bool DQ, bool DK> struct B2Rows;
-#define LFAMD_B2ROWS(TY, MM, DQ_, DK_, FN)                                                            \
-  template <> struct B2Rows<TY, MM, DQ_, DK_> {                                                        \
-    static constexpr B2Shape S{MM};                                                                    \
-    __device__ static void run(float (&dk)[2 * S.JC], float (&cs)[S.EPL], const void* g, const void* q,    \
-                               void* dq, unsigned qs, int nfull, int tail, const void* gt, const void* qt, \
-                               unsigned rda, unsigned vq, unsigned goff, unsigned gofft, unsigned rs,       \
-                               float vx, float vrt, unsigned kka, const unsigned (&st)[S.EPL],              \
-                               unsigned wpar, const unsigned (&g0)[S.EPL], const unsigned (&q0)[kB2RB]) {   \
-      FN;                                                                                              \
-    }                                                                                                  \
+#define LFAMD_B2ROWS(TY, MM, DQ_, DK_, FN)                                                               \
+  template <> struct B2Rows<TY, MM, DQ_, DK_> {                                                           \
+    __device__ static void run(float (&dk)[2 * ((MM + 1) / 2)], const void* q3, const void* ql, void* dq,  \
+                               unsigned qs, int rows, unsigned wpar, unsigned rda, unsigned vq4,           \
+                               unsigned vqs, unsigned kka, const unsigned (&q0)[kB2Unroll]) {               \
+      FN(dk, q3, ql, dq, qs, rows, wpar, rda, vq4, vqs, kka, q0);                                         \
+    }                                                                                                     \
   };
-#define LFAMD_B2ARGS dk, cs, g, q, dq, qs, nfull, tail, gt, qt, rda, vq, goff, gofft, rs, vx, vrt, kka, st, wpar, g0, q0
-#define LFAMD_B2ALL(TY, TN, MM)                                                \
-  LFAMD_B2ROWS(TY, MM, true, true, bwd2_rows_##TN##_m##MM##_qk(LFAMD_B2ARGS))   \
-  LFAMD_B2ROWS(TY, MM, true, false, bwd2_rows_##TN##_m##MM##_q(LFAMD_B2ARGS))   \
-  LFAMD_B2ROWS(TY, MM, false, true, bwd2_rows_##TN##_m##MM##_k(LFAMD_B2ARGS))
+#define LFAMD_B2ALL(TY, TN, MM)                                    \
+  LFAMD_B2ROWS(TY, MM, true, true, bwd2_rows_##TN##_m##MM##_qk)     \
+  LFAMD_B2ROWS(TY, MM, true, false, bwd2_rows_##TN##_m##MM##_q)     \
+  LFAMD_B2ROWS(TY, MM, false, true, bwd2_rows_##TN##_m##MM##_k)
 LFAMD_B2ALL(f16s, f16, 49)
 LFAMD_B2ALL(bf16s, bf16, 49)
 LFAMD_B2ALL(f16s, f16, 32)
@@ -98,161 +109,232 @@ LFAMD_B2ALL(bf16s, bf16, 32)
 LFAMD_B2ALL(f16s, f16, 16)
 LFAMD_B2ALL(bf16s, bf16, 16)
 #undef LFAMD_B2ALL
-#undef LFAMD_B2ARGS
 #undef LFAMD_B2ROWS
 
-// Grid: (nx workgroups per slice, channel blocks, B*H). The slice's N rows are
-// split evenly over its nx * 8 waves.
+// Loads `count` >= 1 16-bit elements from `src` as 4-byte words: word b of the
+// workgroup in thread b % kB2Threads, slot b / kB2Threads. The first word may
+// start one element before `src` and the last end one after the span (never
+// outside the 4-byte-aligned words holding the span's own bytes); slots past
+// the last word load it again. Returns the number of elements before `src` in
+// word 0 (0 or 1).
+template <int MAXW>
+__device__ __forceinline__ int load_words(const uint16_t* src, int count, int tid, uint32_t (&wd)[MAXW]) {
+  const int skew = (int)(reinterpret_cast<uintptr_t>(src) & 3) >> 1;
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(src - skew);
+  const int last = ((count + skew + 1) >> 1) - 1;
+#pragma unroll
+  for (int i = 0; i < MAXW; ++i) wd[i] = base[min(tid + i * kB2Threads, last)];
+  return skew;
+}
+
+// a where c, else b, as one v_cndmask on a lane mask (a plain select lets the
+// compiler branch around the computation of a).
+__device__ __forceinline__ int select_lanes(bool c, int a, int b) {
+  const unsigned long long m = __builtin_amdgcn_ballot_w64(c);
+  int r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(m));
+  return r;
+}
+
+// Calls f(row, col, valid, bits) for both 16-bit halves of every word loaded by
+// load_words: (row, col) = (e / M, e % M) for the element index e of the half,
+// valid = e in [0, count) (f is to route an invalid element to a dummy
+// location). (row, col) advance incrementally from word to word; there are no
+// branches. In each call of a wave the lanes hold elements two apart.
+template <int M, int MAXW, typename F>
+__device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int skew, int count, int tid, F f) {
+  constexpr int kStep = 2 * kB2Threads, kDR = kStep / M, kDC = kStep % M;
+  int e = 2 * tid - skew;            // >= -1
+  int row = (e + M) / M - 1;         // -1 for e = -1
+  int col = e - row * M;
+#pragma unroll
+  for (int i = 0; i < MAXW; ++i) {
+    f(row, col, (unsigned)e < (unsigned)count, (uint16_t)(wd[i] & 0xffff));
+    const int wrap = col == M - 1 ? 1 : 0;
+    f(row + wrap, wrap ? 0 : col + 1, (unsigned)(e + 1) < (unsigned)count, (uint16_t)(wd[i] >> 16));
+    e += kStep;
+    col += kDC;
+    row += kDR;
+    const int carry = col >= M ? 1 : 0;
+    col -= carry * M;
+    row += carry;
+  }
+}
+
+// Grid: (nx workgroups per slice, channel blocks, B*H). Workgroup x takes rows
+// [x*N/nx, (x+1)*N/nx) of its slice, at most kB2MaxRows of them (the host
+// plan sizes nx for that), split evenly over the 8 waves.
 template <typename T, int M, bool DQ, bool DK>
-__global__ void __launch_bounds__(64 * kB2Waves, 1)
+__global__ void __launch_bounds__(kB2Threads, 1)
 laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, const T* __restrict__ key,
                     T* __restrict__ dq, float* __restrict__ partial, int N, int C) {
   constexpr B2Shape S{M};
-  constexpr int JC = S.JC, EPL = S.EPL, XV = S.XV, HP = S.HP, PITCH = S.PITCH;
-  const int wave = uniform(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  constexpr int JC = S.JC, HP = S.HP, PITCH = S.PITCH, NKK = S.NKK;
+  static_assert(M >= 2, "M >= 2");
+  const int tid = threadIdx.x;
+  const int wave = uniform(tid >> 6);
+  const int lane = tid & 63;
   const int x = blockIdx.x, nx = gridDim.x, cb = blockIdx.y, bh = blockIdx.z;
   const int ncb = gridDim.y;
 
   extern __shared__ __align__(16) unsigned char smem[];
   const unsigned ldsBase = (unsigned)(uintptr_t)smem;
-  float* kkt = reinterpret_cast<float*>(smem);                                   // [NKK][64][4]
-  unsigned char* slot = smem + S.kk_bytes() + wave * S.slot_bytes();             // this wave's staging slot
-  const unsigned slotA = ldsBase + S.kk_bytes() + wave * S.slot_bytes();
-  const unsigned scratchA = slotA + (kB2RB + 1) * PITCH * 4;
+  float* colsum = reinterpret_cast<float*>(smem);                     // [kB2Waves][M]: column sums of 2g
+  float* kkt = reinterpret_cast<float*>(smem + S.kk_off());           // [NKK][65][4]
+  float* rowsA = reinterpret_cast<float*>(smem + S.rows_off());       // [rows + 1][PITCH]
+  const unsigned rowsBase = ldsBase + S.rows_off();
 
-  // This wave's rows.
-  const int gw = x * kB2Waves + wave, nw = nx * kB2Waves;
-  const int r0 = uniform((int)((int64_t)gw * N / nw)), r1 = uniform((int)((int64_t)(gw + 1) * N / nw));
-  const int rows = r1 - r0;
-  // The first batch's raw grad elements and query patterns are loaded before the
-  // key table is built, so that their memory latency overlaps it.
-  const int nfull0 = rows / kB2RB, tail0 = rows - nfull0 * kB2RB;
-  const int rl = lane >> 3, xsl = lane & 7;
-  unsigned g0[EPL], q0[kB2RB];
-  {
-    const uint16_t* gsrc = reinterpret_cast<const uint16_t*>(gout) + ((size_t)bh * N + r0) * M;
-    const uint16_t* qsrc = reinterpret_cast<const uint16_t*>(query) + ((size_t)bh * N + r0) * C + cb * 64 +
-                           2 * (lane & 31) + (lane >> 5);
-    const int nr = nfull0 > 0 ? kB2RB : tail0;
-    const int rr0 = nfull0 > 0 ? rl : min(rl, max(nr - 1, 0));
-    const int eoff = rr0 * M + (xsl < XV ? xsl * EPL : 0);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) g0[e] = rows > 0 ? gsrc[eoff + e] : 0u;
-#pragma unroll
-    for (int rr = 0; rr < kB2RB; ++rr) q0[rr] = rr < nr ? qsrc[(size_t)rr * C] : 0u;
-  }
+  const int P0 = (int)((int64_t)x * N / nx), P1 = (int)((int64_t)(x + 1) * N / nx);
+  const int n = P1 - P0;
+  const int nm = n * M;
+  const uint16_t* qsl = reinterpret_cast<const uint16_t*>(query) + (size_t)bh * N * C + cb * 64;
 
-  // Key terms 0.5 - T(k[c][col]) for lane (h, p): [c][j] = channel 2p + c, column h*JC + j.
-  const uint16_t* kb = reinterpret_cast<const uint16_t*>(key) + (size_t)bh * C * M;
-  for (int t = threadIdx.x; t < 64 * S.NKK * 4; t += blockDim.x) {
-    const int l = (t >> 2) & 63, grp = t >> 8, e = grp * 4 + (t & 3);
-    float v = 0.0f;
-    if (e < 2 * JC) {
-      const int c = e / JC, j = e - c * JC;
-      const int col = (l >> 5) * JC + j;
-      const int ch = cb * 64 + 2 * (l & 31) + c;
-      if (col < M) v = 0.5f - tmap16(kb[(size_t)ch * M + col]);
-    }
-    kkt[t] = v;
-  }
-  // The staging slot starts zeroed (half 1's pad column of an odd M is never written).
-  for (int t = lane; t * 4 < S.slot_bytes(); t += 64) reinterpret_cast<float*>(slot)[t] = 0.0f;
-  __syncthreads();
-
-  float dk[2 * JC], cs[EPL];
-  if (rows > 0) {
-    const int nfull = rows / kB2RB, tail = rows - nfull * kB2RB;
-    const T* gw0 = gout + ((size_t)bh * N + r0) * M;
-    const T* qw0 = query + ((size_t)bh * N + r0) * C + cb * 64;
-    T* dqw0 = dq + ((size_t)bh * N + r0) * C + cb * 64;
-    const T* gt = gw0 + (size_t)nfull * kB2RB * M;
-    const T* qt = qw0 + (size_t)nfull * kB2RB * C;
-    // Staging lane (r, xs): row r of the batch, elements [xs*EPL, xs*EPL + EPL).
-    const int r = lane >> 3, xs = lane & 7;
-    const bool xv = xs < XV;
-    unsigned st[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const int col = xs * EPL + e;
-      const int h = col >= JC ? 1 : 0;
-      st[e] = xv ? slotA + (unsigned)(r * PITCH + h * HP + (col - h * JC)) * 4 : scratchA + lane % 16 * 4;
-    }
-    const unsigned rs = xs < 4 ? slotA + (unsigned)(r * PITCH + (xs & 1) * HP + JC) * 4 : scratchA + lane % 16 * 4;
-    const unsigned goff = (unsigned)(r * M + (xv ? xs * EPL : 0)) * 2;
-    const int rt = tail > 0 ? min(r, tail - 1) : 0;
-    const unsigned gofft = (unsigned)(rt * M + (xv ? xs * EPL : 0)) * 2;
-    const unsigned rda = slotA + (unsigned)((lane >> 5) * HP) * 4;
-    const unsigned vq = (unsigned)(2 * (lane & 31) + (lane >> 5)) * 2;
-    const unsigned kka = ldsBase + (unsigned)lane * 16;
-    B2Rows<T, M, DQ, DK>::run(dk, cs, gw0, qw0, dqw0, (unsigned)C * 2, nfull, tail, gt, qt, rda, vq, goff, gofft, rs,
-                      xv ? 1.0f : 0.0f, r < tail ? 1.0f : 0.0f, kka, st, (unsigned)uniform(wave >= 4 ? 1 : 0), g0, q0);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 2 * JC; ++j) dk[j] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) cs[e] = 0.0f;
-  }
-
-  if constexpr (!DK) return;
-  // Column sums of 2g over this wave's rows: column col = xs*EPL + e collects the
-  // staging lanes (r, xs) of the 8 batch rows r, summed in r order.
-  float* csw = reinterpret_cast<float*>(slot);            // [64][EPL]
-  float* colsum = csw + 64 * EPL;                          // [M] sum_i g (half of the 2g sum)
-  wave_sync();
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) csw[lane * EPL + e] = cs[e];
-  wave_sync();
-  if (lane < M) {
-    const int xs = lane / EPL, e = lane - xs * EPL;
-    float s = 0.0f;
-#pragma unroll
-    for (int rr = 0; rr < kB2RB; ++rr) s += csw[(rr * 8 + xs) * EPL + e];
-    colsum[lane] = 0.5f * s;
-  }
-  wave_sync();
-  // Partial grad_key of this wave: column sum minus the accumulated 2g y.
+  // All loads first: the key block [64][M] of the channel block, the grad rows
+  // (n*M contiguous elements) and the first query pairs of this wave's row loop.
+  constexpr int kKeyW = (64 * M + 2 + 2 * kB2Threads - 1) / (2 * kB2Threads);
+  uint32_t kwd[kKeyW];
+  const int kskew = load_words(reinterpret_cast<const uint16_t*>(key) + ((size_t)bh * C + cb * 64) * M, 64 * M, tid, kwd);
+  constexpr int kRowW = (kB2MaxRows * M + 2 + 2 * kB2Threads - 1) / (2 * kB2Threads);
+  uint32_t gwd[kRowW];
+  const int gskew = load_words(reinterpret_cast<const uint16_t*>(gout) + ((size_t)bh * N + P0) * M, nm, tid, gwd);
+  const int w0 = uniform((int)((int64_t)wave * n / kB2Waves)), w1 = uniform((int)((int64_t)(wave + 1) * n / kB2Waves));
+  const int rows = w1 - w0;  // at most kB2MaxRows / kB2Waves = 64
   const int h = lane >> 5, p = lane & 31;
+  unsigned q0[kB2Unroll];
+  {
+    const uint32_t* qpair = reinterpret_cast<const uint32_t*>(qsl + (size_t)(P0 + w0) * C) + p;
 #pragma unroll
-  for (int j = 0; j < JC; ++j) {
-    const int col = h * JC + j;
-    const float cv = colsum[col < M ? col : 0];
-    dk[j] = cv - dk[j];
-    dk[JC + j] = cv - dk[JC + j];
+    for (int k = 0; k < kB2Unroll; ++k) q0[k] = rows > 0 ? qpair[(size_t)min(k, rows - 1) * (C / 2)] : 0u;
   }
 
-  // Workgroup sum over the waves in a fixed order: wave w adds into accumulator
-  // w % kB2Bufs in rounds of increasing w / kB2Bufs; accumulators are [M][65]
-  // (channel fastest, padded), summed 0..3 and written channel-major.
-  float* red = reinterpret_cast<float*>(smem);
-  float* buf = red + (wave % kB2Bufs) * M * 65;
-  __syncthreads();
-  for (int round = 0; round * kB2Bufs < kB2Waves; ++round) {
-    if (wave / kB2Bufs == round) {
+  // Key terms 0.5 - T(k[c][col]) for lane (h, p): entry [c][j] of the lane
+  // (channel 2p + c, column 2j + h) at kkt[((e / 4) * 65 + lane) * 4 + e % 4],
+  // e = c*JC + j; entries without a key column are zero.
+  // (Invalid elements go to the spare entry [0][64][0].)
+  scatter_words<M>(kwd, kskew, 64 * M, tid, [&](int ch, int col, bool valid, uint16_t bits) {
+    const int l = (ch >> 1) + 32 * (col & 1), e = (ch & 1) * JC + (col >> 1);
+    const int a = ((e >> 2) * 65 + l) * 4 + (e & 3);
+    kkt[select_lanes(valid, a, 64 * 4)] = 0.5f - tmap16(bits);
+  });
+  if (tid < 64) {
 #pragma unroll
-      for (int j = 0; j < JC; ++j) {
-        const int col = h * JC + j;
-        if (col < M) {
-          float* a = buf + col * 65 + 2 * p;
-          if (round == 0) {
-            a[0] = dk[j];
-            a[1] = dk[JC + j];
-          } else {
-            a[0] += dk[j];
-            a[1] += dk[JC + j];
-          }
+    for (int e = 2 * JC; e < 4 * NKK; ++e) kkt[((e >> 2) * 65 + tid) * 4 + (e & 3)] = 0.0f;
+    if (M % 2 && tid >= 32) {
+      kkt[(((JC - 1) >> 2) * 65 + tid) * 4 + ((JC - 1) & 3)] = 0.0f;
+      kkt[(((2 * JC - 1) >> 2) * 65 + tid) * 4 + ((2 * JC - 1) & 3)] = 0.0f;
+    }
+  }
+  // Grad rows as 2g: column col of row r at rowsA[r*PITCH + (col % 2)*HP + col / 2].
+  // (Invalid elements go to slot 0 of the spare row n.)
+  scatter_words<M>(gwd, gskew, nm, tid, [&](int row, int col, bool valid, uint16_t bits) {
+    const float v = g2f<T>(bits);
+    const int a = __mul24(row, PITCH) + (col & 1) * HP + (col >> 1);
+    rowsA[select_lanes(valid, a, n * PITCH)] = v + v;
+  });
+  __syncthreads();
+
+  // Each wave completes its own rows (its LDS operations are performed in
+  // order, so its row loop below sees them without another barrier).
+  if (lane < rows) {
+    // Row sum of g (half of the sum of the staged 2g) into slot JC of both
+    // halves, read as 16-byte groups; an odd M's missing column of half 1
+    // (slot JC - 1) is zeroed.
+    float* rp = rowsA + (w0 + lane) * PITCH;
+    if (DQ) {
+      float s2 = 0.0f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int cols = hh == 0 ? JC : M - JC;
+#pragma unroll
+        for (int g = 0; g * 4 < cols; ++g) {
+          const float4 a = *reinterpret_cast<const float4*>(rp + hh * HP + 4 * g);
+          const float b = (4 * g + 1 < cols ? a.x + a.y : a.x) + (4 * g + 3 < cols ? a.z + a.w : 4 * g + 2 < cols ? a.z : 0.0f);
+          s2 += b;
+        }
+      }
+      rp[JC] = 0.5f * s2;
+      rp[HP + JC] = 0.5f * s2;
+    }
+    if (M % 2) rp[HP + JC - 1] = 0.0f;
+  }
+  if (DK) {
+    // Column sums of 2g over the wave's rows: lane (group, r) sums the 4-column
+    // group `group` of rows w0 + r, w0 + r + RQ, ...; then a fixed butterfly
+    // over the RQ lanes of the group.
+    constexpr int NG0 = (JC + 3) / 4, NG1 = (M - JC + 3) / 4, NGT = NG0 + NG1;
+    constexpr int RQ = NGT <= 4 ? 16 : NGT <= 8 ? 8 : NGT <= 16 ? 4 : NGT <= 32 ? 2 : 1;
+    static_assert(NGT * RQ <= 64, "column groups of a wave");
+    const int grp = lane / RQ, r = lane % RQ;
+    const int hh = grp >= NG0 ? 1 : 0;
+    const int g = grp - hh * NG0;
+    float4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (grp < NGT) {
+      const float* cp = rowsA + (w0 + r) * PITCH + hh * HP + 4 * g;
+#pragma unroll
+      for (int k = 0; k < (kB2MaxRows / kB2Waves + RQ - 1) / RQ; ++k) {
+        if (r + k * RQ < rows) {
+          const float4 v = *reinterpret_cast<const float4*>(cp + k * RQ * PITCH);
+          a.x += v.x;
+          a.y += v.y;
+          a.z += v.z;
+          a.w += v.w;
         }
       }
     }
-    __syncthreads();
-  }
-  float* out = partial + (((size_t)bh * ncb + cb) * nx + x) * 64 * M;   // [64][M] channel-major
-  for (int t = threadIdx.x; t < 64 * M; t += blockDim.x) {
-    const int c = t / M, col = t - c * M;
-    float s = red[col * 65 + c];
 #pragma unroll
-    for (int b = 1; b < kB2Bufs; ++b) s += red[b * M * 65 + col * 65 + c];
-    out[t] = s;
+    for (int m = 1; m < RQ; m <<= 1) {
+      a.x += __shfl_xor(a.x, m);
+      a.y += __shfl_xor(a.y, m);
+      a.z += __shfl_xor(a.z, m);
+      a.w += __shfl_xor(a.w, m);
+    }
+    if (grp < NGT && r == 0) {
+      const int cols = hh == 0 ? JC : M - JC;
+      const float v4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (4 * g + k < cols) colsum[wave * M + 2 * (4 * g + k) + hh] = v4[k];
+    }
+  }
+  float dk[2 * JC];
+#pragma unroll
+  for (int j = 0; j < 2 * JC; ++j) dk[j] = 0.0f;
+  if (rows > 0) {
+    const unsigned rda = rowsBase + (unsigned)(w0 * PITCH + h * HP) * 4;
+    const uint16_t* q3 = uniform_ptr(qsl + (size_t)(P0 + w0 + kB2Unroll - 1) * C);
+    const uint16_t* ql = uniform_ptr(qsl + (size_t)(P0 + w1 - 1) * C);
+    uint16_t* dqrow = uniform_ptr(reinterpret_cast<uint16_t*>(dq) + ((size_t)bh * N + P0 + w0) * C + cb * 64);
+    B2Rows<T, M, DQ, DK>::run(dk, q3, ql, dqrow, (unsigned)C * 2, rows, (unsigned)uniform(wave >= 4 ? 1 : 0), rda,
+                              (unsigned)p * 4, (unsigned)(2 * p + h) * 2, ldsBase + S.kk_off() + (unsigned)lane * 16,
+                              q0);
+  }
+  if constexpr (!DK) return;
+
+  // Workgroup grad_key partial: per wave, half its column sums of 2g minus its
+  // accumulated 2g y; summed over the waves in wave order and written
+  // channel-major. (A wave's column sums were written by its own lanes.)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem + S.colsum_bytes());   // [kB2Waves][M][65]
+  {
+    float* buf = red + wave * M * 65;
+#pragma unroll
+    for (int j = 0; j < JC; ++j) {
+      const int col = 2 * j + h;
+      if (col < M) {
+        const float cs = 0.5f * colsum[wave * M + col];
+        buf[col * 65 + 2 * p] = cs - dk[j];
+        buf[col * 65 + 2 * p + 1] = cs - dk[JC + j];
+      }
+    }
+  }
+  __syncthreads();
+  float* out = partial + (((size_t)bh * ncb + cb) * nx + x) * 64 * M;   // [64][M] channel-major
+  for (int t = tid; t < 64 * M; t += kB2Threads) {
+    const int c = t / M, col = t - c * M;
+    float s2 = red[col * 65 + c];
+#pragma unroll
+    for (int w = 1; w < kB2Waves; ++w) s2 += red[w * M * 65 + col * 65 + c];
+    out[t] = s2;
   }
 }
 
@@ -270,7 +352,15 @@ laplace_dk_reduce_t_kernel(const float* __restrict__ partial, T* __restrict__ dk
   if (cb * 64 + c >= C) return;
   const float* p = partial + ((size_t)bh * ncb + cb) * nx * n + t;
   float s = 0.0f;
-  for (int i = 0; i < nx; ++i) s += p[(size_t)i * n];
+  int i = 0;
+  for (; i + 8 <= nx; i += 8) {  // eight loads in flight, summed in order
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[(size_t)(i + k) * n];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += v[k];
+  }
+  for (; i < nx; ++i) s += p[(size_t)i * n];
   dk[((size_t)bh * C + cb * 64 + c) * M + col] = from_acc<T>(s);
 }
 
@@ -283,8 +373,11 @@ B2Plan plan_b2(int64_t BH, int64_t N, int64_t M, int64_t C) {
   B2Plan p{};
   p.ncb = (int)(C / 64);
   const int64_t slices = BH * p.ncb;
-  p.nx = (int)std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
-                                                      (N + kB2Waves - 1) / kB2Waves));
+  // One workgroup per CU where the rows allow (at least 8 rows each), and never
+  // more than kB2MaxRows rows per workgroup (its LDS holds that many).
+  p.nx = (int)std::max<int64_t>((N + kB2MaxRows - 1) / kB2MaxRows,
+                                std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
+                                                                       (N + kB2Waves - 1) / kB2Waves)));
   p.lds = (size_t)B2Shape((int)M).lds_bytes();
   p.partialElems = (size_t)slices * p.nx * 64 * (size_t)M;
   return p;
@@ -294,7 +387,7 @@ template <typename T, int M, bool DQ, bool DK>
 int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, int64_t BH, int64_t N,
                 int64_t C, const B2Plan& p, hipStream_t st) {
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
-  hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK>), grid, dim3(64 * kB2Waves), p.lds, st, static_cast<const T*>(g),
+  hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK>), grid, dim3(kB2Threads), p.lds, st, static_cast<const T*>(g),
                      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<T*>(dq),
                      static_cast<float*>(ws), (int)N, (int)C);
   int s = check_launch("laplace backward (column-split)");
@@ -326,7 +419,8 @@ int launch_b2(int dtype, const void* g, const void* q, const void* k, void* dq, 
 
 // grad_query and / or grad_key on the column-split kernel (null dq or dk: that
 // half is skipped): fp16 / bf16, M in {16, 32, 49}, C a multiple of 64 (one
-// channel block per 64 channels), N >= 1.
+// channel block per 64 channels), N >= 1. The caller also needs the query
+// 4-byte aligned (it is read as channel pairs).
 bool b2_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C) {
   if (!(dtype == LFAMD_F16 || dtype == LFAMD_BF16)) return false;
   if (!(M == 16 || M == 32 || M == 49)) return false;

@@ -81,6 +81,14 @@ __device__ __forceinline__ float mix_fms_fh(float s, uint32_t g, float acc) {
 
 // Wave-uniform value hint (moves a VGPR that is known to be uniform to an SGPR).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Pointer form of uniform().
+template <typename P>
+__device__ __forceinline__ P* uniform_ptr(P* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<P*>(((uint64_t)hi << 32) | lo);
+}
 
 // Orders the LDS accesses of one wave around this point: what any lane of the
 // wave wrote before it is visible to every lane of the wave after it.
