@@ -25,7 +25,7 @@ LIB_PATH = os.path.join(PKG_DIR, "liblfamd.so")
 EXT_NAME = "Laplace_subtraction_cuda"
 EXT_PATH = os.path.join(PKG_DIR, EXT_NAME + ".so")
 
-HIP_SOURCES = ["laplace_kernels.hip", "laplace_bwd2.hip", "newton_kernels.hip", "mix_kernels.hip",
+HIP_SOURCES = ["laplace_kernels.hip", "laplace_bwd2.hip", "laplace_fwd2.hip", "newton_kernels.hip", "mix_kernels.hip",
                "lf_runtime.hip"]
 TORCH_SOURCES = ["wrapper.cpp", "LaplaceSubtraction_hip.cpp", "NewtonInverse_hip.cpp"]
 

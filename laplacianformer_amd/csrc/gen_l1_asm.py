@@ -39,6 +39,7 @@ import sys
 LANES = 64
 UNROLL = 4        # rows per loop iteration (= depth of the query prefetch ring)
 KK_GSTRIDE = (LANES + 1) * 16   # bytes between 16-byte groups of the key-term table ([group][65][4] floats)
+STORE_POLICY = " nt"
 
 
 class Regs:
@@ -225,7 +226,7 @@ def variant(dtype, M, DQ=True, DK=True):
                 add(f"v_cvt_pk_bf16_f32 v{T0}, v{T0}, v{T0}")
             else:
                 add(f"v_cvt_f16_f32 v{T0}, v{T0}")
-            add(f"global_store_short v{VQS}, v{T0}, s[{SD}:{SD+1}]")
+            add(f"global_store_short v{VQS}, v{T0}, s[{SD}:{SD+1}]" + STORE_POLICY)
             add(f"s_add_u32 s{SD}, s{SD}, s{SQS}")
             add(f"s_addc_u32 s{SD+1}, s{SD+1}, 0")
     add(f"v_add_u32 v{RDA}, {UNROLL * PITCH * 4}, v{RDA}")
@@ -269,6 +270,122 @@ __device__ __forceinline__ void {name}(float (&dk)[{2*JC}], const void* q3, cons
     return name, src, dict(JC=JC, HP=HP, PITCH=PITCH, nmine=nmine)
 
 
+FWD_JB = 7          # key columns per forward column block
+FWD_KP = 56 * 4     # bytes per channel of the forward key tile ([C][56] fp32)
+
+
+def fwd_variant(R, top=256):
+    """Returns (name, C++ source) of the channel loop of the row-staged forward
+    (laplace_fwd2.hip) for R row sets per lane, using VGPRs below `top` (256:
+    two waves per SIMD; 128: four).
+
+    Per channel c and row set s: T = q[s][c] - k[c][j] (v_sub_f32) and
+    acc[s][j] += |T| (v_add_f32 with the |.| modifier), j < 7, channels in
+    ascending order. The query tile is read as 16-byte vectors (4 channels of
+    one row per lane), one group ahead; the key row of a channel as two
+    16-byte reads (7 columns + padding), one channel ahead. Eight channels per
+    loop iteration (two query groups, so the two query buffers alternate
+    statically). Register banks: K[j] and acc[s][j] in bank j % 4, query
+    channel cc in bank cc; each T is placed in a bank different from both its
+    source query register (the sub's src0) and its accumulator (the add reads
+    T as src0 and writes the accumulator)."""
+    r = Regs(top)
+    QA = [r.take(4, align=4) for _ in range(R)]
+    QB = [r.take(4, align=4) for _ in range(R)]
+    KS = [r.take(8, align=4) for _ in range(2)]
+    ACC = r.take(8 * R, align=4)            # acc[s][j] = ACC + 8s + j (bank j % 4)
+    TB = r.take(16, align=4)                # temporaries: bank b holds TB + b, TB + 4 + b, ...
+    QADDR = [r.take(1) for _ in range(R)]
+    KADDR = r.take(1)
+    lo = r.next
+    SC = 72
+    L = []
+    add = L.append
+
+    def acc(s, j):
+        return ACC + 8 * s + j
+
+    add("s_waitcnt vmcnt(0) lgkmcnt(0)")
+    add(f"s_mov_b32 s{SC}, %[iters]")
+    for s_ in range(R):
+        add(f"v_mov_b32 v{QADDR[s_]}, %[qa{s_}]")
+    add(f"v_mov_b32 v{KADDR}, %[ka]")
+    for s_ in range(R):
+        for j in range(FWD_JB):
+            add(f"v_mov_b32 v{acc(s_, j)}, 0")
+    for s_ in range(R):
+        add(f"ds_read_b128 v[{QA[s_]}:{QA[s_] + 3}], v{QADDR[s_]}")
+    add(f"ds_read_b128 v[{KS[0]}:{KS[0] + 3}], v{KADDR}")
+    add(f"ds_read_b128 v[{KS[0] + 4}:{KS[0] + 7}], v{KADDR} offset:16")
+    add("FL_%=:")
+    for ci in range(8):
+        Q = QA if ci < 4 else QB
+        cc = ci % 4
+        K = KS[ci % 2]
+        Kn = KS[(ci + 1) % 2]
+        nq = 0
+        if ci == 0 or ci == 4:
+            dst = QB if ci == 0 else QA
+            off = 16 if ci == 0 else 32
+            for s_ in range(R):
+                add(f"ds_read_b128 v[{dst[s_]}:{dst[s_] + 3}], v{QADDR[s_]} offset:{off}")
+            nq = R
+        koff = (ci + 1) * FWD_KP
+        add(f"ds_read_b128 v[{Kn}:{Kn + 3}], v{KADDR} offset:{koff}")
+        add(f"ds_read_b128 v[{Kn + 4}:{Kn + 7}], v{KADDR} offset:{koff + 16}")
+        add(f"s_waitcnt lgkmcnt({nq + 2})")
+        for s_ in range(R):
+            qreg = Q[s_] + cc
+            used = [0, 0, 0, 0]
+            ts = []
+            for j in range(FWD_JB):
+                ok = [b for b in range(4) if b != qreg % 4 and b != acc(s_, j) % 4 and used[b] < 4]
+                b = min(ok, key=lambda b: used[b])
+                t = TB + 4 * used[b] + b
+                used[b] += 1
+                ts.append(t)
+                add(f"v_sub_f32 v{t}, v{qreg}, v{K + j}")
+            for j in range(FWD_JB):
+                add(f"v_add_f32_e64 v{acc(s_, j)}, |v{ts[j]}|, v{acc(s_, j)}")
+    for s_ in range(R):
+        add(f"v_add_u32 v{QADDR[s_]}, 32, v{QADDR[s_]}")
+    add(f"v_add_u32 v{KADDR}, {8 * FWD_KP}, v{KADDR}")
+    add(f"s_sub_u32 s{SC}, s{SC}, 1")
+    add(f"s_cmp_gt_u32 s{SC}, 0")
+    add("s_cbranch_scc1 FL_%=")
+    add("s_waitcnt lgkmcnt(0)")
+    for s_ in range(R):
+        for j in range(FWD_JB):
+            add(f"v_mov_b32 %[a{s_}_{j}], v{acc(s_, j)}")
+
+    name = f"fwd2_sums_r{R}"
+    asm = "\n".join("      \"" + x + "\\n\"" for x in L)
+    outs = ", ".join(f"[a{s_}_{j}] \"=v\"(acc[{s_}][{j}])" for s_ in range(R) for j in range(FWD_JB))
+    ins = ", ".join(["[iters] \"s\"(iters)", "[ka] \"v\"(ka)"] + [f"[qa{s_}] \"v\"(qa[{s_}])" for s_ in range(R)])
+    clob = ", ".join([f"\"v{v}\"" for v in range(lo, top)] + [f"\"s{SC}\"", "\"memory\""])
+    if top != 256:
+        name += f"_v{top}"
+    src = f"""
+// Channel loop of the row-staged forward for {R} row set(s) per lane ({top - lo} private VGPRs below v{top}):
+// acc[s][j] = sum over channels c < 8 * iters of |q[s][c] - k[c][j]|, c ascending. qa[s]: LDS
+// byte address of the lane's row of set s in the fp32 query tile (channel 0); ka: LDS byte
+// address of the lane's 8-column key block at channel 0 (rows of {FWD_KP} bytes). Reads go one
+// query group and one channel past the end (the tiles' padding and the next tile; unused).
+__device__ __forceinline__ void {name}(float (&acc)[{R}][{FWD_JB}], const unsigned (&qa)[{R}], unsigned ka, int iters) {{
+  asm volatile(
+{asm}
+      : {outs}
+      : {ins}
+      : {clob});
+}}
+"""
+    return name, src
+
+
+FWD_RS = (1, 2, 3, 4, 5, 6, 7)
+FWD_RS_V128 = (1, 2, 3)
+
+
 VARIANTS = [(dt, M, dq, dk) for dt in ("f16", "bf16") for M in (49, 32, 16)
             for (dq, dk) in ((True, True), (True, False), (False, True))]
 
@@ -279,6 +396,14 @@ def main(out_path):
     for dt, M, dq, dk in VARIANTS:
         name, src, info = variant(dt, M, dq, dk)
         parts.append(f"// {name}: {info}")
+        parts.append(src)
+    for R in FWD_RS:
+        name, src = fwd_variant(R)
+        parts.append(f"// {name}")
+        parts.append(src)
+    for R in FWD_RS_V128:
+        name, src = fwd_variant(R, 128)
+        parts.append(f"// {name}")
         parts.append(src)
     parts.append("}  // namespace lfamd")
     text = "\n".join(parts) + "\n"

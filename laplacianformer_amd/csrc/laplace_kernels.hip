@@ -1839,6 +1839,8 @@ int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* o
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d.C == 0) return zero_fill(output, d.BH() * d.N * d.M * (int64_t)dtype_size(dtype), st);
   if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace forward: null pointer");
+  if (f2_ok(dtype, d.BH(), d.N, d.M, d.C, query))
+    return f2_launch(dtype, false, query, key, output, d.BH(), d.N, d.C, 0.0f, st);
   if (fwd_bcast_ok(dtype, d, query, dtype_size(dtype))) {
     switch (dtype) {
       case LFAMD_F32: return launch_fwd_bcast<float>(query, key, output, d, st);
@@ -1911,6 +1913,8 @@ int lfamd_laplace_kernel_forward(int dtype, const void* query, const void* key, 
                 dtype, (long long)d.M, (long long)d.C);
   if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace kernel forward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (f2_ok(dtype, d.BH(), d.N, d.M, d.C, query))
+    return f2_launch(dtype, true, query, key, output, d.BH(), d.N, d.C, scale, st);
   switch (dtype) {
     case LFAMD_F32: return launch_fwd_bcast<float, kEpiExp>(query, key, output, d, st, scale);
     case LFAMD_F16: return launch_fwd_bcast<f16s, kEpiExp>(query, key, output, d, st, scale);

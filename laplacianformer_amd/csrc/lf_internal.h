@@ -30,6 +30,12 @@ size_t b2_workspace_elems(int64_t BH, int64_t N, int64_t M, int64_t C);
 int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, size_t wsBytes,
               int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who);
 
+// Row-staged forward of LaplaceSubtraction at M = 49 (laplace_fwd2.hip); kernelEpi:
+// exp(-scale * distance) in fp32 instead of the distance in the element type.
+bool f2_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C, const void* q);
+int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,
+              float scale, hipStream_t st);
+
 inline bool valid_dtype(int dt) {
   return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;
 }

@@ -1,0 +1,69 @@
+"""GPU parity of the row-staged M = 49 forward (laplace_fwd2.hip) across its work plans.
+
+Each shape is chosen (for 256 CUs) to reach one plan of the kernel: 16 waves with
+runs of 1-3 row sets and a tail wave, 16 waves with workgroups one row apart (the
+tail length differs between them), and 8 waves with 7-set runs (full and partial
+last set). The distance must be bit-identical to the fp32 serial oracle (the
+kernel sums the channels in the reference's order); the fused exp(-s * distance)
+variant is held to the fp32 rounding of s * d and expf.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from lfcheck import assert_bitwise, gen
+
+pytestmark = pytest.mark.gpu
+
+# (B, H, N, M, C, what)
+SHAPES = [
+    (1, 64, 272, 49, 64, "16 waves, 1 set + 4-row tail"),
+    (1, 16, 2176, 49, 32, "16 waves, 2 sets + 8-row tail"),
+    (1, 8, 5120, 49, 64, "16 waves, 3 sets (last partial)"),
+    (4, 32, 784, 49, 64, "16 waves, 6 sets + 8-row tail (config-5 layer shape)"),
+    (32, 1, 3141, 49, 64, "16 waves, 6 sets + 8/9-row tails (workgroups one row apart)"),
+    (1, 8, 13440, 49, 40, "8 waves, 7 sets (last partial)"),
+    (1, 8, 14336, 49, 8, "8 waves, 7 full sets"),
+]
+
+
+def _ids(s):
+    return "x".join(map(str, s[:5]))
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_fwd2_plans(gpu, shape, dt):
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C, what = shape
+    print(f"fwd2 {shape[:5]} {dt}: {what}", flush=True)
+    q = gen((B, H, N, C), 500 + N, dt)
+    k = gen((B, H, C, M), 501 + N, dt)
+    L = lf.ext()
+    out = torch.empty((B, H, N, M), dtype=q.dtype, device=gpu)
+    L.LaplaceSubtraction_forward(q.to(gpu), k.to(gpu), out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.laplace_forward(q, k, dt), dt, f"forward bits ({what})")
+
+
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[5]], ids=_ids)
+def test_fwd2_kernel_epilogue(gpu, shape):
+    """The fused exp(-s * d) output of the same kernel, fp16 inputs."""
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C, what = shape
+    print(f"fwd2 exp {shape[:5]}: {what}", flush=True)
+    q = gen((B, H, N, C), 600 + N, "f16")
+    k = gen((B, H, C, M), 601 + N, "f16")
+    s = 1.0 / math.sqrt(C)
+    out = torch.empty((B, H, N, M), dtype=torch.float32, device=gpu)
+    assert lf.ext().LaplaceKernel_forward(q.to(gpu), k.to(gpu), out, s) is True
+    d32 = oracle.laplace_forward(q, k, "f32").astype(np.float64)
+    ref = np.exp(-s * d32)
+    got = out.cpu().double().numpy()
+    lim = ref * (2.0 ** -21) * (1.0 + s * d32) + 1e-38
+    assert not (np.abs(got - ref) > lim).any(), what
