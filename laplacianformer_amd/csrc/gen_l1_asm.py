@@ -1,28 +1,34 @@
 #!/usr/bin/env python3
-"""Generator of the hand-scheduled gfx950 row loop of the L1 backward.
+"""Generator of the hand-scheduled gfx950 inner loops of the L1 kernels.
 
-Writes ``l1_asm_gen.h``: one ``__device__`` function per (element type, key
-count M, grad_query / grad_key selection) holding a single ``asm volatile``
-block, the row loop of one wave of the column-split backward
-(``laplace_bwd2.hip``). The grad rows are already staged in LDS by the
-workgroup (2g as fp32, each half row 16-byte aligned, the row sum in slot JC
-of each half); the block reads them back, loads the query row of each step,
-and issues the arithmetic and the grad_query stores. It is generated rather
-than written by hand because its value lies in the register map:
+Writes ``l1_asm_gen.h``: ``__device__`` functions each holding a single
+``asm volatile`` block:
 
-* every VALU instruction reads VGPR operands only (an SGPR operand halves the
-  issue rate on gfx950);
-* VGPR banks (register number mod 4) are chosen as measured fastest for this
-  loop at two waves per SIMD (the step values at the parity opposite to the
-  grad values, the grad_query accumulators in banks 1 and 2), and
-  ``v_fmac_f32``'s src0 is never in the accumulator's bank: each product has
-  two candidate src0 registers, the grad value and the step value, in
-  different banks, and the generator picks the one that differs;
-* hazards the hardware does not interlock are covered explicitly (``s_nop``
-  before a ``v_permlane32_swap`` reading just-written VGPRs): the compiler
-  does not insert wait states inside inline asm.
+* ``bwd2_rows_*``: the row loop of one wave of the column-split backward
+  (``laplace_bwd2.hip``), per element type, key count M and grad_query /
+  grad_key selection. The grad rows are already staged in LDS by the
+  workgroup (2g as fp32, each half row 16-byte aligned, the half's sum of g in
+  slot JC); the block reads them back, loads the query row of each step, and
+  issues the arithmetic and the grad_query stores.
+* ``fwd2_sums_*``: the channel loop of the row-staged forward
+  (``laplace_fwd2.hip``) for R row sets per lane.
 
-The arithmetic per (row i, key column j, channel c), with T() the
+They are generated rather than written by hand because their value lies in
+the schedule and the register map:
+
+* every VALU instruction reads VGPR operands only (an SGPR in src1, which
+  needs the VOP3 encoding, lowers the issue rate on gfx950);
+* ``v_fmac_f32``'s src0 is never in the accumulator's VGPR bank (register
+  number mod 4): each product has two candidate src0 registers, the grad value
+  and the step value, in different banks, and the generator picks the one that
+  differs;
+* LDS and global waits are exact counts of the operations issued since the one
+  needed, and dependent work is interleaved with independent work across rows
+  (backward) or one channel ahead (forward);
+* nothing needs software wait states (the compiler does not insert them
+  inside inline asm): there are no DPP, permlane or VALU-written SGPR reads.
+
+The backward arithmetic per (row i, key column j, channel c), with T() the
 order-preserving map of a 16-bit float pattern onto the fp32 values
 2^22 + 2^14 + t/2 (t = signed magnitude of the pattern, so +0 and -0 coincide):
 
@@ -70,11 +76,25 @@ def variant(dtype, M, DQ=True, DK=True):
 
     DQ / DK select the grad_query and grad_key halves of the work: without DK
     there are no grad_key accumulators, without DQ no grad_query accumulation
-    or stores (the query rows are still needed for the steps)."""
+    or stores (the query rows are still needed for the steps).
+
+    Lane (h, p) holds its two channels in the order (own, partner): c0 =
+    2p + h, c1 = 2p + 1 - h, so that the grad_query partial a lane owes its
+    partner (lane p + 32 (1 - h), the other column half) is always the c1
+    accumulator: one ds_bpermute_b32 exchanges them (v_permlane32_swap costs
+    the SIMD about ten times a v_fmac).
+
+    Software pipelining across rows: T(q) of row r + 1 is computed during row
+    r, and the grad_query of row r is finished during row r + 1 (the partials
+    exchanged after its first group, summed, rounded and stored a few groups
+    later), so no instruction waits on a just-written operand; the
+    accumulators and T(q) alternate between two register sets by row parity.
+    Each half subtracts its own half of the row sum (slot JC of the staged
+    half row) at the end of the row."""
     assert DQ or DK
     JC, HP, NG, PITCH = shape(M)
     RSLOT = JC
-    assert RSLOT // 4 == NG - 1
+    assert RSLOT // 4 == NG - 1 and NG >= 3
     bf16 = dtype == "bf16"
 
     r = Regs()
@@ -82,13 +102,17 @@ def variant(dtype, M, DQ=True, DK=True):
     DK_ = r.take(2 * JC, bank=1) if DK else None      # grad_key accumulators [c][j]
     G = r.take(16, align=4)                           # grad ring: 4 slots of 4 (bank k for element k)
     Y = r.take(8, bank=3)                             # step values [c][k]
-    DQR = [r.take(1, bank=1), r.take(1, bank=2)] if DQ else None   # grad_query accumulators [c]
-    TQ = r.take(2, bank=1)                            # T(q) of the current row [c]
+    DQA = [[r.take(1, bank=1), r.take(1, bank=2)] for _ in range(2)] if DQ else None  # grad_query [parity][c0, c1]
+    RECV = r.take(1) if DQ else None                  # the partner's c1 partial (= this lane's channel)
+    TQ = [r.take(2, bank=1) for _ in range(2)]        # T(q) [parity][c]
     QR = r.take(UNROLL)                               # query pattern pairs of the next rows (ring)
     RDA = r.take(1)       # LDS byte address of the current iteration's first row (lane's half)
     VQ4 = r.take(1)       # byte offset of the lane's channel pair in a query row
     VQS = r.take(1)       # byte offset of the lane's own channel in a grad_query row
-    T0 = r.take(4)        # temporaries
+    T0 = r.take(4)        # T-map temporaries
+    FT = r.take(1)        # grad_query finishing temporary
+    SHF = r.take(4)       # bit offsets in the query pair: c0 value, c0 sign, c1 value, c1 sign
+    PADDR = r.take(1)     # ds_bpermute address of the partner lane
     lo = r.next
     nmine = 256 - lo
 
@@ -96,15 +120,17 @@ def variant(dtype, M, DQ=True, DK=True):
     S = 72
     SQ = S                # 64-bit: query row of the latest prefetch
     SQL = S + 2           # 64-bit: the wave's last query row (prefetch clamp)
-    SD = S + 4            # 64-bit: grad_query row of the current row
+    SD = S + 4            # 64-bit: grad_query row of the next store
     SQS = S + 6           # row stride (bytes)
     SLEFT = S + 7         # rows left, counted at iteration starts
     SPR = S + 8           # priority phase
     SPC = S + 9           # iterations until the next priority flip
-    STMP = S + 10         # 64-bit temporary
+    STMP = S + 10         # 64-bit temporary (prefetch address)
     SRN = S + 12          # row index of the latest prefetch
     SROWS = S + 13        # rows of the wave
-    SREG_HI = S + 13
+    SDN = S + 14          # 64-bit temporary (next grad_query row)
+    SFLAG = S + 16        # 0 until the first (placeholder) grad_query store
+    SREG_HI = S + 16
 
     L = []
     add = L.append
@@ -118,6 +144,32 @@ def variant(dtype, M, DQ=True, DK=True):
             return f"v_fmac_f32 v{acc}, v{gk}, v{yk}"
         return f"v_fmac_f32 v{acc}, v{yk}, v{gk}"
 
+    def tmap(x, tq):
+        # T of the lane's c0 and c1 patterns (bit offsets per lane): as_float(0x4a808000 + t),
+        # t = +-magnitude.
+        for c in range(2):
+            add(f"v_bfe_u32 v{T0}, v{x}, v{SHF + 2*c}, 15")
+            add(f"v_bfe_i32 v{T0 + 1}, v{x}, v{SHF + 2*c + 1}, 1")
+            add(f"v_sub_u32 v{T0 + 2}, 0x4a808000, v{T0 + 1}")
+            add(f"v_xad_u32 v{tq + c}, v{T0}, v{T0 + 1}, v{T0 + 2}")
+
+    def finish_store(pp):
+        # The lane's own channel: its c0 partial (its column half) plus the
+        # partner's c1 partial (the other half), received by ds_bpermute. The
+        # very first store of the wave is a placeholder at the first row,
+        # rewritten by that row's own store.
+        add(f"v_add_f32 v{FT}, v{DQA[pp][0]}, v{RECV}")
+        if bf16:
+            add(f"v_cvt_pk_bf16_f32 v{FT}, v{FT}, v{FT}")
+        else:
+            add(f"v_cvt_f16_f32 v{FT}, v{FT}")
+        add(f"global_store_short v{VQS}, v{FT}, s[{SD}:{SD+1}]" + STORE_POLICY)
+        add(f"s_add_u32 s{SDN}, s{SD}, s{SQS}")
+        add(f"s_addc_u32 s{SDN+1}, s{SD+1}, 0")
+        add(f"s_cmp_lg_u32 s{SFLAG}, 0")
+        add(f"s_cselect_b64 s[{SD}:{SD+1}], s[{SDN}:{SDN+1}], s[{SD}:{SD+1}]")
+        add(f"s_mov_b32 s{SFLAG}, 1")
+
     # ---- entry ---------------------------------------------------------------
     add("s_waitcnt vmcnt(0) lgkmcnt(0)")
     add(f"s_mov_b64 s[{SQ}:{SQ+1}], %[q3]")
@@ -129,9 +181,13 @@ def variant(dtype, M, DQ=True, DK=True):
     add(f"s_mov_b32 s{SRN}, {UNROLL - 1}")
     add(f"s_mov_b32 s{SPR}, %[wpar]")
     add(f"s_mov_b32 s{SPC}, 0")
+    add(f"s_mov_b32 s{SFLAG}, 0")
     add(f"v_mov_b32 v{RDA}, %[rda]")
     add(f"v_mov_b32 v{VQ4}, %[vq4]")
     add(f"v_mov_b32 v{VQS}, %[vqs]")
+    for c in range(4):
+        add(f"v_mov_b32 v{SHF + c}, %[shf{c}]")
+    add(f"v_mov_b32 v{PADDR}, %[paddr]")
     for k in range(UNROLL):
         add(f"v_mov_b32 v{QR + k}, %[q0_{k}]")
     for i in range((2 * JC + 3) // 4):
@@ -139,13 +195,20 @@ def variant(dtype, M, DQ=True, DK=True):
     if DK:
         for j in range(2 * JC):
             add(f"v_mov_b32 v{DK_ + j}, %[dk{j}]")
+    tmap(QR, TQ[0])
     add("s_waitcnt lgkmcnt(0)")
 
     ring = 4
     ahead = 3
-    # VMEM operations per row: the prefetch load, plus the grad_query store.
-    per_row = 2 if DQ else 1
-    vmc = per_row * (UNROLL - 1) + (1 if DQ else 0)
+    # VMEM operations per row: the prefetch load, then the grad_query store.
+    # T(q) of row r + 1 is computed in row r: its load (issued in row r - 3) is
+    # followed by that row's store and two operations in each of rows r - 2,
+    # r - 1 and r.
+    vmc = 7 if DQ else 3
+    # Group after which the previous row's grad_query is stored: the exchange
+    # (issued after group 0) is older than the group's g_fin reads.
+    g_fin = min(ahead, NG - 1)
+    g_tmap = NG - 2               # group after which T(q) of the next row is computed
 
     def pos_addr(p):
         rr, g = divmod(p, NG)
@@ -170,24 +233,14 @@ def variant(dtype, M, DQ=True, DK=True):
     add("s_setprio 0")
     add("PR_%=_d:")
     for rr in range(UNROLL):
+        par = rr % 2
         if rr > 0:
             add(f"s_cmp_le_u32 s{SLEFT}, {rr}")
-            add("s_cbranch_scc1 RX_%=")
-        # The query pair of this row (prefetched UNROLL rows ago, or loaded by the
-        # caller): at most vmc younger VMEM operations may be outstanding.
-        add(f"s_waitcnt vmcnt({vmc})")
+            add(f"s_cbranch_scc1 RX{rr}_%=")
         x = QR + rr
-        # T of the low and high patterns: as_float(0x4a808000 + t), t = +-magnitude.
-        add(f"v_and_b32 v{T0}, 0x7fff, v{x}")
-        add(f"v_bfe_i32 v{T0 + 1}, v{x}, 15, 1")
-        add(f"v_sub_u32 v{T0 + 2}, 0x4a808000, v{T0 + 1}")
-        add(f"v_xad_u32 v{TQ}, v{T0}, v{T0 + 1}, v{T0 + 2}")
-        add(f"v_bfe_u32 v{T0}, v{x}, 16, 15")
-        add(f"v_ashrrev_i32 v{T0 + 1}, 31, v{x}")
-        add(f"v_sub_u32 v{T0 + 2}, 0x4a808000, v{T0 + 1}")
-        add(f"v_xad_u32 v{TQ + 1}, v{T0}, v{T0 + 1}, v{T0 + 2}")
-        # Prefetch the query pair UNROLL rows ahead into the freed slot; past the
-        # wave's last row the last row is read again (never out of bounds).
+        # Prefetch the query pair UNROLL rows ahead into this row's slot (its T(q)
+        # was taken in the previous row); past the wave's last row the last row is
+        # read again (never out of bounds).
         add(f"s_add_u32 s{SQ}, s{SQ}, s{SQS}")
         add(f"s_addc_u32 s{SQ+1}, s{SQ+1}, 0")
         add(f"s_add_u32 s{SRN}, s{SRN}, 1")
@@ -198,41 +251,48 @@ def variant(dtype, M, DQ=True, DK=True):
             p = rr * NG + g
             pn = p + ahead
             add(f"ds_read_b128 v[{G + 4*(pn % ring)}:{G + 4*(pn % ring) + 3}], v{RDA} offset:{pos_addr(pn)}")
-            add(f"s_waitcnt lgkmcnt({ahead})")
+            add(f"s_waitcnt lgkmcnt({g_fin if DQ and g == g_fin else ahead})")
             gs = G + 4 * (p % ring)
             cols = grp_cols(g)
             for c in range(2):
                 for k, j in enumerate(cols):
-                    add(f"v_add_f32_e64 v{Y + 4*c + k}, v{TQ + c}, v{KK + c*JC + j} clamp")
+                    add(f"v_add_f32_e64 v{Y + 4*c + k}, v{TQ[par] + c}, v{KK + c*JC + j} clamp")
             for k, j in enumerate(cols):
                 for c in range(2):
                     if DQ:
                         if j == 0:
-                            add(f"v_mul_f32 v{DQR[c]}, v{gs + k}, v{Y + 4*c + k}")
+                            add(f"v_mul_f32 v{DQA[par][c]}, v{gs + k}, v{Y + 4*c + k}")
                         else:
-                            add(fmac(DQR[c], gs + k, Y + 4*c + k))
+                            add(fmac(DQA[par][c], gs + k, Y + 4*c + k))
                     if DK:
                         add(fmac(DK_ + c*JC + j, gs + k, Y + 4*c + k))
+            if DQ and g == 0:
+                add(f"ds_bpermute_b32 v{RECV}, v{PADDR}, v{DQA[1 - par][1]}")
+            if DQ and g == g_fin:
+                finish_store(1 - par)
+            if g == g_tmap:
+                # T(q) of the next row, into the other parity's registers.
+                add(f"s_waitcnt vmcnt({vmc})")
+                tmap(QR + (rr + 1) % UNROLL, TQ[1 - par])
         if DQ:
-            # Lanes 0-31 hold column half 0 of channels (2p, 2p+1), lanes 32-63 half 1;
-            # after the swap lane p holds both halves of channel 2p, lane 32+p of 2p+1.
+            # This row's grad_query: minus the lane's half of the row sum.
             rg = G + 4 * ((rr * NG + NG - 1) % ring) + (RSLOT % 4)
-            add("s_nop 4")
-            add(f"v_permlane32_swap_b32 v{DQR[0]}, v{DQR[1]}")
-            add("s_nop 1")
-            add(f"v_add_f32 v{T0}, v{DQR[0]}, v{DQR[1]}")
-            add(f"v_sub_f32 v{T0}, v{T0}, v{rg}")
-            if bf16:
-                add(f"v_cvt_pk_bf16_f32 v{T0}, v{T0}, v{T0}")
-            else:
-                add(f"v_cvt_f16_f32 v{T0}, v{T0}")
-            add(f"global_store_short v{VQS}, v{T0}, s[{SD}:{SD+1}]" + STORE_POLICY)
-            add(f"s_add_u32 s{SD}, s{SD}, s{SQS}")
-            add(f"s_addc_u32 s{SD+1}, s{SD+1}, 0")
+            for c in range(2):
+                add(f"v_sub_f32 v{DQA[par][c]}, v{DQA[par][c]}, v{rg}")
     add(f"v_add_u32 v{RDA}, {UNROLL * PITCH * 4}, v{RDA}")
     add(f"s_sub_u32 s{SLEFT}, s{SLEFT}, {UNROLL}")
     add(f"s_cmp_gt_i32 s{SLEFT}, 0")
     add("s_cbranch_scc1 RL_%=")
+    # Exits: the grad_query of the last computed row is still to be stored.
+    for rr in (UNROLL, 1, 2, 3):
+        if rr != UNROLL:
+            add(f"RX{rr}_%=:")
+        if DQ:
+            pp = (rr - 1) % 2
+            add(f"ds_bpermute_b32 v{RECV}, v{PADDR}, v{DQA[pp][1]}")
+            add("s_waitcnt lgkmcnt(0)")
+            finish_store(pp)
+        add("s_branch RX_%=")
     add("RX_%=:")
     add("s_setprio 0")
     add("s_waitcnt vmcnt(0) lgkmcnt(0)")
@@ -246,7 +306,8 @@ def variant(dtype, M, DQ=True, DK=True):
     outs = ", ".join([f"[dk{j}] \"+v\"(dk[{j}])" for j in range(2 * JC)]) if DK else ""
     ins = ", ".join([
         "[q3] \"s\"(q3)", "[ql] \"s\"(qlast)", "[dq] \"s\"(dq)", "[qs] \"s\"(qstride)", "[rows] \"s\"(rows)",
-        "[wpar] \"s\"(wpar)", "[rda] \"v\"(rda)", "[vq4] \"v\"(vq4)", "[vqs] \"v\"(vqs)", "[kka] \"v\"(kka)"] +
+        "[wpar] \"s\"(wpar)", "[rda] \"v\"(rda)", "[vq4] \"v\"(vq4)", "[vqs] \"v\"(vqs)", "[kka] \"v\"(kka)",
+        "[paddr] \"v\"(paddr)"] + [f"[shf{c}] \"v\"(shf[{c}])" for c in range(4)] +
         [f"[q0_{k}] \"v\"(q0[{k}])" for k in range(UNROLL)])
     clob = ", ".join([f"\"v{v}\"" for v in range(lo, 256)] +
                      [f"\"s{s}\"" for s in range(S, SREG_HI + 1)] + ["\"vcc\"", "\"memory\""])
@@ -256,10 +317,12 @@ def variant(dtype, M, DQ=True, DK=True):
 // rows >= 1 rows; q0: the query pairs of the first {UNROLL} rows (loaded by the caller,
 // rows past the wave's end repeat its last row); q3: the query row {UNROLL - 1} rows after the
 // first (prefetches advance from it); qlast: the wave's last query row; dq: the first
-// grad_query row; rda: LDS address of the first staged row plus the lane's half offset.
+// grad_query row; rda: LDS address of the first staged row plus the lane's half offset;
+// shf: bit offsets of the lane's c0 value, c0 sign, c1 value, c1 sign in a query pair;
+// paddr: 4 * (the partner lane).
 __device__ __forceinline__ void {name}(float (&dk)[{2*JC}], const void* q3, const void* qlast, void* dq,
     unsigned qstride, int rows, unsigned wpar, unsigned rda, unsigned vq4, unsigned vqs, unsigned kka,
-    const unsigned (&q0)[{UNROLL}]) {{
+    unsigned paddr, const unsigned (&shf)[4], const unsigned (&q0)[{UNROLL}]) {{
   asm volatile(
 {asm}
       : {outs}

@@ -21,19 +21,22 @@
 // these waves, and the SIMD issues two VALU instructions per 4 cycles only from
 // an even number of waves), one per CU, and takes a contiguous range of at most
 // 512 rows of one (b, h) slice and one channel block of 64 channels. Lane
-// (h, p), h = lane / 32, p = lane % 32, owns channels 2p and 2p + 1 and the key
-// columns of parity h (column 2j + h, j < JC = ceil(M / 2)); its key terms and
-// grad_key sums stay in registers.
+// (h, p), h = lane / 32, p = lane % 32, owns channels 2p + h and 2p + 1 - h (in
+// that order) and the key columns of parity h (column 2j + h, j < JC =
+// ceil(M / 2)); its key terms and grad_key sums stay in registers, and its
+// grad_query is that of channel 2p + h (the other column half's partial comes
+// from lane (1 - h, p)).
 //
 // The workgroup stages its grad rows in LDS in one pass: 4-byte loads, all in
 // flight at once, scattered as 2g in fp32 to row r, half h = col % 2, slot
 // col / 2 (so consecutive lanes write consecutive LDS words), each half 16-byte
-// aligned with the row sum of g in slot JC. Each wave then adds the row sums and
-// column sums of its own rows and runs its row loop: the generated asm block of
-// l1_asm_gen.h, in which every 16-byte wave-wide grad read (two addresses, one
-// per half) feeds 24 VALU instructions (two channels x four columns x three),
-// the register map is chosen for the co-issue of the SIMD's two waves, and
-// query rows are prefetched four rows ahead.
+// aligned with that half's sum of g in slot JC. Each wave then adds the half-row
+// sums and column sums of its own rows and runs its row loop: the generated asm
+// block of l1_asm_gen.h, in which every 16-byte wave-wide grad read (two
+// addresses, one per half) feeds 24 VALU instructions (two channels x four
+// columns x three), query rows are prefetched four rows ahead, and the T(q) of
+// the next row and the grad_query of the previous row are interleaved with the
+// current row's arithmetic.
 //
 // grad_key: per wave, half its column sums of 2g minus its accumulated 2g y,
 // summed over the waves in LDS in wave order; the workgroup partials of a slice
@@ -94,8 +97,9 @@ template <typename T, int M, bool DQ, bool DK> struct B2Rows;
   template <> struct B2Rows<TY, MM, DQ_, DK_> {                                                           \
     __device__ static void run(float (&dk)[2 * ((MM + 1) / 2)], const void* q3, const void* ql, void* dq,  \
                                unsigned qs, int rows, unsigned wpar, unsigned rda, unsigned vq4,           \
-                               unsigned vqs, unsigned kka, const unsigned (&q0)[kB2Unroll]) {               \
-      FN(dk, q3, ql, dq, qs, rows, wpar, rda, vq4, vqs, kka, q0);                                         \
+                               unsigned vqs, unsigned kka, unsigned paddr, const unsigned (&shf)[4],       \
+                               const unsigned (&q0)[kB2Unroll]) {                                          \
+      FN(dk, q3, ql, dq, qs, rows, wpar, rda, vq4, vqs, kka, paddr, shf, q0);                             \
     }                                                                                                     \
   };
 #define LFAMD_B2ALL(TY, TN, MM)                                    \
@@ -208,11 +212,12 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
   }
 
   // Key terms 0.5 - T(k[c][col]) for lane (h, p): entry [c][j] of the lane
-  // (channel 2p + c, column 2j + h) at kkt[((e / 4) * 65 + lane) * 4 + e % 4],
-  // e = c*JC + j; entries without a key column are zero.
-  // (Invalid elements go to the spare entry [0][64][0].)
+  // (channel 2p + (c ^ h): the lane's own channel first, column 2j + h) at
+  // kkt[((e / 4) * 65 + lane) * 4 + e % 4], e = c*JC + j; entries without a
+  // key column are zero. (Invalid elements go to the spare entry [0][64][0].)
   scatter_words<M>(kwd, kskew, 64 * M, tid, [&](int ch, int col, bool valid, uint16_t bits) {
-    const int l = (ch >> 1) + 32 * (col & 1), e = (ch & 1) * JC + (col >> 1);
+    const int hc = col & 1;
+    const int l = (ch >> 1) + 32 * hc, e = ((ch & 1) ^ hc) * JC + (col >> 1);
     const int a = ((e >> 2) * 65 + l) * 4 + (e & 3);
     kkt[select_lanes(valid, a, 64 * 4)] = 0.5f - tmap16(bits);
   });
@@ -236,24 +241,23 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
   // Each wave completes its own rows (its LDS operations are performed in
   // order, so its row loop below sees them without another barrier).
   if (lane < rows) {
-    // Row sum of g (half of the sum of the staged 2g) into slot JC of both
-    // halves, read as 16-byte groups; an odd M's missing column of half 1
-    // (slot JC - 1) is zeroed.
+    // Each half's sum of g (half of the sum of its staged 2g) into its slot JC,
+    // read as 16-byte groups; an odd M's missing column of half 1 (slot JC - 1)
+    // is zeroed.
     float* rp = rowsA + (w0 + lane) * PITCH;
     if (DQ) {
-      float s2 = 0.0f;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int cols = hh == 0 ? JC : M - JC;
+        float s2 = 0.0f;
 #pragma unroll
         for (int g = 0; g * 4 < cols; ++g) {
           const float4 a = *reinterpret_cast<const float4*>(rp + hh * HP + 4 * g);
           const float b = (4 * g + 1 < cols ? a.x + a.y : a.x) + (4 * g + 3 < cols ? a.z + a.w : 4 * g + 2 < cols ? a.z : 0.0f);
           s2 += b;
         }
+        rp[hh * HP + JC] = 0.5f * s2;
       }
-      rp[JC] = 0.5f * s2;
-      rp[HP + JC] = 0.5f * s2;
     }
     if (M % 2) rp[HP + JC - 1] = 0.0f;
   }
@@ -304,9 +308,11 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
     const uint16_t* q3 = uniform_ptr(qsl + (size_t)(P0 + w0 + kB2Unroll - 1) * C);
     const uint16_t* ql = uniform_ptr(qsl + (size_t)(P0 + w1 - 1) * C);
     uint16_t* dqrow = uniform_ptr(reinterpret_cast<uint16_t*>(dq) + ((size_t)bh * N + P0 + w0) * C + cb * 64);
+    // Bit offsets of the lane's channels in a query pair (own channel 2p + h first).
+    const unsigned shf[4] = {16u * h, 16u * h + 15u, 16u - 16u * h, 31u - 16u * h};
     B2Rows<T, M, DQ, DK>::run(dk, q3, ql, dqrow, (unsigned)C * 2, rows, (unsigned)uniform(wave >= 4 ? 1 : 0), rda,
                               (unsigned)p * 4, (unsigned)(2 * p + h) * 2, ldsBase + S.kk_off() + (unsigned)lane * 16,
-                              q0);
+                              (unsigned)(lane ^ 32) * 4, shf, q0);
   }
   if constexpr (!DK) return;
 
@@ -322,8 +328,8 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
       const int col = 2 * j + h;
       if (col < M) {
         const float cs = 0.5f * colsum[wave * M + col];
-        buf[col * 65 + 2 * p] = cs - dk[j];
-        buf[col * 65 + 2 * p + 1] = cs - dk[JC + j];
+        buf[col * 65 + 2 * p + h] = cs - dk[j];            // own channel
+        buf[col * 65 + 2 * p + 1 - h] = cs - dk[JC + j];   // partner's channel
       }
     }
   }
