@@ -28,6 +28,8 @@ inline void NewtonInverse_forward(const at::Tensor mat, at::Tensor output, int64
 inline void NewtonInverse_backward(const at::Tensor grad_output, const at::Tensor inverse, at::Tensor grad_mat) {
   TORCH_CHECK(grad_output.is_cuda() && inverse.is_cuda(), "tensors must be on GPU");
   TORCH_CHECK(grad_output.dim() == 4 && inverse.dim() == 4, "must be 4D");
+  // (Not in the reference: the kernels read and write B*H*N*N elements.)
+  TORCH_CHECK(inverse.size(-1) == inverse.size(-2), "last two dims of inverse must be equal");
 #if defined(WITH_HIP)
   NewtonInverse_backward_cuda(grad_output, inverse, grad_mat);
 #else

@@ -34,6 +34,10 @@ SHAPES = [
     # Odd M beyond the register-resident set: column blocks with 16-bit rows of odd length.
     (1, 2, 77, 81, 64),
     (2, 1, 50, 225, 40),
+    # M > 256: the multi-block backward (16-bit grad staging, dq over several column
+    # blocks), with full and partial channel blocks.
+    (1, 1, 70, 300, 64),
+    (1, 2, 33, 260, 40),
 ]
 DTYPES = ["f32", "f16", "bf16", "f64"]
 
@@ -132,7 +136,7 @@ def test_laplace_config4_sampled(gpu):
     assert torch.equal(dq.cpu(), dq2.cpu())
 
 
-@pytest.mark.parametrize("dt", ["f32", "f16", "f64"])
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16", "f64"])
 def test_reduce_forward(gpu, dt):
     import laplacianformer_amd as lf
 
@@ -142,8 +146,90 @@ def test_reduce_forward(gpu, dt):
         out = torch.empty((B, H, N, M), dtype=q.dtype, device=gpu)
         lf.ext().LaplaceSubtraction_reduce_forward(q.to(gpu), k.to(gpu), out)
         ref = oracle.laplace_reduce_forward(q, k, dt)
-        got = out.cpu().numpy()
-        assert np.array_equal(got.astype(np.float64), np.asarray(ref, dtype=np.float64)), (dt, C)
+        got = out.cpu().to(torch.float64).numpy()
+        assert np.array_equal(got, np.asarray(ref, dtype=np.float64)), (dt, C)
+
+
+# Non-finite inputs in the backward (M = 49, C = 64: the 16-bit column-split
+# kernel for fp16 / bf16, the clamped-step kernel for fp32). Rows 0-7 of channel 3
+# and rows 8-15 of channel 5 hold +inf / -inf, as do key columns 0-4 of channel 3
+# and 10-14 of channel 5, so those pairs are infinite ties; rows 20 / 21 of
+# channels 7 / 9 hold NaN of either sign.
+#  * 16-bit: the order-preserving image of the patterns makes an infinite tie an
+#    exact tie (sgn 0, as the reference's sign of inf - inf = NaN), and orders a
+#    NaN pattern beyond the infinity of its sign (sgn +-1 against every key; the
+#    reference gives 0) -- the oracle is run with the NaN replaced by a finite
+#    value beyond every key of its channel.
+#  * fp32: sgn of a NaN difference (a NaN input or an infinite tie) is -1 (the
+#    clamp of NaN is 0); the reference gives 0 -- the oracle is run with each
+#    infinity replaced by a finite value that keeps every comparison but makes the
+#    ties q < k, and the NaN by a value below every key.
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_laplace_nonfinite_backward(gpu, dt):
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = 1, 1, 64, 49, 64
+    print(f"laplace non-finite backward {dt}", flush=True)
+    q, k, g = _inputs(B, H, N, M, C, dt, seed=91)
+    q = q.float()
+    k = k.float()
+    q[..., 0:8, 3] = float("inf")
+    q[..., 8:16, 5] = float("-inf")
+    k[..., 3, 0:5] = float("inf")
+    k[..., 5, 10:15] = float("-inf")
+    q[..., 20, 7] = float("nan")
+    q[..., 21, 9] = -float("nan") if dt != "f32" else float("nan")
+    qd, kd = q.to(TORCH_DT[dt]), k.to(TORCH_DT[dt])
+    L = lf.ext()
+    dq = torch.empty_like(qd, device=gpu)
+    dk = torch.empty_like(kd, device=gpu)
+    L.LaplaceSubtraction_backward(g.to(gpu), qd.to(gpu), kd.to(gpu), dq, dk)
+    torch.cuda.synchronize()
+    qr, kr = q.double().clone(), k.double().clone()
+    big = 1.0e30
+    if dt != "f32":
+        # The NaN's sign is that of its 16-bit pattern (the cast may not keep the
+        # fp32 sign: torch rounds fp32 NaN to bf16 0xffff).
+        for i, c in ((20, 7), (21, 9)):
+            neg = qd[0, 0, i, c].view(torch.int16).item() < 0
+            qr[..., i, c] = -big if neg else big
+    else:
+        qr[qr == float("inf")] = big
+        qr[qr == float("-inf")] = -2 * big
+        kr[kr == float("inf")] = 2 * big
+        kr[kr == float("-inf")] = -big
+        qr[torch.isnan(qr)] = -4 * big
+    refs = l1_refs(qr, kr, g.double(), "f64")
+    assert_l1_close(dq, refs["dq"][0], dt, f"{dt} dq non-finite", refs["dq"][1])
+    assert_l1_close(dk, refs["dk"][0], dt, f"{dt} dk non-finite", refs["dk"][1])
+
+
+@pytest.mark.parametrize("M", [49, 300])
+def test_laplace_misaligned_grad(gpu, M):
+    """fp16 grad_output that is a contiguous view at an odd element offset (its
+    data is 2-byte but not 4-byte aligned): the backward kernels that read
+    grad rows as 4-byte words must not be chosen; results match the oracle."""
+    import laplacianformer_amd as lf
+
+    B, H, N, C = 1, 2, 90, 64
+    print(f"laplace misaligned grad M={M}", flush=True)
+    q, k, g = _inputs(B, H, N, M, C, "f16", seed=17 + M)
+    buf = torch.empty(g.numel() + 1, dtype=torch.float16, device=gpu)
+    buf[1:] = g.reshape(-1).to(gpu)
+    gd = buf[1:].view(g.shape)
+    assert gd.is_contiguous() and gd.storage_offset() == 1
+    L = lf.ext()
+    qd, kd = q.to(gpu), k.to(gpu)
+    dq, dk = torch.empty_like(qd), torch.empty_like(kd)
+    dq1, dk1 = torch.empty_like(qd), torch.empty_like(kd)
+    L.LaplaceSubtraction_backward(gd, qd, kd, dq, dk)
+    L.LaplaceSubtraction_backward_query(gd, qd, kd, dq1)
+    L.LaplaceSubtraction_backward_key(gd, qd, kd, dk1)
+    torch.cuda.synchronize()
+    refs = l1_refs(q, k, g, "f16")
+    for tag, a, b in (("fused", dq, dk), ("separate", dq1, dk1)):
+        assert_l1_close(a, refs["dq"][0], "f16", f"{tag} dq", refs["dq"][1])
+        assert_l1_close(b, refs["dk"][0], "f16", f"{tag} dk", refs["dk"][1])
 
 
 def test_empty_and_errors(gpu):

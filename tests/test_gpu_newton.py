@@ -50,15 +50,31 @@ def test_newton_forward_dtypes(gpu, dt, n):
 def test_newton_backward(gpu, dt, n):
     import laplacianformer_amd as lf
 
-    if dt == "f64" and n > 96:
-        pytest.skip("fp64 envelope is n <= 96")
     print(f"newton backward {dt} n={n}", flush=True)
     V = gen((2, 2, n, n), 7 + n, dt, scale=0.3)
     G = gen((2, 2, n, n), 8 + n, dt)
     out = torch.empty_like(V, device=gpu)
+    if dt == "f64" and n > 96:
+        # Outside the fp64 envelope (two fp64 n x n buffers per workgroup in LDS):
+        # the documented rejection, before any launch.
+        with pytest.raises(RuntimeError, match="fp64"):
+            lf.ext().NewtonInverse_backward(G.to(gpu), V.to(gpu), out)
+        return
     lf.ext().NewtonInverse_backward(G.to(gpu), V.to(gpu), out)
     ref = oracle.newton_backward(G, V, dt)
     assert_newton_close(out, ref, dt, f"bwd {dt} n={n}", rtol=1e-5 if dt != "f64" else 1e-12)
+
+
+def test_newton_backward_not_square(gpu):
+    """A non-square inverse is rejected before any launch (the kernels would read
+    and write B*H*N*N elements of [B, H, N, K] tensors)."""
+    import laplacianformer_amd as lf
+
+    V = torch.zeros((1, 2, 8, 5), device=gpu)
+    G = torch.zeros((1, 2, 8, 5), device=gpu)
+    out = torch.empty((1, 2, 8, 5), device=gpu)
+    with pytest.raises(RuntimeError, match="last two dims of inverse must be equal"):
+        lf.ext().NewtonInverse_backward(G, V, out)
 
 
 def test_newton_config3(gpu):
