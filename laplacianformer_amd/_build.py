@@ -107,7 +107,9 @@ def build_torch_ext(verbose=False, jobs=4):
     _run(["g++", "-shared", "-fPIC", "-o", tmp, *objs,
           f"-L{PKG_DIR}", "-llfamd", f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
           "-ltorch_hip", "-ltorch_python", "-lamdhip64",
-          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"], verbose)
+          # $ORIGIN: next to liblfamd.so inside the package; $ORIGIN/laplacianformer_amd:
+          # the same file installed as the top-level module next to the package (setup.py).
+          "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/laplacianformer_amd", f"-Wl,-rpath,{libdir}"], verbose)
     os.replace(tmp, EXT_PATH)
     return EXT_PATH
 
@@ -116,6 +118,27 @@ def build(verbose=False):
     """Compile both libraries (always recompiles)."""
     build_hip(verbose)
     build_torch_ext(verbose)
+    return LIB_PATH, EXT_PATH
+
+
+def _newest(paths):
+    return max((os.path.getmtime(p) for p in paths if os.path.exists(p)), default=0.0)
+
+
+def build_if_stale(verbose=False):
+    """Compile what is missing or older than its sources (setup.py's build step)."""
+    hip_inputs = [os.path.join(CSRC, f) for f in os.listdir(CSRC)
+                  if f.endswith((".hip", ".h", ".py")) and f != "l1_asm_gen.h"]
+    hip_inputs.append(os.path.join(REPO_DIR, "include", "laplacianformer_amd.h"))
+    hip_inputs.append(os.path.abspath(__file__))
+    if not os.path.exists(LIB_PATH) or os.path.getmtime(LIB_PATH) < _newest(hip_inputs):
+        build_hip(verbose)
+    tdir = os.path.join(CSRC, "torch")
+    torch_inputs = [os.path.join(tdir, f) for f in os.listdir(tdir) if f.endswith(".cpp")]
+    torch_inputs += [os.path.join(tdir, "include", f) for f in os.listdir(os.path.join(tdir, "include"))]
+    torch_inputs += [LIB_PATH, os.path.abspath(__file__)]
+    if not os.path.exists(EXT_PATH) or os.path.getmtime(EXT_PATH) < _newest(torch_inputs):
+        build_torch_ext(verbose)
     return LIB_PATH, EXT_PATH
 
 
