@@ -89,6 +89,21 @@ int lfamd_laplace_backward(int dtype, const void* grad_output, const void* query
                            int64_t channels, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* lfamd_laplace_backward without a workspace argument and without allocating:
+ * the grad_key partials live in a static device array of
+ * lfamd_laplace_backward_noalloc_limit() bytes (8 MiB) that each GPU holds until
+ * the process ends; sizes needing more workspace return LFAMD_ERR_UNSUPPORTED.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (HIP graph capture, serving loops, harnesses forbidding hipMalloc).
+ * Calls that overlap on one GPU share the array and race. */
+int lfamd_laplace_backward_noalloc(int dtype, const void* grad_output, const void* query,
+                                   const void* key, void* grad_query, void* grad_key,
+                                   int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,
+                                   int64_t channels, void* stream);
+
+/* Bytes of the static scratch of lfamd_laplace_backward_noalloc. */
+size_t lfamd_laplace_backward_noalloc_limit(void);
+
 /* Legacy "reduce" forward: the same distance, accumulated in the element type
  * by min(C,256) partial sums folded by a halving tree, exactly as the reference
  * kernel does (including its behaviour when min(C,256) is not a power of two).

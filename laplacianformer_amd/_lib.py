@@ -32,6 +32,8 @@ CAPI_PROTOTYPES = [
     ("lfamd_laplace_backward_key", _I, [_I, _P, _P, _P, _P] + _DIMS + [_P, _SZ, _P]),
     ("lfamd_laplace_backward", _I, [_I, _P, _P, _P, _P, _P] + _DIMS + [_P, _SZ, _P]),
     ("lfamd_laplace_reduce_forward", _I, [_I, _P, _P, _P] + _DIMS + [_P]),
+    ("lfamd_laplace_backward_noalloc", _I, [_I, _P, _P, _P, _P, _P] + _DIMS + [_P]),
+    ("lfamd_laplace_backward_noalloc_limit", _SZ, []),
     ("lfamd_laplace_kernel_forward", _I, [_I, _P, _P, _P] + _DIMS + [ctypes.c_float, _P]),
     ("lfamd_laplace_kernel_backward", _I, [_I, _P, _P, _P, _P, _P, _P] + _DIMS + [ctypes.c_float, _P, _SZ, _P]),
     ("lfamd_newton_workspace_size", _SZ, [_I, _I64, _I64]),
