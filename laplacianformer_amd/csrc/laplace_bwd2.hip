@@ -27,16 +27,17 @@
 // grad_query is that of channel 2p + h (the other column half's partial comes
 // from lane (1 - h, p)).
 //
-// The workgroup stages its grad rows in LDS in one pass: 4-byte loads, all in
-// flight at once, scattered as 2g in fp32 to row r, half h = col % 2, slot
-// col / 2 (so consecutive lanes write consecutive LDS words), each half 16-byte
-// aligned with that half's sum of g in slot JC. Each wave then adds the half-row
-// sums and column sums of its own rows and runs its row loop: the generated asm
-// block of l1_asm_gen.h, in which every 16-byte wave-wide grad read (two
-// addresses, one per half) feeds 24 VALU instructions (two channels x four
-// columns x three), query rows are prefetched four rows ahead, and the T(q) of
-// the next row and the grad_query of the previous row are interleaved with the
-// current row's arithmetic.
+// The workgroup stages the key terms in LDS (the only barrier before the row
+// loops); each wave stages its own grad rows: one 2-byte load per lane per row
+// (lane = column), all in flight at once, written as 2g in fp32 to row r, half
+// h = col % 2, slot col / 2 (consecutive lanes write consecutive LDS words),
+// each half 16-byte aligned with that half's sum of g in slot JC. The wave
+// then adds the half-row sums and column sums of its rows and runs its row
+// loop: the generated asm block of l1_asm_gen.h, in which every 16-byte
+// wave-wide grad read (two addresses, one per half) feeds 24 VALU instructions
+// (two channels x four columns x three), query rows are prefetched four rows
+// ahead, and the T(q) of the next row and the grad_query of the previous row
+// are interleaved with the current row's arithmetic.
 //
 // grad_key: per wave, half its column sums of 2g minus its accumulated 2g y,
 // summed over the waves in LDS in wave order; the workgroup partials of a slice
@@ -190,20 +191,30 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
 
   const int P0 = (int)((int64_t)x * N / nx), P1 = (int)((int64_t)(x + 1) * N / nx);
   const int n = P1 - P0;
-  const int nm = n * M;
   const uint16_t* qsl = reinterpret_cast<const uint16_t*>(query) + (size_t)bh * N * C + cb * 64;
 
-  // All loads first: the key block [64][M] of the channel block, the grad rows
-  // (n*M contiguous elements) and the first query pairs of this wave's row loop.
+  // All loads first: the key block [64][M] of the channel block (the whole
+  // workgroup), this wave's own grad rows (lane = column: RPI rows of M
+  // columns per load) and the first query pairs of its row loop.
   constexpr int kKeyW = (64 * M + 2 + 2 * kB2Threads - 1) / (2 * kB2Threads);
   uint32_t kwd[kKeyW];
   const int kskew = load_words(reinterpret_cast<const uint16_t*>(key) + ((size_t)bh * C + cb * 64) * M, 64 * M, tid, kwd);
-  constexpr int kRowW = (kB2MaxRows * M + 2 + 2 * kB2Threads - 1) / (2 * kB2Threads);
-  uint32_t gwd[kRowW];
-  const int gskew = load_words(reinterpret_cast<const uint16_t*>(gout) + ((size_t)bh * N + P0) * M, nm, tid, gwd);
   const int w0 = uniform((int)((int64_t)wave * n / kB2Waves)), w1 = uniform((int)((int64_t)(wave + 1) * n / kB2Waves));
   const int rows = w1 - w0;  // at most kB2MaxRows / kB2Waves = 64
   const int h = lane >> 5, p = lane & 31;
+  constexpr int RPI = 64 / M;                                         // rows per load instruction
+  constexpr int kOwnLoads = (kB2MaxRows / kB2Waves + RPI - 1) / RPI;
+  const int lrow = lane / M, lcol = lane - lrow * M;
+  uint16_t gv[kOwnLoads];
+  {
+    // Unconditional loads, the row clamped to the wave's last (its first when
+    // it has none, w0 < n): a clamped lane holds the value of the row it is
+    // later stored to, so the stores need no lane mask.
+    const uint16_t* gw = reinterpret_cast<const uint16_t*>(gout) + ((size_t)bh * N + P0 + w0) * M + lcol;
+    const int rlast = max(rows, 1) - 1;
+#pragma unroll
+    for (int i = 0; i < kOwnLoads; ++i) gv[i] = gw[(size_t)min(i * RPI + lrow, rlast) * M];
+  }
   unsigned q0[kB2Unroll];
   {
     const uint32_t* qpair = reinterpret_cast<const uint32_t*>(qsl + (size_t)(P0 + w0) * C) + p;
@@ -229,17 +240,21 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
       kkt[(((2 * JC - 1) >> 2) * 65 + tid) * 4 + ((2 * JC - 1) & 3)] = 0.0f;
     }
   }
-  // Grad rows as 2g: column col of row r at rowsA[r*PITCH + (col % 2)*HP + col / 2].
-  // (Invalid elements go to slot 0 of the spare row n.)
-  scatter_words<M>(gwd, gskew, nm, tid, [&](int row, int col, bool valid, uint16_t bits) {
-    const float v = g2f<T>(bits);
-    const int a = __mul24(row, PITCH) + (col & 1) * HP + (col >> 1);
-    rowsA[select_lanes(valid, a, n * PITCH)] = v + v;
-  });
-  __syncthreads();
+  __syncthreads();  // the key-term table is complete
 
-  // Each wave completes its own rows (its LDS operations are performed in
-  // order, so its row loop below sees them without another barrier).
+  // Each wave stages and completes its own rows (its LDS operations are
+  // performed in order, so its row loop below sees them without a barrier).
+  // Grad rows as 2g: column col of row r at rowsA[r*PITCH + (col % 2)*HP + col / 2].
+  {
+    float* dst = rowsA + w0 * PITCH + (lcol & 1) * HP + (lcol >> 1);
+#pragma unroll
+    for (int i = 0; i < kOwnLoads; ++i) {
+      if (i * RPI < rows) {  // wave-uniform; lanes past the last row rewrite it with its own value
+        const float v = g2f<T>(gv[i]);
+        dst[min(i * RPI + lrow, rows - 1) * PITCH] = v + v;
+      }
+    }
+  }
   if (lane < rows) {
     // Each half's sum of g (half of the sum of its staged 2g) into its slot JC,
     // read as 16-byte groups; an odd M's missing column of half 1 (slot JC - 1)
