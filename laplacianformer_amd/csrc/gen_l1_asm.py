@@ -65,10 +65,10 @@ class Regs:
 def shape(M):
     """(JC, HP, NG, PITCH): columns per lane half, LDS slots per half row (JC
     columns, the row sum, padding to 16 bytes), 16-byte groups per half row,
-    floats per staged row."""
+    floats per staged row (both halves and 16 bytes of bank padding)."""
     JC = (M + 1) // 2
     HP = ((JC + 1 + 3) // 4) * 4
-    return JC, HP, HP // 4, 2 * HP
+    return JC, HP, HP // 4, 2 * HP + 4
 
 
 def variant(dtype, M, DQ=True, DK=True):

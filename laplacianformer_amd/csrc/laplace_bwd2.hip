@@ -62,7 +62,7 @@ constexpr int kB2Threads = 64 * kB2Waves;
 struct B2Shape {
   int M, JC, HP, PITCH, NKK;
   __host__ __device__ constexpr B2Shape(int m)
-      : M(m), JC((m + 1) / 2), HP((((m + 1) / 2) + 1 + 3) / 4 * 4), PITCH(2 * ((((m + 1) / 2) + 1 + 3) / 4 * 4)),
+      : M(m), JC((m + 1) / 2), HP((((m + 1) / 2) + 1 + 3) / 4 * 4), PITCH(2 * ((((m + 1) / 2) + 1 + 3) / 4 * 4) + 4),
         NKK((2 * ((m + 1) / 2) + 3) / 4) {}
   // LDS: the waves' column sums of 2g [kB2Waves][M] | key-term table
   // [NKK][65][4] (lane-major 16-byte groups, one spare group per table row so
@@ -244,16 +244,30 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
 
   // Each wave stages and completes its own rows (its LDS operations are
   // performed in order, so its row loop below sees them without a barrier).
-  // Grad rows as 2g: column col of row r at rowsA[r*PITCH + (col % 2)*HP + col / 2].
+  // Grad rows as 2g: column col of row r at rowsA[r*PITCH + (col % 2)*HP + col / 2]
+  // (the row pitch is 16 bytes more than the two halves, so that lanes reading
+  // consecutive rows spread over the banks). The column sums of 2g over the
+  // wave's rows are taken from the same registers, in row order.
+  float csum = 0.0f;
   {
     float* dst = rowsA + w0 * PITCH + (lcol & 1) * HP + (lcol >> 1);
 #pragma unroll
     for (int i = 0; i < kOwnLoads; ++i) {
       if (i * RPI < rows) {  // wave-uniform; lanes past the last row rewrite it with its own value
         const float v = g2f<T>(gv[i]);
-        dst[min(i * RPI + lrow, rows - 1) * PITCH] = v + v;
+        const int r = i * RPI + lrow;
+        dst[min(r, rows - 1) * PITCH] = v + v;
+        if (DK) csum += r < rows ? v + v : 0.0f;
       }
     }
+  }
+  if (DK) {
+    // Lanes lcol + M t (t < 64 / M) hold the same column when M divides 64.
+    if constexpr (64 % M == 0) {
+#pragma unroll
+      for (int m = M; m < 64; m <<= 1) csum += __shfl_xor(csum, m);
+    }
+    if (lane < M) colsum[wave * M + lane] = csum;
   }
   if (lane < rows) {
     // Each half's sum of g (half of the sum of its staged 2g) into its slot JC,
@@ -275,45 +289,6 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
       }
     }
     if (M % 2) rp[HP + JC - 1] = 0.0f;
-  }
-  if (DK) {
-    // Column sums of 2g over the wave's rows: lane (group, r) sums the 4-column
-    // group `group` of rows w0 + r, w0 + r + RQ, ...; then a fixed butterfly
-    // over the RQ lanes of the group.
-    constexpr int NG0 = (JC + 3) / 4, NG1 = (M - JC + 3) / 4, NGT = NG0 + NG1;
-    constexpr int RQ = NGT <= 4 ? 16 : NGT <= 8 ? 8 : NGT <= 16 ? 4 : NGT <= 32 ? 2 : 1;
-    static_assert(NGT * RQ <= 64, "column groups of a wave");
-    const int grp = lane / RQ, r = lane % RQ;
-    const int hh = grp >= NG0 ? 1 : 0;
-    const int g = grp - hh * NG0;
-    float4 a = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (grp < NGT) {
-      const float* cp = rowsA + (w0 + r) * PITCH + hh * HP + 4 * g;
-#pragma unroll
-      for (int k = 0; k < (kB2MaxRows / kB2Waves + RQ - 1) / RQ; ++k) {
-        if (r + k * RQ < rows) {
-          const float4 v = *reinterpret_cast<const float4*>(cp + k * RQ * PITCH);
-          a.x += v.x;
-          a.y += v.y;
-          a.z += v.z;
-          a.w += v.w;
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 1; m < RQ; m <<= 1) {
-      a.x += __shfl_xor(a.x, m);
-      a.y += __shfl_xor(a.y, m);
-      a.z += __shfl_xor(a.z, m);
-      a.w += __shfl_xor(a.w, m);
-    }
-    if (grp < NGT && r == 0) {
-      const int cols = hh == 0 ? JC : M - JC;
-      const float v4[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (4 * g + k < cols) colsum[wave * M + 2 * (4 * g + k) + hh] = v4[k];
-    }
   }
   float dk[2 * JC];
 #pragma unroll
