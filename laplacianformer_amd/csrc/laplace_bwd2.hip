@@ -169,10 +169,15 @@ __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int sk
 // Grid: (nx workgroups per slice, channel blocks, B*H). Workgroup x takes rows
 // [x*N/nx, (x+1)*N/nx) of its slice, at most kB2MaxRows of them (the host
 // plan sizes nx for that), split evenly over the 8 waves.
-template <typename T, int M, bool DQ, bool DK>
+//
+// GK: the gradient is that of the fused Laplacian kernel K = exp(-s * distance)
+// (fp32 gk = dL/dK and kv = K instead of gout): the staged 2g is
+// (-2s * gk) * kv, i.e. 2 * fl(fl(-s * gk) * kv) exactly.
+template <typename T, int M, bool DQ, bool DK, bool GK = false>
 __global__ void __launch_bounds__(kB2Threads, 1)
-laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, const T* __restrict__ key,
-                    T* __restrict__ dq, float* __restrict__ partial, int N, int C) {
+laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, const float* __restrict__ kv,
+                    float gscale, const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ dq,
+                    float* __restrict__ partial, int N, int C) {
   constexpr B2Shape S{M};
   constexpr int JC = S.JC, HP = S.HP, PITCH = S.PITCH, NKK = S.NKK;
   static_assert(M >= 2, "M >= 2");
@@ -205,15 +210,38 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
   constexpr int RPI = 64 / M;                                         // rows per load instruction
   constexpr int kOwnLoads = (kB2MaxRows / kB2Waves + RPI - 1) / RPI;
   const int lrow = lane / M, lcol = lane - lrow * M;
-  uint16_t gv[kOwnLoads];
+  uint16_t gv[GK ? 1 : kOwnLoads];
+  float ga[GK ? kOwnLoads : 1], ka[GK ? kOwnLoads : 1];
   {
     // Unconditional loads, the row clamped to the wave's last (its first when
     // it has none, w0 < n): a clamped lane holds the value of the row it is
     // later stored to, so the stores need no lane mask.
-    const uint16_t* gw = reinterpret_cast<const uint16_t*>(gout) + ((size_t)bh * N + P0 + w0) * M + lcol;
+    const size_t e0 = ((size_t)bh * N + P0 + w0) * M + lcol;
     const int rlast = max(rows, 1) - 1;
+    if constexpr (GK) {
+      // Two fp32 loads per element: the first half of the rows is combined
+      // into 2g before the second half is loaded (the register file holds
+      // one half's pairs at a time).
 #pragma unroll
-    for (int i = 0; i < kOwnLoads; ++i) gv[i] = gw[(size_t)min(i * RPI + lrow, rlast) * M];
+      for (int i = 0; i < kOwnLoads / 2; ++i) {
+        const size_t e = e0 + (size_t)min(i * RPI + lrow, rlast) * M;
+        ga[i] = gk[e];
+        ka[i] = kv[e];
+      }
+#pragma unroll
+      for (int i = 0; i < kOwnLoads / 2; ++i) ga[i] = (-2.0f * gscale * ga[i]) * ka[i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = kOwnLoads / 2; i < kOwnLoads; ++i) {
+        const size_t e = e0 + (size_t)min(i * RPI + lrow, rlast) * M;
+        ga[i] = gk[e];
+        ka[i] = kv[e];
+      }
+    } else {
+      const uint16_t* gw = reinterpret_cast<const uint16_t*>(gout) + e0;
+#pragma unroll
+      for (int i = 0; i < kOwnLoads; ++i) gv[i] = gw[(size_t)min(i * RPI + lrow, rlast) * M];
+    }
   }
   unsigned q0[kB2Unroll];
   {
@@ -254,10 +282,16 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const T* __restrict__ query, con
 #pragma unroll
     for (int i = 0; i < kOwnLoads; ++i) {
       if (i * RPI < rows) {  // wave-uniform; lanes past the last row rewrite it with its own value
-        const float v = g2f<T>(gv[i]);
+        float v2;
+        if constexpr (GK) {
+          v2 = i < kOwnLoads / 2 ? ga[i] : (-2.0f * gscale * ga[i]) * ka[i];
+        } else {
+          const float v = g2f<T>(gv[i]);
+          v2 = v + v;
+        }
         const int r = i * RPI + lrow;
-        dst[min(r, rows - 1) * PITCH] = v + v;
-        if (DK) csum += r < rows ? v + v : 0.0f;
+        dst[min(r, rows - 1) * PITCH] = v2;
+        if (DK) csum += r < rows ? v2 : 0.0f;
       }
     }
   }
@@ -381,11 +415,16 @@ B2Plan plan_b2(int64_t BH, int64_t N, int64_t M, int64_t C) {
 
 template <typename T, int M, bool DQ, bool DK>
 int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, int64_t BH, int64_t N,
-                int64_t C, const B2Plan& p, hipStream_t st) {
+                int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg) {
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
-  hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK>), grid, dim3(kB2Threads), p.lds, st, static_cast<const T*>(g),
-                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<T*>(dq),
-                     static_cast<float*>(ws), (int)N, (int)C);
+  if (kg.gk)
+    hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(kB2Threads), p.lds, st,
+                       static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)N, (int)C);
+  else
+    hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, false>), grid, dim3(kB2Threads), p.lds, st,
+                       static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)N, (int)C);
   int s = check_launch("laplace backward (column-split)");
   if (s || !DK) return s;
   dim3 rgrid((64 * M + 255) / 256, p.ncb, (unsigned)BH);
@@ -396,19 +435,19 @@ int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk,
 
 template <typename T, bool DQ, bool DK>
 int launch_b2_t(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, int64_t BH, int64_t N,
-                int64_t M, int64_t C, const B2Plan& p, hipStream_t st) {
+                int64_t M, int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg) {
   switch (M) {
-    case 16: return launch_b2_m<T, 16, DQ, DK>(g, q, k, dq, dk, ws, BH, N, C, p, st);
-    case 32: return launch_b2_m<T, 32, DQ, DK>(g, q, k, dq, dk, ws, BH, N, C, p, st);
-    default: return launch_b2_m<T, 49, DQ, DK>(g, q, k, dq, dk, ws, BH, N, C, p, st);
+    case 16: return launch_b2_m<T, 16, DQ, DK>(g, q, k, dq, dk, ws, BH, N, C, p, st, kg);
+    case 32: return launch_b2_m<T, 32, DQ, DK>(g, q, k, dq, dk, ws, BH, N, C, p, st, kg);
+    default: return launch_b2_m<T, 49, DQ, DK>(g, q, k, dq, dk, ws, BH, N, C, p, st, kg);
   }
 }
 
 template <bool DQ, bool DK>
 int launch_b2(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, int64_t BH,
-              int64_t N, int64_t M, int64_t C, const B2Plan& p, hipStream_t st) {
-  if (dtype == LFAMD_BF16) return launch_b2_t<bf16s, DQ, DK>(g, q, k, dq, dk, ws, BH, N, M, C, p, st);
-  return launch_b2_t<f16s, DQ, DK>(g, q, k, dq, dk, ws, BH, N, M, C, p, st);
+              int64_t N, int64_t M, int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg) {
+  if (dtype == LFAMD_BF16) return launch_b2_t<bf16s, DQ, DK>(g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
+  return launch_b2_t<f16s, DQ, DK>(g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
 }
 
 }  // namespace
@@ -429,13 +468,14 @@ size_t b2_workspace_elems(int64_t BH, int64_t N, int64_t M, int64_t C) {
 }
 
 int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, size_t wsBytes,
-              int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who) {
+              int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who, const B2Grad& kg) {
   const B2Plan p = plan_b2(BH, N, M, C);
   if (dk && (!ws || wsBytes < p.partialElems * 4))
     return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, p.partialElems * 4, wsBytes);
-  if (dq && dk) return launch_b2<true, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st);
-  if (dq) return launch_b2<true, false>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st);
-  return launch_b2<false, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st);
+  if (kg.gk && dtype != LFAMD_F16) return fail(LFAMD_ERR_UNSUPPORTED, "%s: fused kernel gradient needs fp16", who);
+  if (dq && dk) return launch_b2<true, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
+  if (dq) return launch_b2<true, false>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
+  return launch_b2<false, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
 }
 
 }  // namespace lfamd

@@ -1939,6 +1939,9 @@ int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const flo
                 (long long)d.N, (long long)d.M);
   if (!grad_kernel || !kernel || !query || !key) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (b2_ok(dtype, d.BH(), d.N, d.M, d.C) && (reinterpret_cast<uintptr_t>(query) & 3) == 0)
+    return b2_launch(dtype, nullptr, query, key, grad_query, grad_key, workspace, workspace_bytes, d.BH(), d.N, d.M,
+                     d.C, st, who, B2Grad{grad_kernel, kernel, scale});
   const KernGrad kg{grad_kernel, kernel, scale};
   if (!kernel_bwd_bcast(d)) {
     const MbPlan mp = plan_mb(d, doDk);

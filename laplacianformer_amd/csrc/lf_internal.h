@@ -25,10 +25,18 @@ int max_lds_bytes();
 int num_cus();
 
 // Column-split fused backward of 16-bit LaplaceSubtraction (laplace_bwd2.hip).
+// With B2Grad::gk set, the gradient is that of the fused kernel exp(-scale * distance):
+// fp32 gk = dL/dK and kv = K replace g (fp16 only).
+struct B2Grad {
+  const float* gk = nullptr;
+  const float* kv = nullptr;
+  float scale = 0.0f;
+};
 bool b2_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C);
 size_t b2_workspace_elems(int64_t BH, int64_t N, int64_t M, int64_t C);
 int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, size_t wsBytes,
-              int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who);
+              int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who,
+              const B2Grad& kg = B2Grad{});
 
 // Row-staged forward of LaplaceSubtraction at M = 49 (laplace_fwd2.hip); kernelEpi:
 // exp(-scale * distance) in fp32 instead of the distance in the element type.
