@@ -192,6 +192,18 @@ int lfamd_mix_rows(int dtype, const void* a, const float* b, int c_dtype, void* 
                    int64_t rows, int inner, int cols, int64_t b_col_stride, int64_t b_inner_stride,
                    int64_t b_slice_stride, void* stream);
 
+/* Bytes of workspace lfamd_tall_t needs for these sizes (per-workgroup fp32 partials). */
+size_t lfamd_tall_t_workspace_size(int64_t slices, int64_t rows);
+
+/* c[s][p][q] = sum_{n < rows} a[s][n][p] * b[s][n][q] for s < slices, p < inner, q < cols:
+ * a fp32 [slices][rows][inner], b of element type `b_dtype` (F32, F16 or BF16, used as fp32)
+ * [slices][rows][cols], c fp32 [slices][inner][cols], all contiguous; inner, cols <= 64
+ * (LFAMD_ERR_UNSUPPORTED beyond). Summed in fp32 over per-workgroup row ranges, then over the
+ * workgroups in a fixed order (deterministic). No reference counterpart: the attention layer's
+ * K_km^T.V and K_qm^T.grad_out (the reference leaves the layer to its caller). */
+int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t slices, int64_t rows,
+                 int inner, int cols, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Runtime ------------------------------------------------------------ */
 
 /* HIP runtime version as major*100 + minor (e.g. 700 for 7.0), the convention

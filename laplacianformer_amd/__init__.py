@@ -9,11 +9,11 @@ from .attention import LaplacianAttention, laplacian_attention
 from .graphs import GraphedStep
 from .functional import (LaplaceKernelFunction, LaplaceSubtractionFunction, NewtonInverseFunction,
                          TallMixFunction, TallProductFunction, laplace_kernel, laplace_subtraction, mix_rows,
-                         newton_inverse, tall_mix, tall_product)
+                         newton_inverse, tall_mix, tall_product, tall_t)
 
 __all__ = [
     "EXT_PATH", "LIB_PATH", "capi", "check", "dtype_code", "ext", "LaplaceKernelFunction",
     "LaplaceSubtractionFunction", "NewtonInverseFunction", "LaplacianAttention", "laplace_kernel",
     "laplace_subtraction", "laplacian_attention", "newton_inverse", "TallMixFunction", "TallProductFunction",
-    "mix_rows", "tall_mix", "tall_product", "GraphedStep",
+    "mix_rows", "tall_mix", "tall_product", "tall_t", "GraphedStep",
 ]

@@ -17,7 +17,8 @@ products from there on run in that type. The result is returned in the input
 type. The products that stream the N-row matrices (K_qm . W with
 W = NewtonInverse(K_mm) . K_km^T V, and in the backward G . W^T, V . grad_kv^T,
 K_km . grad_kv) run on the HIP row-product kernel (inner and output widths
-<= 64); K_km^T V, K_qm^T G and the M x M products on the library GEMM.
+<= 64), K_km^T V and K_qm^T G on the HIP split-row reduction, the M x M
+products on the library GEMM.
 """
 from __future__ import annotations
 
@@ -26,7 +27,7 @@ import math
 import torch
 
 from ._lib import ext
-from .functional import _acc_type, laplace_kernel, mix_rows, newton_inverse, tall_mix, tall_product
+from .functional import _acc_type, laplace_kernel, mix_rows, newton_inverse, tall_mix, tall_product, tall_t
 
 
 def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int, dtype: torch.dtype | None = None) -> torch.Tensor:
@@ -105,7 +106,7 @@ class _AttentionFunction(torch.autograd.Function):
         k_km = _kernel_fwd(k, km_cm, s)
         inv = torch.empty_like(k_mm)
         ext().NewtonInverse_forward(k_mm, inv, int(iters))
-        kv = torch.matmul(k_km.transpose(-1, -2), v.float())              # K_km^T V  [B,H,M,d]
+        kv = tall_t(k_km, v)                                               # K_km^T V  [B,H,M,d]
         w = torch.matmul(inv, kv)                                         # [B,H,M,d]
         out = mix_rows(k_qm, w.transpose(-1, -2), in_dtype)              # K_qm W, rounded once
         ctx.grid, ctx.pool, ctx.s = grid, pool, s
@@ -118,7 +119,7 @@ class _AttentionFunction(torch.autograd.Function):
         s, p = ctx.s, ctx.pool
         g = g.contiguous()
         d_kqm = mix_rows(g, w, torch.float32)                             # G W^T       [B,H,N,M]
-        d_w = torch.matmul(k_qm.transpose(-1, -2), g.float())             # K_qm^T G    [B,H,M,d]
+        d_w = tall_t(k_qm, g)                                             # K_qm^T G    [B,H,M,d]
         d_inv = torch.matmul(d_w, kv.transpose(-1, -2))                   # [B,H,M,M]
         d_kv = torch.matmul(inv.transpose(-1, -2), d_w)                   # [B,H,M,d]
         d_kkm = mix_rows(v, d_kv, torch.float32)                          # V dkv^T     [B,H,N,M]

@@ -193,4 +193,26 @@ void MixRows_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c) {
                                       (int)Q, b.stride(nd - 2), b.stride(nd - 1), bSlice, detail::stream_of(a)));
 }
 
+void TallT_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c) {
+  TORCH_CHECK(a.dim() >= 2 && b.dim() == a.dim() && c.dim() == a.dim(), "tall_t: a, b, c need the same rank >= 2");
+  TORCH_CHECK(a.is_contiguous() && b.is_contiguous() && c.is_contiguous(), "tall_t: a, b and c must be contiguous");
+  TORCH_CHECK(a.scalar_type() == at::kFloat && c.scalar_type() == at::kFloat, "tall_t: a and c must be float32");
+  TORCH_CHECK(a.device() == b.device() && a.device() == c.device(), "tall_t: tensors on different devices");
+  const int nd = (int)a.dim();
+  const int64_t N = a.size(nd - 2), P = a.size(nd - 1), Q = b.size(nd - 1);
+  TORCH_CHECK(b.size(nd - 2) == N && c.size(nd - 2) == P && c.size(nd - 1) == Q, "tall_t: shapes ", a.sizes(), " ",
+              b.sizes(), " ", c.sizes(), " do not chain");
+  int64_t S = 1;
+  for (int i = nd - 3; i >= 0; --i) {
+    TORCH_CHECK(a.size(i) == b.size(i) && a.size(i) == c.size(i), "tall_t: batch dims differ");
+    S *= a.size(i);
+  }
+  const int bt = detail::abi_dtype(b, "tall_t");
+  at::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+  const size_t ws_bytes = lfamd_tall_t_workspace_size(S, N);
+  at::Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, a.options().dtype(at::kByte));
+  detail::check_status(lfamd_tall_t(bt, a.data_ptr<float>(), b.data_ptr(), c.data_ptr<float>(), S, N, (int)P, (int)Q,
+                                    ws.data_ptr(), ws_bytes, detail::stream_of(a)));
+}
+
 }  // namespace laplace

@@ -34,6 +34,8 @@ bool LaplaceKernel_backward_cuda(const at::Tensor gradKernel, const at::Tensor k
 // C[..., n, q] = sum_p A[..., n, p] * B[..., q, p] for a small B read through its
 // strides, inner and output widths <= 64 (lfamd_mix_rows).
 void MixRows_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c);
+// C[..., p, q] = sum_n A[..., n, p] * B[..., n, q], A and C float32, widths <= 64 (lfamd_tall_t).
+void TallT_cuda(const at::Tensor a, const at::Tensor b, at::Tensor c);
 #endif
 
 inline void LaplaceSubtraction_forward(const at::Tensor query, const at::Tensor key, at::Tensor output) {
@@ -109,6 +111,17 @@ inline void MixRows(const at::Tensor a, const at::Tensor b, at::Tensor c) {
   if (a.is_cuda() && b.is_cuda() && c.is_cuda()) {
 #if defined(WITH_HIP)
     return MixRows_cuda(a, b, c);
+#else
+    AT_ERROR("Not compiled with GPU support");
+#endif
+  }
+  AT_ERROR("Not implemented on the CPU");
+}
+
+inline void TallT(const at::Tensor a, const at::Tensor b, at::Tensor c) {
+  if (a.is_cuda() && b.is_cuda() && c.is_cuda()) {
+#if defined(WITH_HIP)
+    return TallT_cuda(a, b, c);
 #else
     AT_ERROR("Not compiled with GPU support");
 #endif

@@ -62,6 +62,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("MixRows", &MixRows,
         "MixRows (a, b, c): c[..., n, q] = sum_p a[..., n, p] * b[..., q, p] in float32, widths <= 64 "
         "(the attention layer's products; b is read through its strides)");
+  m.def("TallT", &TallT,
+        "TallT (a, b, c): c[..., p, q] = sum_n a[..., n, p] * b[..., n, q], a and c float32, widths <= 64 "
+        "(the attention layer's K^T V products)");
 }
 
 }  // namespace laplace

@@ -138,11 +138,23 @@ def mix_rows(a: torch.Tensor, b_qp: torch.Tensor, out_dtype: torch.dtype = torch
     return c
 
 
+def tall_t(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T @ b -> fp32 [..., P, Q] for a tall fp32 a [..., N, P] and b [..., N, Q]
+    (fp32/fp16/bf16, used as fp32): the HIP split-row reduction where P, Q <= 64,
+    torch.matmul elsewhere."""
+    if a.dtype == torch.float32 and b.dtype in (torch.float32, torch.float16, torch.bfloat16) \
+            and _mixable(a.shape[-1], b.shape[-1]):
+        a, b = a.contiguous(), b.contiguous()
+        c = torch.empty(a.shape[:-2] + (a.shape[-1], b.shape[-1]), dtype=torch.float32, device=a.device)
+        ext().TallT(a, b, c)
+        return c
+    return torch.matmul(a.transpose(-1, -2).float(), b.float())
+
+
 class TallMixFunction(torch.autograd.Function):
     """C = A @ W for a tall A [..., N, P] and a small fp32 W [..., P, Q] (the
-    attention layer's K_qm . (V^-1 . kv)); both products of the backward that
-    stream A's rows (grad_A = G W^T) run on the row-product kernel, grad_W = A^T G
-    on the library GEMM."""
+    attention layer's K_qm . (V^-1 . kv)); grad_A = G W^T on the row-product
+    kernel, grad_W = A^T G on the split-row reduction (tall_t)."""
 
     @staticmethod
     def forward(ctx, a: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
@@ -154,20 +166,20 @@ class TallMixFunction(torch.autograd.Function):
         a, w = ctx.saved_tensors
         g = g.contiguous()
         ga = mix_rows(g, w, a.dtype) if ctx.needs_input_grad[0] else None
-        gw = torch.matmul(a.transpose(-1, -2).float(), g.float()).to(w.dtype) if ctx.needs_input_grad[1] else None
+        gw = tall_t(a.float(), g).to(w.dtype) if ctx.needs_input_grad[1] else None
         return ga, gw, None
 
 
 class TallProductFunction(torch.autograd.Function):
     """C = A^T @ B for tall A [..., N, P] (fp32) and B [..., N, Q] (any float
     type, used as fp32) -> [..., P, Q] (the layer's K_km^T V); forward on the
-    library GEMM, both row-streaming backward products on the row-product kernel:
-    grad_A = B G^T, grad_B = A G."""
+    split-row reduction (tall_t), both row-streaming backward products on the
+    row-product kernel: grad_A = B G^T, grad_B = A G."""
 
     @staticmethod
     def forward(ctx, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         ctx.save_for_backward(a, b)
-        return torch.matmul(a.transpose(-1, -2), b.float())
+        return tall_t(a, b)
 
     @staticmethod
     def backward(ctx, g: torch.Tensor):

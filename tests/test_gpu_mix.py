@@ -66,6 +66,36 @@ def test_mix_rows_rejects(gpu):
         lf.mix_rows(torch.randn(2, 2, 10, 5, device=gpu), b.transpose(0, 1))
 
 
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 64, 784, 49, 64), (1, 3, 100, 7, 64), (1, 1, 1, 1, 1), (3, 2, 65, 64, 64),
+                                   (1, 5, 129, 33, 17), (1, 2, 3000, 49, 64), (2, 1, 0, 49, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_tall_t(gpu, dt, shape):
+    """c = a^T b over the rows (lfamd_tall_t, torch export TallT) against an fp64 CPU product,
+    |err| <= 1e-5 * sum_n |a| |b|; deterministic (two calls give the same bits)."""
+    import laplacianformer_amd as lf
+
+    B, H, N, P, Q = shape
+    print(f"tall_t {shape} {dt}", flush=True)
+    a = gen((B, H, N, P), 31 + N + P, "f32")
+    b = gen((B, H, N, Q), 32 + N + Q, dt)
+    c = lf.tall_t(a.to(gpu), b.to(gpu))
+    assert c.shape == (B, H, P, Q) and c.dtype == torch.float32
+    _check(c, a.transpose(-1, -2), b.transpose(-1, -2), "a^T b")
+    assert torch.equal(c, lf.tall_t(a.to(gpu), b.to(gpu)))
+
+
+def test_tall_t_rejects(gpu):
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    a = torch.randn(1, 1, 10, 65, device=gpu)
+    with pytest.raises(RuntimeError):
+        L.TallT(a, torch.randn(1, 1, 10, 8, device=gpu), torch.empty(1, 1, 65, 8, device=gpu))  # P = 65 > 64
+    with pytest.raises(RuntimeError):
+        L.TallT(a[..., :8].half(), torch.randn(1, 1, 10, 8, device=gpu), torch.empty(1, 1, 8, 8, device=gpu))
+
+
 @pytest.mark.parametrize("vdt", ["f32", "f16"])
 def test_tall_functions_autograd(gpu, vdt):
     """K_qm . W and K_km^T V with their gradients (the layer's use), against fp64 CPU autograd."""
