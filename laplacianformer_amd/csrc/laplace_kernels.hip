@@ -1791,6 +1791,8 @@ int bwd_common(int dtype, const void* g, const void* q, const void* k, void* dq,
   }
   if (!g || !q || !k || (doDq && !dq) || (doDk && !dk)) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
   const size_t acc = dtype == LFAMD_F64 ? 8 : 4;
+  if (doDk && ws && (reinterpret_cast<uintptr_t>(ws) & (acc - 1)))
+    return fail(LFAMD_ERR_ARG, "%s: workspace not %zu-byte aligned", who, acc);
   if (b2_ok(dtype, d.BH(), d.N, d.M, d.C) && (reinterpret_cast<uintptr_t>(q) & 3) == 0)
     return b2_launch(dtype, g, q, k, doDq ? dq : nullptr, doDk ? dk : nullptr, ws, wsBytes, d.BH(), d.N, d.M, d.C,
                      st, who);

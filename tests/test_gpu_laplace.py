@@ -283,6 +283,10 @@ def test_capi_direct(gpu):
     rc = lib.lfamd_laplace_backward_key(dt, gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), dk.data_ptr(),
                                         B, H, N, M, C, ws.data_ptr(), 1, s)
     assert rc == 1 and b"workspace" in lib.lfamd_last_error()
+    # A workspace off the partials' 4-byte alignment is rejected too.
+    rc = lib.lfamd_laplace_backward_key(dt, gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), dk.data_ptr(),
+                                        B, H, N, M, C, ws.data_ptr() + 2, ws_bytes, s)
+    assert rc == 1 and b"aligned" in lib.lfamd_last_error()
 
 
 @pytest.mark.parametrize("dt,M", [("f32", 49), ("bf16", 256), ("f16", 49)])
