@@ -80,11 +80,6 @@ struct B2Shape {
   }
 };
 
-// T(pattern) = 2^22 + 2^14 + t / 2 (see the file comment), as the fp32 bit pattern 0x4a808000 + t.
-__device__ __forceinline__ float tmap16(uint16_t bits) {
-  const int t = (bits & 0x8000) ? -(int)(bits & 0x7fff) : (int)bits;
-  return __builtin_bit_cast(float, (uint32_t)(0x4a808000 + t));
-}
 
 template <typename T> __device__ __forceinline__ float g2f(uint16_t b);
 template <> __device__ __forceinline__ float g2f<f16s>(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }

@@ -983,7 +983,8 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
   // have zero grad and key, so they add nothing and are not stored).
   constexpr int MC = kMbMC, RB = kMbRB, M = CB * MC;
   constexpr int MP = MC;                       // LDS row pitch of a staged batch (floats)
-  constexpr bool kF16 = std::is_same<T, f16s>::value;
+  // 16-bit inputs take the ordered-pattern step (tmap16): y = clamp(T(q) + (1/2 - T(k))).
+  constexpr bool k16 = std::is_same<T, f16s>::value || std::is_same<T, bf16s>::value;
   // Grad elements per fetched 32-bit word: 2 for 16-bit grads, 1 for fp32 grads and
   // for the kernel-gradient source (fp32 gK and K, g = -s * gK * K formed at staging).
   static_assert(GSRC == kGradF16 || std::is_same<T, f16s>::value, "kernel-gradient source: fp16 only");
@@ -1056,12 +1057,17 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
   int t0 = grp;  // this group's first batch
   if (t0 < nb) fetch(t0);
 
-  // Key tile (global [C][M], coalesced over j), scaled for fp16.
+  // Key tile (global [C][M], coalesced over j): 16-bit keys as the step terms
+  // 1/2 - T(k) (see tmap16), fp32 keys as values. Columns past Mt have zero grad.
   for (int t = threadIdx.x; t < 64 * M; t += blockDim.x) {
     const int cl = t / M, j = t - cl * M;
     const int cc = chb * 64 + cl;
-    const float v = (cc < C && j < Mt) ? to_acc(kb[(size_t)cc * Mt + j]) : 0.0f;
-    big[j * 64 + cl] = kF16 ? v * 16777216.0f : v;
+    const bool in = cc < C && j < Mt;
+    const T kv = kb[(size_t)min(cc, C - 1) * Mt + min(j, Mt - 1)];
+    if constexpr (k16)
+      big[j * 64 + cl] = in ? 0.5f - tmap16(kv.bits) : 0.0f;
+    else
+      big[j * 64 + cl] = in ? to_acc(kv) : 0.0f;
   }
   __syncthreads();
   float kreg[MC], dka[MC];
@@ -1104,8 +1110,10 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
       }
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
-        const float v = to_acc(qpre[r]);
-        qsm[r * 64 + lane] = kF16 ? v * 16777216.0f : v;
+        if constexpr (k16)
+          qsm[r * 64 + lane] = tmap16(qpre[r].bits);
+        else
+          qsm[r * 64 + lane] = to_acc(qpre[r]);
       }
       wave_sync();
       if (DQ) {
@@ -1154,8 +1162,8 @@ laplace_bwd_mb_kernel(const T* __restrict__ gout, const T* __restrict__ query, c
           for (int u = 0; u < 4; ++u) {
             const int j = jq * 4 + u;
             float y;
-            if constexpr (kF16) {
-              y = half_step(qv - kreg[j]);
+            if constexpr (k16) {
+              y = __builtin_amdgcn_fmed3f(qv + kreg[j], 0.0f, 1.0f);  // one clamped add
             } else {
               const float e = (qv - kreg[j]) * scl;
               y = __builtin_amdgcn_fmed3f(__builtin_fmaf(e, scl, 0.5f), 0.0f, 1.0f);

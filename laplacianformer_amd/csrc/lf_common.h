@@ -103,6 +103,17 @@ __device__ __forceinline__ void wave_sync() {
 // (kernels run with DX10 clamping), one full-rate VALU instruction with inline
 // constants. For a d that is 0 or at least 1 in magnitude the result is exactly
 // 0 (d < 0), 0.5 (d == 0) or 1 (d > 0), i.e. (sgn(d) + 1) / 2.
+// Ordered map of a 16-bit float pattern (fp16 or bf16): T = 2^22 + 2^14 + t / 2,
+// the fp32 bit pattern 0x4a808000 + t, with t the signed magnitude of the pattern
+// (+0 and -0 both 0). T is strictly increasing in the value over every non-NaN
+// pattern (infinities included) and its values are multiples of 1/2 in [2^22, 2^23),
+// so T(q) + (1/2 - T(k)) is exact and clamps to exactly 0, 1/2 or 1 =
+// (sgn(q - k) + 1) / 2. A NaN pattern orders beyond the infinities by its sign bit.
+__device__ __forceinline__ float tmap16(uint16_t bits) {
+  const int t = (bits & 0x8000) ? -(int)(bits & 0x7fff) : (int)bits;
+  return __builtin_bit_cast(float, (uint32_t)(0x4a808000 + t));
+}
+
 __device__ __forceinline__ float half_step(float d) {
   return __builtin_amdgcn_fmed3f(__builtin_fmaf(d, 0.5f, 0.5f), 0.0f, 1.0f);
 }

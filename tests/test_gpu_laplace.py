@@ -150,8 +150,9 @@ def test_reduce_forward(gpu, dt):
         assert np.array_equal(got, np.asarray(ref, dtype=np.float64)), (dt, C)
 
 
-# Non-finite inputs in the backward (M = 49, C = 64: the 16-bit column-split
-# kernel for fp16 / bf16, the clamped-step kernel for fp32). Rows 0-7 of channel 3
+# Non-finite inputs in the backward (C = 64; M = 49: the 16-bit column-split
+# kernel for fp16 / bf16, the clamped-step kernel for fp32; M = 64: the
+# column-block kernel, with the same steps). Rows 0-7 of channel 3
 # and rows 8-15 of channel 5 hold +inf / -inf, as do key columns 0-4 of channel 3
 # and 10-14 of channel 5, so those pairs are infinite ties; rows 20 / 21 of
 # channels 7 / 9 hold NaN of either sign.
@@ -164,12 +165,13 @@ def test_reduce_forward(gpu, dt):
 #    clamp of NaN is 0); the reference gives 0 -- the oracle is run with each
 #    infinity replaced by a finite value that keeps every comparison but makes the
 #    ties q < k, and the NaN by a value below every key.
+@pytest.mark.parametrize("M", [49, 64])
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
-def test_laplace_nonfinite_backward(gpu, dt):
+def test_laplace_nonfinite_backward(gpu, dt, M):
     import laplacianformer_amd as lf
 
-    B, H, N, M, C = 1, 1, 64, 49, 64
-    print(f"laplace non-finite backward {dt}", flush=True)
+    B, H, N, C = 1, 1, 64, 64
+    print(f"laplace non-finite backward {dt} M={M}", flush=True)
     q, k, g = _inputs(B, H, N, M, C, dt, seed=91)
     q = q.float()
     k = k.float()
