@@ -337,10 +337,11 @@ FWD_JB = 7          # key columns per forward column block
 FWD_KP = 56 * 4     # bytes per channel of the forward key tile ([C][56] fp32)
 
 
-def fwd_variant(R, top=256):
+def fwd_variant(R, top=256, jb=FWD_JB, kp=FWD_KP, prefix="fwd2"):
     """Returns (name, C++ source) of the channel loop of the row-staged forward
     (laplace_fwd2.hip) for R row sets per lane, using VGPRs below `top` (256:
-    two waves per SIMD; 128: four).
+    two waves per SIMD; 128: four), for blocks of `jb` key columns (7 for M = 49;
+    8 for the wide-landmark kernel) in a key tile of `kp` bytes per channel.
 
     Per channel c and row set s: T = q[s][c] - k[c][j] (v_sub_f32) and
     acc[s][j] += |T| (v_add_f32 with the |.| modifier), j < 7, channels in
@@ -374,7 +375,7 @@ def fwd_variant(R, top=256):
         add(f"v_mov_b32 v{QADDR[s_]}, %[qa{s_}]")
     add(f"v_mov_b32 v{KADDR}, %[ka]")
     for s_ in range(R):
-        for j in range(FWD_JB):
+        for j in range(jb):
             add(f"v_mov_b32 v{acc(s_, j)}, 0")
     for s_ in range(R):
         add(f"ds_read_b128 v[{QA[s_]}:{QA[s_] + 3}], v{QADDR[s_]}")
@@ -393,7 +394,7 @@ def fwd_variant(R, top=256):
             for s_ in range(R):
                 add(f"ds_read_b128 v[{dst[s_]}:{dst[s_] + 3}], v{QADDR[s_]} offset:{off}")
             nq = R
-        koff = (ci + 1) * FWD_KP
+        koff = (ci + 1) * kp
         add(f"ds_read_b128 v[{Kn}:{Kn + 3}], v{KADDR} offset:{koff}")
         add(f"ds_read_b128 v[{Kn + 4}:{Kn + 7}], v{KADDR} offset:{koff + 16}")
         add(f"s_waitcnt lgkmcnt({nq + 2})")
@@ -401,29 +402,29 @@ def fwd_variant(R, top=256):
             qreg = Q[s_] + cc
             used = [0, 0, 0, 0]
             ts = []
-            for j in range(FWD_JB):
+            for j in range(jb):
                 ok = [b for b in range(4) if b != qreg % 4 and b != acc(s_, j) % 4 and used[b] < 4]
                 b = min(ok, key=lambda b: used[b])
                 t = TB + 4 * used[b] + b
                 used[b] += 1
                 ts.append(t)
                 add(f"v_sub_f32 v{t}, v{qreg}, v{K + j}")
-            for j in range(FWD_JB):
+            for j in range(jb):
                 add(f"v_add_f32_e64 v{acc(s_, j)}, |v{ts[j]}|, v{acc(s_, j)}")
     for s_ in range(R):
         add(f"v_add_u32 v{QADDR[s_]}, 32, v{QADDR[s_]}")
-    add(f"v_add_u32 v{KADDR}, {8 * FWD_KP}, v{KADDR}")
+    add(f"v_add_u32 v{KADDR}, {8 * kp}, v{KADDR}")
     add(f"s_sub_u32 s{SC}, s{SC}, 1")
     add(f"s_cmp_gt_u32 s{SC}, 0")
     add("s_cbranch_scc1 FL_%=")
     add("s_waitcnt lgkmcnt(0)")
     for s_ in range(R):
-        for j in range(FWD_JB):
+        for j in range(jb):
             add(f"v_mov_b32 %[a{s_}_{j}], v{acc(s_, j)}")
 
-    name = f"fwd2_sums_r{R}"
+    name = f"{prefix}_sums_r{R}"
     asm = "\n".join("      \"" + x + "\\n\"" for x in L)
-    outs = ", ".join(f"[a{s_}_{j}] \"=v\"(acc[{s_}][{j}])" for s_ in range(R) for j in range(FWD_JB))
+    outs = ", ".join(f"[a{s_}_{j}] \"=v\"(acc[{s_}][{j}])" for s_ in range(R) for j in range(jb))
     ins = ", ".join(["[iters] \"s\"(iters)", "[ka] \"v\"(ka)"] + [f"[qa{s_}] \"v\"(qa[{s_}])" for s_ in range(R)])
     clob = ", ".join([f"\"v{v}\"" for v in range(lo, top)] + [f"\"s{SC}\"", "\"memory\""])
     if top != 256:
@@ -432,9 +433,9 @@ def fwd_variant(R, top=256):
 // Channel loop of the row-staged forward for {R} row set(s) per lane ({top - lo} private VGPRs below v{top}):
 // acc[s][j] = sum over channels c < 8 * iters of |q[s][c] - k[c][j]|, c ascending. qa[s]: LDS
 // byte address of the lane's row of set s in the fp32 query tile (channel 0); ka: LDS byte
-// address of the lane's 8-column key block at channel 0 (rows of {FWD_KP} bytes). Reads go one
+// address of the lane's 8-column key block at channel 0 (rows of {kp} bytes). Reads go one
 // query group and one channel past the end (the tiles' padding and the next tile; unused).
-__device__ __forceinline__ void {name}(float (&acc)[{R}][{FWD_JB}], const unsigned (&qa)[{R}], unsigned ka, int iters) {{
+__device__ __forceinline__ void {name}(float (&acc)[{R}][{jb}], const unsigned (&qa)[{R}], unsigned ka, int iters) {{
   asm volatile(
 {asm}
       : {outs}
@@ -446,6 +447,8 @@ __device__ __forceinline__ void {name}(float (&acc)[{R}][{FWD_JB}], const unsign
 
 
 FWD_RS = (1, 2, 3, 4, 5, 6, 7)
+FWD3_KP = 256 * 4   # bytes per channel of the wide-landmark kernel's key tile ([C][256] fp32)
+FWD3_RS = (3,)
 FWD_RS_V128 = (1, 2, 3)
 
 
@@ -466,6 +469,10 @@ def main(out_path):
         parts.append(src)
     for R in FWD_RS_V128:
         name, src = fwd_variant(R, 128)
+        parts.append(f"// {name}")
+        parts.append(src)
+    for R in FWD3_RS:
+        name, src = fwd_variant(R, 128, jb=8, kp=FWD3_KP, prefix="fwd3")
         parts.append(f"// {name}")
         parts.append(src)
     parts.append("}  // namespace lfamd")

@@ -406,6 +406,123 @@ int launch_f2_t(const void* q, const void* k, void* o, int64_t BH, int64_t N, in
   return launch_f2_w<T, EPI, 8>(q, k, o, BH, N, C, scale, p, st);
 }
 
+// ---------------------------------------------------------------------------
+// Wide landmark sets, M in {128, 256} (M = 256). A workgroup
+// of 16 waves (4 per SIMD, 128 VGPRs) takes 192 rows (3 row sets) of one slice:
+// the rows staged as fp32 [row][C + 4] as above, the slice's key as fp32 with a
+// fixed pitch of 256 columns per channel. Wave w computes the 8-column blocks
+// w, w + 16 (M / 128 of them) for the 3 sets with the generated channel loop
+// (fwd3_sums_r3_v128: per channel the block's 8 keys as two broadcast 16-byte reads
+// feed 48 VALU instructions), c ascending in fp32 (bit-identical to the
+// reference's order). A lane's 8 results of a row are one 16-byte store for
+// 16-bit outputs (two for fp32), written from registers: the output tile
+// would not fit in the LDS beside the key.
+constexpr int kF3Sets = 3;
+constexpr int kF3Rows = 64 * kF3Sets;
+constexpr int kF3KP = 256;
+constexpr int kF3Waves = 16;
+
+__host__ __device__ constexpr size_t f3_lds_bytes(int C) {
+  return (size_t)C * kF3KP * 4 + (size_t)kF3Rows * (C + 4) * 4;
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* dst, const float (&a)[8]);
+template <>
+__device__ __forceinline__ void store8<float>(float* dst, const float (&a)[8]) {
+  reinterpret_cast<float4*>(dst)[0] = make_float4(a[0], a[1], a[2], a[3]);
+  reinterpret_cast<float4*>(dst)[1] = make_float4(a[4], a[5], a[6], a[7]);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* dst, const float (&a)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    w[e] = (uint32_t)from_acc<T>(a[2 * e]).bits | ((uint32_t)from_acc<T>(a[2 * e + 1]).bits << 16);
+  *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Grid: (workgroups per slice = ceil(N / 192), B*H).
+template <typename T>
+__global__ void __launch_bounds__(64 * kF3Waves, 1)
+laplace_fwd3_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out, int N, int M,
+                    int C) {
+  constexpr int THREADS = 64 * kF3Waves;
+  constexpr int EV = 16 / (int)sizeof(T);
+  const int tid = threadIdx.x;
+  const int wave = uniform(tid >> 6);
+  const int lane = tid & 63;
+  const int x = blockIdx.x, bh = blockIdx.y;
+  const int P0 = x * kF3Rows, n = min(kF3Rows, N - P0);
+  const int QP = C + 4;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* ktile = reinterpret_cast<float*>(smem);                          // [C][256]
+  float* qtile = reinterpret_cast<float*>(smem + (size_t)C * kF3KP * 4);   // [n][C + 4]
+
+  constexpr int kQL = (kF3Rows * kF2MaxC / EV + THREADS - 1) / THREADS;
+  const int qvecs = n * C / EV, vpr = C / EV;
+  const uint4* qsrc = reinterpret_cast<const uint4*>(query + ((size_t)bh * N + P0) * C);
+  uint4 qv[kQL];
+#pragma unroll
+  for (int i = 0; i < kQL; ++i) qv[i] = qsrc[min(tid + i * THREADS, qvecs - 1)];
+  constexpr int kKL = (kF2MaxC * kF3KP + THREADS - 1) / THREADS;
+  const int kn = C * M;
+  const T* ksrc = key + (size_t)bh * C * M;
+  T kvv[kKL];
+#pragma unroll
+  for (int i = 0; i < kKL; ++i) kvv[i] = ksrc[min(tid + i * THREADS, kn - 1)];
+#pragma unroll
+  for (int i = 0; i < kKL; ++i) {
+    const int t = tid + i * THREADS;
+    if (t < kn) {
+      const int c = t / M, j = t - c * M;
+      ktile[c * kF3KP + j] = to_acc(kvv[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kQL; ++i) {
+    const int u = tid + i * THREADS;
+    if (u < qvecs) {
+      const int row = u / vpr, c0 = (u - row * vpr) * EV;
+      float f[EV];
+      widen16<T>(qv[i], f);
+      float4* dst = reinterpret_cast<float4*>(qtile + row * QP + c0);
+#pragma unroll
+      for (int e = 0; e < EV / 4; ++e) dst[e] = make_float4(f[4 * e], f[4 * e + 1], f[4 * e + 2], f[4 * e + 3]);
+    }
+  }
+  __syncthreads();
+
+  const unsigned kBase = (unsigned)(uintptr_t)ktile, qBase = (unsigned)(uintptr_t)qtile;
+  unsigned qa[kF3Sets];
+#pragma unroll
+  for (int s = 0; s < kF3Sets; ++s) qa[s] = qBase + (unsigned)(min(64 * s + lane, n - 1) * QP) * 4;
+  const int nblk = M / 8;
+  for (int b = wave; b < nblk; b += kF3Waves) {  // wave-uniform
+    float acc[kF3Sets][8];
+    fwd3_sums_r3_v128(acc, qa, kBase + (unsigned)b * 32, C / 8);
+#pragma unroll
+    for (int s = 0; s < kF3Sets; ++s) {
+      const int row = 64 * s + lane;
+      if (row < n) store8<T>(out + ((size_t)bh * N + P0 + row) * M + 8 * b, acc[s]);
+    }
+  }
+}
+
+template <typename T>
+int launch_f3(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
+  auto kern = laplace_fwd3_kernel<T>;
+  const size_t lds = f3_lds_bytes((int)C);
+  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
+  const int64_t nx = (N + kF3Rows - 1) / kF3Rows;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nx, (unsigned)BH), dim3(64 * kF3Waves), lds, st, static_cast<const T*>(q),
+                     static_cast<const T*>(k), static_cast<T*>(o), (int)N, (int)M, (int)C);
+  return check_launch("laplace forward (wide landmarks)");
+}
+
 }  // namespace
 
 // The row-staged forward: fp32 / fp16 / bf16, M = 49, 8 <= C <= 64 with
@@ -415,6 +532,22 @@ bool f2_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C, const void* q
   if (M != kF2M || C < 8 || C > kF2MaxC || C % 8 != 0 || N <= 0 || BH <= 0 || BH > 65535) return false;
   if ((reinterpret_cast<uintptr_t>(q) & 15) != 0) return false;
   return N <= INT32_MAX / kF2M;
+}
+
+// The wide-landmark forward: fp32 / fp16 / bf16, M in {128, 256}, 8 <= C <= 64
+// with C % 8 == 0, 16-byte aligned query and output, N >= 1.
+bool f3_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C, const void* q, const void* out) {
+  if (!(dtype == LFAMD_F32 || dtype == LFAMD_F16 || dtype == LFAMD_BF16)) return false;
+  if (!(M == 128 || M == 256) || C < 8 || C > kF2MaxC || C % 8 != 0 || N <= 0 || BH <= 0 || BH > 65535) return false;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15) != 0) return false;
+  return N <= INT32_MAX / M && f3_lds_bytes((int)C) <= (size_t)max_lds_bytes();
+}
+
+int f3_launch(int dtype, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C,
+              hipStream_t st) {
+  if (dtype == LFAMD_F32) return launch_f3<float>(q, k, o, BH, N, M, C, st);
+  if (dtype == LFAMD_F16) return launch_f3<f16s>(q, k, o, BH, N, M, C, st);
+  return launch_f3<bf16s>(q, k, o, BH, N, M, C, st);
 }
 
 int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,

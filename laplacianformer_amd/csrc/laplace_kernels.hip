@@ -1851,6 +1851,8 @@ int lfamd_laplace_forward(int dtype, const void* query, const void* key, void* o
   if (!query || !key || !output) return fail(LFAMD_ERR_ARG, "laplace forward: null pointer");
   if (f2_ok(dtype, d.BH(), d.N, d.M, d.C, query))
     return f2_launch(dtype, false, query, key, output, d.BH(), d.N, d.C, 0.0f, st);
+  if (f3_ok(dtype, d.BH(), d.N, d.M, d.C, query, output))
+    return f3_launch(dtype, query, key, output, d.BH(), d.N, d.M, d.C, st);
   if (fwd_bcast_ok(dtype, d, query, dtype_size(dtype))) {
     switch (dtype) {
       case LFAMD_F32: return launch_fwd_bcast<float>(query, key, output, d, st);

@@ -41,6 +41,10 @@ int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, 
 // Row-staged forward of LaplaceSubtraction at M = 49 (laplace_fwd2.hip); kernelEpi:
 // exp(-scale * distance) in fp32 instead of the distance in the element type.
 bool f2_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C, const void* q);
+// Wide-landmark forward, M in {128, 256} (laplace_fwd2.hip).
+bool f3_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C, const void* q, const void* out);
+int f3_launch(int dtype, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C,
+              hipStream_t st);
 int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,
               float scale, hipStream_t st);
 

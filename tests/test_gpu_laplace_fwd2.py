@@ -50,6 +50,32 @@ def test_fwd2_plans(gpu, shape, dt):
     assert_bitwise(out, oracle.laplace_forward(q, k, dt), dt, f"forward bits ({what})")
 
 
+# The wide-landmark forward (M in {128, 256}): whole and partial 192-row
+# workgroups, one-row slices, C = 8 and 40, the config-4 shape on two slices.
+WIDE = [
+    (1, 2, 700, 128, 64),
+    (2, 1, 192, 256, 64),
+    (1, 1, 1, 256, 8),
+    (1, 3, 385, 256, 40),
+    (1, 2, 4096, 256, 64),
+]
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", WIDE, ids=lambda s: "x".join(map(str, s)))
+def test_fwd3_wide(gpu, shape, dt):
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = shape
+    print(f"fwd3 {shape} {dt}", flush=True)
+    q = gen((B, H, N, C), 700 + N, dt)
+    k = gen((B, H, C, M), 701 + N, dt)
+    out = torch.empty((B, H, N, M), dtype=q.dtype, device=gpu)
+    lf.ext().LaplaceSubtraction_forward(q.to(gpu), k.to(gpu), out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.laplace_forward(q, k, dt), dt, f"forward bits {shape}")
+
+
 @pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[5]], ids=_ids)
 def test_fwd2_kernel_epilogue(gpu, shape):
     """The fused exp(-s * d) output of the same kernel, fp16 inputs."""
