@@ -51,13 +51,15 @@ def test_fwd2_plans(gpu, shape, dt):
 
 
 # The wide-landmark forward (M in {128, 256}): whole and partial 192-row
-# workgroups, one-row slices, C = 8 and 40, the config-4 shape on two slices.
+# workgroups, one-row slices, C = 8 to 64, the config-4 shape on two slices.
 WIDE = [
     (1, 2, 700, 128, 64),
     (2, 1, 192, 256, 64),
     (1, 1, 1, 256, 8),
     (1, 3, 385, 256, 40),
     (1, 2, 4096, 256, 64),
+    (2, 3, 500, 128, 16),
+    (1, 4, 1000, 256, 8),
 ]
 
 
