@@ -294,6 +294,27 @@ def bench_cfg4(args, dev):
             "steps_per_window": steps}
 
 
+def bench_small_d(args, dev):
+    """An output-write-bound small-d case: config 4's shape with d = 8 (B=16 H=8 N=4096 M=256,
+    bf16): 2 flop-equivalents per triple against 2 bytes of output per (i, j), so HBM bytes,
+    not VALU work, bound it. Reported as achieved GB/s against the 8 TB/s HBM peak."""
+    import torch
+
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    B, H, N, M, C = 16, 8, 4096, 256, 8
+    q = gen((B, H, N, C), 1051, torch.bfloat16).to(dev)
+    k = gen((B, H, C, M), 1052, torch.bfloat16).to(dev)
+    out = torch.empty((B, H, N, M), dtype=torch.bfloat16, device=dev)
+    t = per_call(lambda: L.LaplaceSubtraction_forward(q, k, out), max(SECTION_REPS, args.steps // 10), args.warmup)
+    nbytes = 2 * (q.numel() + k.numel() + out.numel())
+    gbs = nbytes / (t["median"] * 1e-3) / 1e9
+    return {"workload": "LaplaceSubtraction forward B=16 H=8 N=4096 M=256 d=8 bf16 (output-write-bound)",
+            "ms": t, "bytes": nbytes, "gb_per_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS,
+            "kernel": "laplace_fwd3_kernel<bf16s> (16-byte stores from registers)"}
+
+
 def reference_figure(args, dev):
     """The reference's published comparison (README benchmark figure: each op against eager
     PyTorch on the same GPU at N = 16, 32, 64, 128, forward and backward), on this GPU.
@@ -512,6 +533,7 @@ def main():
     layer = bench_layer(args, dev) if args.only in ("layer", "all") else None
     cfg4 = bench_cfg4(args, dev) if args.only in ("cfg4", "all") else None
     fig = reference_figure(args, dev) if args.only in ("figure", "all") else None
+    small_d = bench_small_d(args, dev) if args.only in ("figure", "all") else None
 
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
@@ -599,6 +621,8 @@ def main():
         line["config4"] = cfg4
     if fig:
         line["reference_figure"] = fig
+    if small_d:
+        line["small_d"] = small_d
     if args.calib_copy:
         src = torch.empty(args.calib_copy << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
