@@ -408,10 +408,11 @@ int launch_f2_t(const void* q, const void* k, void* o, int64_t BH, int64_t N, in
 
 // ---------------------------------------------------------------------------
 // Wide landmark sets, M in {128, 256} (M = 256). A workgroup
-// of 16 waves (4 per SIMD, 128 VGPRs) takes 192 rows (3 row sets) of one slice:
+// of WAVES waves (128 VGPRs each; 16: one workgroup per CU, 8: two per CU for
+// C <= 16) takes 192 rows (3 row sets) of one slice:
 // the rows staged as fp32 [row][C + 4] as above, the slice's key as fp32 with a
 // fixed pitch of 256 columns per channel. Wave w computes the 8-column blocks
-// w, w + 16 (M / 128 of them) for the 3 sets with the generated channel loop
+// w, w + WAVES, ... for the 3 sets with the generated channel loop
 // (fwd3_sums_r3_v128: per channel the block's 8 keys as two broadcast 16-byte reads
 // feed 48 VALU instructions), c ascending in fp32 (bit-identical to the
 // reference's order). A lane's 8 results of a row are one 16-byte store for
@@ -420,7 +421,6 @@ int launch_f2_t(const void* q, const void* k, void* o, int64_t BH, int64_t N, in
 constexpr int kF3Sets = 3;
 constexpr int kF3Rows = 64 * kF3Sets;
 constexpr int kF3KP = 256;
-constexpr int kF3Waves = 16;
 
 __host__ __device__ constexpr size_t f3_lds_bytes(int C) {
   return (size_t)C * kF3KP * 4 + (size_t)kF3Rows * (C + 4) * 4;
@@ -442,12 +442,14 @@ __device__ __forceinline__ void store8(T* dst, const float (&a)[8]) {
   *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Grid: (workgroups per slice = ceil(N / 192), B*H).
-template <typename T>
-__global__ void __launch_bounds__(64 * kF3Waves, 1)
+// Grid: (workgroups per slice = ceil(N / 192), B*H). WAVES = 16 (one workgroup
+// per CU) or 8 (two per CU, for small C: the two workgroups' load, compute and
+// store phases overlap).
+template <typename T, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, 16 / WAVES)
 laplace_fwd3_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out, int N, int M,
                     int C) {
-  constexpr int THREADS = 64 * kF3Waves;
+  constexpr int THREADS = 64 * WAVES;
   constexpr int EV = 16 / (int)sizeof(T);
   const int tid = threadIdx.x;
   const int wave = uniform(tid >> 6);
@@ -499,7 +501,9 @@ laplace_fwd3_kernel(const T* __restrict__ query, const T* __restrict__ key, T* _
 #pragma unroll
   for (int s = 0; s < kF3Sets; ++s) qa[s] = qBase + (unsigned)(min(64 * s + lane, n - 1) * QP) * 4;
   const int nblk = M / 8;
-  for (int b = wave; b < nblk; b += kF3Waves) {  // wave-uniform
+  // Blocks wave, wave + WAVES, ...: the waves writing one row's 16-byte pieces
+  // run concurrently (measured 1.6x faster stores than adjacent blocks per wave).
+  for (int b = wave; b < nblk; b += WAVES) {  // wave-uniform
     float acc[kF3Sets][8];
     fwd3_sums_r3_v128(acc, qa, kBase + (unsigned)b * 32, C / 8);
 #pragma unroll
@@ -510,17 +514,24 @@ laplace_fwd3_kernel(const T* __restrict__ query, const T* __restrict__ key, T* _
   }
 }
 
-template <typename T>
-int launch_f3(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
-  auto kern = laplace_fwd3_kernel<T>;
+template <typename T, int WAVES>
+int launch_f3_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
+  auto kern = laplace_fwd3_kernel<T, WAVES>;
   const size_t lds = f3_lds_bytes((int)C);
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
   const int64_t nx = (N + kF3Rows - 1) / kF3Rows;
-  hipLaunchKernelGGL(kern, dim3((unsigned)nx, (unsigned)BH), dim3(64 * kF3Waves), lds, st, static_cast<const T*>(q),
+  hipLaunchKernelGGL(kern, dim3((unsigned)nx, (unsigned)BH), dim3(64 * WAVES), lds, st, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<T*>(o), (int)N, (int)M, (int)C);
   return check_launch("laplace forward (wide landmarks)");
+}
+
+template <typename T>
+int launch_f3(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
+  if (2 * f3_lds_bytes((int)C) <= (size_t)max_lds_bytes() && C <= 16)
+    return launch_f3_w<T, 8>(q, k, o, BH, N, M, C, st);
+  return launch_f3_w<T, 16>(q, k, o, BH, N, M, C, st);
 }
 
 }  // namespace
