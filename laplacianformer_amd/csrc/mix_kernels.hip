@@ -12,14 +12,16 @@
 // Each A value feeds Q multiply-adds, so a VALU kernel would read it from LDS
 // once per wave-wide FMA and be LDS-bound; the matrix cores take 4 k-steps of a
 // 16 x 16 tile per 16-byte operand read instead. C is written in fp32, fp16 or
-// bf16 (one rounding of the fp32 sum). A workgroup (4 waves) takes
-// 64-row tiles of A in turn (the next tile's loads in flight during the current
-// one's products): A rows and B staged in LDS (pitch 68 floats), wave w computes
-// rows [16w, 16w + 16) x all Q columns as four 16 x 16 v_mfma_f32_16x16x4_f32
-// accumulators, with the B operand (64 values per lane) in registers for the
-// whole tile and k permuted per lane (k = 16 kb + 4 (lane / 16) + step) so that
-// both operands are read as float4. fp32 products and sums throughout; tests
-// compare against an fp64 product within 1e-5 of sum |a| |b|.
+// bf16 (one rounding of the fp32 sum). A workgroup (4 waves) stages B once in
+// LDS (pitch 68 floats); after that single barrier each wave works alone on
+// 16-row groups g, g + 4 * gridDim.x, ... of its slice: the group's rows
+// (loaded one group ahead, unconditionally at clamped indices) go to the wave's
+// own 16 LDS rows, four 16 x 16 v_mfma_f32_16x16x4_f32 accumulators compute
+// its 16 x Q outputs with k permuted per lane (k = 16 kb + 4 (lane / 16) +
+// step) so that both operands are read as float4, and the outputs go back
+// through the same LDS rows to be stored as one contiguous run of 16 * Q
+// elements (64 consecutive per store). fp32 products and sums throughout;
+// tests compare against an fp64 product within 1e-5 of sum |a| |b|.
 #include <algorithm>
 
 #include "lf_common.h"
@@ -30,36 +32,48 @@ namespace lfamd {
 typedef float v4f __attribute__((ext_vector_type(4)));  // one 16 x 16 MFMA accumulator per lane
 
 constexpr int kMixPMax = 64;   // largest inner / output width
-constexpr int kMixRows = 64;   // rows of A per workgroup
+constexpr int kMixRows = 64;   // rows of A per tile of the tall transposed product
 constexpr int kMixLS = 68;     // LDS pitch (floats): lane-varying 16-byte reads without conflicts
+constexpr int kMixGroup = 16;  // rows of A per wave and step
+
+// Orders one wave's LDS stores before its lanes read each other's values (a wave's
+// LDS operations run in issue order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 template <typename TA, typename TC>
 __global__ void __launch_bounds__(256)
 mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __restrict__ C, int N, int P,
                 int Q, int64_t sq, int64_t sp, int64_t bStride) {
-  __shared__ __align__(16) float Bs[kMixPMax * kMixLS];  // Bs[q][p], zero outside Q x P
-  __shared__ __align__(16) float As[kMixRows * kMixLS];  // As[r][p], zero outside the rows and P
+  __shared__ __align__(16) float Bs[kMixPMax * kMixLS];      // Bs[q][p], zero outside Q x P
+  __shared__ __align__(16) float Ws[4][kMixGroup * kMixLS];  // per wave: its A rows, then its C rows
   const int s = blockIdx.y;
-  const int tiles = (N + kMixRows - 1) / kMixRows;
+  const int groups = (N + kMixGroup - 1) / kMixGroup;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
   const float* Bm = B + (size_t)s * bStride;
-  const TA* As0 = A + (size_t)s * N * P;
+  const TA* A0 = A + (size_t)s * N * P;
+  TC* C0 = C + (size_t)s * N * Q;
+  float* W = Ws[wave];
 
-  // A tile t into registers: slot e = (row e / 64, column e % 64), zero outside.
-  float va[16];
-  auto loadA = [&](int t) {
-    const int n0 = t * kMixRows, rows = min(kMixRows, N - n0);
+  // Group g's rows into registers, raw: xa[u] = A[16 g + u][lane] at clamped
+  // indices, zeroed outside the rows and P only when stored to LDS, so that the
+  // loads are unconditional and stay in flight across the current group's work.
+  TA xa[kMixGroup];
+  auto loadA = [&](int g) {
+    const int r0 = kMixGroup * g, last = min(kMixGroup, N - r0) - 1, pc = min(lane, P - 1);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int e = threadIdx.x + 256 * u, r = e >> 6, p = e & 63;
-      va[u] = (r < rows && p < P) ? to_acc(As0[(size_t)(n0 + r) * P + p]) : 0.0f;
-    }
+    for (int u = 0; u < kMixGroup; ++u) xa[u] = A0[(size_t)(r0 + min(u, last)) * P + pc];
   };
-  int t = blockIdx.x;
-  if (t < tiles) loadA(t);  // in flight while B is staged
+  int g = blockIdx.x * 4 + wave;
+  const int gstep = gridDim.x * 4;
+  loadA(min(g, groups - 1));  // in flight while B is staged
 
   // B (4096 slots, 16 per thread), consecutive threads along its smaller stride
-  // (coalesced for W and for W^T); all loads issued before the stores.
+  // (coalesced for W and for W^T).
   {
     const bool qFast = sq < sp;
     float v[16];
@@ -67,69 +81,78 @@ mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __res
     for (int u = 0; u < 16; ++u) {
       const int e = threadIdx.x + 256 * u;
       const int q = qFast ? (e & 63) : (e >> 6), p = qFast ? (e >> 6) : (e & 63);
-      v[u] = (q < Q && p < P) ? Bm[q * sq + p * sp] : 0.0f;
+      v[u] = Bm[min(q, Q - 1) * sq + min(p, P - 1) * sp];
     }
+    // (The empty asm uses every loaded value, so the compiler cannot sink the
+    // loads into per-slot branches that would wait on each in turn.)
+#pragma unroll
+    for (int u = 0; u < 16; ++u) asm volatile("" : "+v"(v[u]));
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int e = threadIdx.x + 256 * u;
       const int q = qFast ? (e & 63) : (e >> 6), p = qFast ? (e >> 6) : (e & 63);
-      Bs[q * kMixLS + p] = v[u];
+      Bs[q * kMixLS + p] = (q < Q && p < P) ? v[u] : 0.0f;
     }
   }
-  __syncthreads();
-  const int li = lane & 15, lg = lane >> 4;
-  float bq[4][4][4];  // [column tile c][k block kb][step]: B[k = 16 kb + 4 lg + step][16 c + li]
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const float4 v = *reinterpret_cast<const float4*>(&Bs[(16 * c + li) * kMixLS + 16 * kb + 4 * lg]);
-      bq[c][kb][0] = v.x; bq[c][kb][1] = v.y; bq[c][kb][2] = v.z; bq[c][kb][3] = v.w;
-    }
+  __syncthreads();  // the only workgroup barrier: from here on each wave works alone
 
-  // Tiles t, t + gridDim.x, ...: the next tile's rows are loaded while this one's
-  // products run.
-  for (; t < tiles; t += gridDim.x) {
+  const float invQ = 1.0f / (float)Q;
+  for (; g < groups; g += gstep) {
+    const int r0 = kMixGroup * g, rows = min(kMixGroup, N - r0);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int e = threadIdx.x + 256 * u;
-      As[(e >> 6) * kMixLS + (e & 63)] = va[u];
-    }
-    __syncthreads();
-    if (t + (int)gridDim.x < tiles) loadA(t + gridDim.x);
+    for (int u = 0; u < kMixGroup; ++u) W[u * kMixLS + lane] = (u < rows && lane < P) ? to_acc(xa[u]) : 0.0f;
+    wave_lds_sync();
+    loadA(min(g + gstep, groups - 1));  // the last group reloads itself (cached)
     v4f acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const float4 v = *reinterpret_cast<const float4*>(&As[(16 * wave + li) * kMixLS + 16 * kb + 4 * lg]);
-      const float a[4] = {v.x, v.y, v.z, v.w};
+      const float4 av = *reinterpret_cast<const float4*>(&W[li * kMixLS + 16 * kb + 4 * lg]);
+      const float a[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
+      for (int c = 0; c < 4; ++c) {
+        const float4 bv = *reinterpret_cast<const float4*>(&Bs[(16 * c + li) * kMixLS + 16 * kb + 4 * lg]);
+        const float b[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], bq[c][kb][st], acc[c], 0, 0, 0);
+        for (int st = 0; st < 4; ++st) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b[st], acc[c], 0, 0, 0);
+      }
     }
-    const int n0 = t * kMixRows, rows = min(kMixRows, N - n0);
-    TC* Cm = C + ((size_t)s * N + n0) * Q;
+    // C rows of the group through the wave's LDS rows (its A rows are read), then
+    // written as one contiguous run of rows * Q elements, 64 consecutive per store.
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * wave + 4 * lg + r, col = 16 * c + li;
-        if (row < rows && col < Q) Cm[(size_t)row * Q + col] = from_acc<TC>(acc[c][r]);
-      }
-    __syncthreads();  // every wave's reads of this tile are done before the next is stored
+      for (int r = 0; r < 4; ++r) W[(4 * lg + r) * kMixLS + 16 * c + li] = acc[c][r];
+    wave_lds_sync();
+    const int total = rows * Q;
+    TC* Cg = C0 + (size_t)r0 * Q;
+    float ov[kMixGroup];
+#pragma unroll
+    for (int j = 0; j < kMixGroup; ++j) {
+      const int f = min(lane + 64 * j, total - 1);
+      const int r = (int)(((float)f + 0.5f) * invQ), col = f - r * Q;
+      ov[j] = W[r * kMixLS + col];
+    }
+    // (Every LDS read is issued before the stores, which are masked per lane.)
+#pragma unroll
+    for (int j = 0; j < kMixGroup; ++j) asm volatile("" : "+v"(ov[j]));
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < kMixGroup; ++j)
+      if (lane + 64 * j < total) Cg[lane + 64 * j] = from_acc<TC>(ov[j]);
   }
 }
 
-// Workgroups per slice: about two per CU over the whole grid (each loops over its
-// share of the slice's 64-row tiles; measured best of 1, 2, 4 and 16 per CU).
+// Workgroups per slice: at most one 16-row group per wave, and about two
+// workgroups per CU over the whole grid (measured at config 5: 18.2 us, against
+// 20.6 / 19.8 / 19.6 us for 1 / 4 / 13 per CU).
 template <typename TA, typename TC>
 int launch_mix(const void* A, const float* B, void* C, int64_t slices, int64_t N, int P, int Q, int64_t sq,
                int64_t sp, int64_t bStride, hipStream_t st) {
-  const int64_t tiles = (N + kMixRows - 1) / kMixRows;
-  const int64_t per = std::max<int64_t>(1, std::min<int64_t>(tiles, (2 * (int64_t)num_cus() + slices - 1) / slices));
+  const int64_t groups = (N + kMixGroup - 1) / kMixGroup;
+  const int64_t per =
+      std::max<int64_t>(1, std::min<int64_t>((groups + 3) / 4, (2 * (int64_t)num_cus() + slices - 1) / slices));
   dim3 grid((unsigned)per, (unsigned)slices);
   hipLaunchKernelGGL((mix_rows_kernel<TA, TC>), grid, dim3(256), 0, st, static_cast<const TA*>(A), B,
                      static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
