@@ -55,6 +55,43 @@ def test_mix_rows_output_type(gpu, dt, out):
     assert torch.equal(c, lf.mix_rows(a, w).to(out))
 
 
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 8, 784, 49, 64), (2, 8, 784, 64, 49), (1, 3, 100, 7, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_mix_rows_wide_range(gpu, dt, shape):
+    """Entries spread over many binades (the bf16 pieces of every operand carry
+    their own exponents): still within 1e-5 of sum |a| |b| of the fp64 product."""
+    import laplacianformer_amd as lf
+
+    B, H, N, P, Q = shape
+    print(f"mix rows wide range {shape} {dt}", flush=True)
+    g = torch.Generator().manual_seed(41 + P)
+    span = 12 if dt == "f16" else 40
+    a = (gen((B, H, N, P), 42 + N, "f32") * torch.exp2(torch.randint(-span, span + 1, (B, H, N, P), generator=g)))
+    a = a.to(TORCH_DT[dt])
+    w = gen((B, H, Q, P), 43 + Q, "f32") * torch.exp2(torch.randint(-40, 41, (B, H, Q, P), generator=g).float())
+    c = lf.mix_rows(a.to(gpu), w.to(gpu))
+    _check(c, a, w, "wide range")
+
+
+def test_mix_rows_nonfinite(gpu):
+    """An infinity or NaN in a row of A, or in a column of B, makes exactly the
+    outputs it takes part in non-finite (for the products through the bf16
+    pieces an infinity may come out as NaN)."""
+    import laplacianformer_amd as lf
+
+    for (N, P, Q) in ((784, 49, 64), (784, 64, 49), (100, 7, 64)):
+        print(f"mix rows nonfinite {N}x{P}x{Q}", flush=True)
+        a = gen((1, 2, N, P), 51, "f32")
+        w = gen((1, 2, Q, P), 52, "f32")
+        a[0, 0, 5, 3] = float("inf")
+        a[0, 1, N - 1, P - 1] = float("nan")
+        w[0, 1, 2, 1] = float("-inf")
+        c = lf.mix_rows(a.to(gpu), w.to(gpu)).cpu()
+        ref = torch.matmul(a.double(), w.double().transpose(-1, -2))
+        assert torch.equal(torch.isfinite(c), torch.isfinite(ref))
+
+
 def test_mix_rows_rejects(gpu):
     import laplacianformer_amd as lf
 
