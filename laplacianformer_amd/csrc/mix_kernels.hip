@@ -6,22 +6,18 @@
 //
 // with A a tall [N, P] matrix per slice s (N in the thousands) and B a small
 // Q x P matrix addressed through element strides (so that both W and W^T are
-// read in place). The layer's K_qm . W, grad_out . W^T, V . grad_kv^T and
-// K_km . grad_kv are all of this form. With an inner dimension of at most 64
-// these products are HBM-bound (A in, C out: ~45 MB per product at config 5).
-// Each A value feeds Q multiply-adds, so a VALU kernel would read it from LDS
-// once per wave-wide FMA and be LDS-bound; the matrix cores take 4 k-steps of a
-// 16 x 16 tile per 16-byte operand read instead. C is written in fp32, fp16 or
-// bf16 (one rounding of the fp32 sum). A workgroup (4 waves) stages B once in
-// LDS (pitch 68 floats); after that single barrier each wave works alone on
-// 16-row groups g, g + 4 * gridDim.x, ... of its slice: the group's rows
-// (loaded one group ahead, unconditionally at clamped indices) go to the wave's
-// own 16 LDS rows, four 16 x 16 v_mfma_f32_16x16x4_f32 accumulators compute
-// its 16 x Q outputs with k permuted per lane (k = 16 kb + 4 (lane / 16) +
-// step) so that both operands are read as float4, and the outputs go back
-// through the same LDS rows to be stored as one contiguous run of 16 * Q
-// elements (64 consecutive per store). fp32 products and sums throughout;
-// tests compare against an fp64 product within 1e-5 of sum |a| |b|.
+// read in place), and the tall transposed product C[s][p][q] = sum_n
+// A[s][n][p] * B[s][n][q]. The layer's K_qm . W, grad_out . W^T, V . grad_kv^T
+// and K_km . grad_kv are of the first form, K_km^T V and K_qm^T grad_out of the
+// second. With inner and output widths of at most 64 they move ~32 MB per
+// product at config 5, and their fp32 products, padded to 64 x 64 tiles, take
+// about as long on the fp32 matrix cores as that HBM traffic. The main kernels
+// (mix_rows_bf16_kernel, tall_t_bf16_kernel) therefore run them on the bf16
+// matrix cores with fp32 operands split exactly into bf16 pieces, to fp32
+// accuracy; operands without 16-byte aligned rows take the fp32 MFMA kernels
+// (mix_rows_kernel, tall_t_kernel). C is written in fp32, fp16 or bf16 (one
+// rounding of the fp32 sum); tests compare against an fp64 product within 1e-5
+// of sum |a| |b|.
 #include <algorithm>
 
 #include "lf_common.h"
@@ -69,6 +65,15 @@ __device__ __forceinline__ void stage_b(float* Bs, const float* __restrict__ Bm,
   }
 }
 
+// The fp32-MFMA row product for any alignment: a workgroup (4 waves) stages B
+// once in LDS (pitch 68 floats); after that single barrier each wave works
+// alone on 16-row groups g, g + 4 * gridDim.x, ... of its slice: the group's
+// rows (loaded one group ahead, unconditionally at clamped indices) go to the
+// wave's own 16 LDS rows, four 16 x 16 v_mfma_f32_16x16x4_f32 accumulators
+// compute its 16 x Q outputs with k permuted per lane (k = 16 kb + 4 (lane / 16)
+// + step) so that both operands are read as float4, and the outputs go back
+// through the same LDS rows to be stored as one contiguous run of 16 * Q
+// elements (64 consecutive per store).
 template <typename TA, typename TC>
 __global__ void __launch_bounds__(256)
 mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __restrict__ C, int N, int P,
