@@ -27,7 +27,7 @@ EXT_PATH = os.path.join(PKG_DIR, EXT_NAME + ".so")
 
 HIP_SOURCES = ["laplace_kernels.hip", "laplace_bwd2.hip", "laplace_fwd2.hip", "newton_kernels.hip", "mix_kernels.hip",
                "lf_runtime.hip", "laplace_noalloc.hip"]
-TORCH_SOURCES = ["wrapper.cpp", "LaplaceSubtraction_hip.cpp", "NewtonInverse_hip.cpp"]
+TORCH_SOURCES = ["wrapper.cpp", "LaplaceSubtraction_hip.cpp", "NewtonInverse_hip.cpp", "LaplacianAttention_hip.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

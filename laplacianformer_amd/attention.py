@@ -27,7 +27,7 @@ import math
 import torch
 
 from ._lib import ext
-from .functional import _acc_type, laplace_kernel, mix_rows, newton_inverse, tall_mix, tall_product, tall_t
+from .functional import _acc_type, laplace_kernel, newton_inverse, tall_mix, tall_product
 
 
 def landmarks(k: torch.Tensor, grid: tuple[int, int], pool: int, dtype: torch.dtype | None = None) -> torch.Tensor:
@@ -64,80 +64,26 @@ class _PooledLandmarks(torch.autograd.Function):
         return gs.expand(B, H, gh // p, p, gw // p, p, d).reshape(B, H, N, d), None, None, None
 
 
-def _kernel_fwd(query: torch.Tensor, key_cm: torch.Tensor, scale: float) -> torch.Tensor:
-    """exp(-scale * L1(query, key)) in fp32: the fused HIP op, or the composition
-    LaplaceKernelFunction falls back to (same arithmetic)."""
-    B, H, N, _ = query.shape
-    out = torch.empty((B, H, N, key_cm.shape[3]), dtype=torch.float32, device=query.device)
-    if ext().LaplaceKernel_forward(query, key_cm, out, scale):
-        return out
-    dist = torch.empty_like(out)
-    ext().LaplaceSubtraction_forward(query.float(), key_cm.float(), dist)
-    return torch.exp(dist * -scale)
-
-
-def _kernel_bwd(grad: torch.Tensor, kern: torch.Tensor, query: torch.Tensor, key_cm: torch.Tensor, scale: float):
-    """(grad_query, grad_key) of exp(-scale * L1(query, key_cm)) for fp32 dL/dK = grad."""
-    dq, dk = torch.empty_like(query), torch.empty_like(key_cm)
-    if ext().LaplaceKernel_backward(grad, kern, query, key_cm, dq, dk, scale):
-        return dq, dk
-    qa, ka = query.float(), key_cm.float()
-    dqa, dka = torch.empty_like(qa), torch.empty_like(ka)
-    ext().LaplaceSubtraction_backward(grad * kern * -scale, qa, ka, dqa, dka)
-    return dqa.to(query.dtype), dka.to(key_cm.dtype)
-
-
 class _AttentionFunction(torch.autograd.Function):
     """The whole layer as one autograd node for 16-bit / fp32 inputs whose widths the
     row-product kernel takes (d, M <= 64): the same operations as the composition in
-    laplacian_attention, issued directly on both sides (one node instead of about ten,
-    so an eager step is not bound by the host's autograd bookkeeping)."""
+    laplacian_attention, issued by the extension's LaplacianAttention_forward /
+    LaplacianAttention_backward (csrc/torch/LaplacianAttention_hip.cpp), so that an
+    eager step makes one host call per direction instead of about forty."""
 
     @staticmethod
     def forward(ctx, q, k, v, grid, pool, iters):
-        in_dtype = q.dtype
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        d = q.shape[-1]
-        s = 1.0 / math.sqrt(d)
-        km = landmarks(k, grid, pool, dtype=torch.float32).to(in_dtype)   # [B,H,M,d]
-        km_cm = km.transpose(-1, -2).contiguous()                          # [B,H,d,M]
-        k_qm = _kernel_fwd(q, km_cm, s)
-        k_mm = _kernel_fwd(km, km_cm, s)
-        k_km = _kernel_fwd(k, km_cm, s)
-        inv = torch.empty_like(k_mm)
-        ext().NewtonInverse_forward(k_mm, inv, int(iters))
-        kv = tall_t(k_km, v)                                               # K_km^T V  [B,H,M,d]
-        w = torch.matmul(inv, kv)                                         # [B,H,M,d]
-        out = mix_rows(k_qm, w.transpose(-1, -2), in_dtype)              # K_qm W, rounded once
-        ctx.grid, ctx.pool, ctx.s = grid, pool, s
-        ctx.save_for_backward(q, k, v, km, km_cm, k_qm, k_mm, k_km, inv, kv, w)
+        gh, gw = grid
+        out, *saved = ext().LaplacianAttention_forward(q, k, v, gh, gw, pool, int(iters))
+        ctx.grid, ctx.pool = grid, pool
+        # saved = km, km_cm, k_qm, k_mm, k_km, inv, kv, w (q, k, v as made contiguous there)
+        ctx.save_for_backward(q.contiguous(), k.contiguous(), v.contiguous(), *saved)
         return out
 
     @staticmethod
     def backward(ctx, g):
-        q, k, v, km, km_cm, k_qm, k_mm, k_km, inv, kv, w = ctx.saved_tensors
-        s, p = ctx.s, ctx.pool
-        g = g.contiguous()
-        d_kqm = mix_rows(g, w, torch.float32)                             # G W^T       [B,H,N,M]
-        d_w = tall_t(k_qm, g)                                             # K_qm^T G    [B,H,M,d]
-        d_inv = torch.matmul(d_w, kv.transpose(-1, -2))                   # [B,H,M,M]
-        d_kv = torch.matmul(inv.transpose(-1, -2), d_w)                   # [B,H,M,d]
-        d_kkm = mix_rows(v, d_kv, torch.float32)                          # V dkv^T     [B,H,N,M]
-        d_v = mix_rows(k_km, d_kv.transpose(-1, -2), v.dtype)             # K_km dkv    [B,H,N,d]
-        d_kmm = torch.empty_like(k_mm)
-        ext().NewtonInverse_backward(d_inv.contiguous(), inv, d_kmm)
-        d_q, d_cm = _kernel_bwd(d_kqm, k_qm, q, km_cm, s)
-        d_km, d_cm2 = _kernel_bwd(d_kmm, k_mm, km, km_cm, s)
-        d_k, d_cm3 = _kernel_bwd(d_kkm, k_km, k, km_cm, s)
-        d_cm += d_cm2
-        d_cm += d_cm3
-        d_km += d_cm.transpose(-1, -2)
-        # Pooling's backward: each landmark's gradient / pool^2 on its pool x pool patch
-        # (divided in fp32, rounded once), added to the distance gradient of k in place.
-        B, H, N, dd = k.shape
         gh, gw = ctx.grid
-        gs = (d_km.float() / (p * p)).to(d_k.dtype)
-        d_k.view(B, H, gh // p, p, gw // p, p, dd).add_(gs.view(B, H, gh // p, 1, gw // p, 1, dd))
+        d_q, d_k, d_v = ext().LaplacianAttention_backward(g, list(ctx.saved_tensors), gh, gw, ctx.pool)
         return d_q, d_k, d_v, None, None, None
 
 

@@ -1,0 +1,143 @@
+// The LaplacianFormer attention layer's forward and backward as two host
+// functions (no reference counterpart: the reference ships the two operators
+// only). They issue the same operations, in the same order, as the per-op
+// composition in attention.py (landmark pooling, three fused Laplacian-kernel
+// distances, NewtonInverse, the tall products and the M x M GEMMs), so that an
+// eager training step pays one Python call per direction instead of about
+// forty: at config 5 the host's per-op dispatch, not the GPU, bounded the step.
+//
+//   Km  = pool x pool mean of K over the gh x gw grid (fp32 sums, input type)
+//   K_xy = exp(-s L1(x, y)), s = 1 / sqrt(d), fp32
+//   out = K_qm . W,  W = NewtonInverse(K_mm) . (K_km^T V)
+#include <ATen/ATen.h>
+#include <torch/types.h>
+
+#include <cmath>
+#include <vector>
+
+#include "LaplaceSubtraction.h"
+#include "LaplacianAttention.h"
+#include "NewtonInverse.h"
+
+namespace laplace {
+
+namespace {
+
+// exp(-scale * L1(query, key_cm)) in fp32: the fused op, or the composition of
+// the distance and an exp where the fused path does not take the shape.
+at::Tensor kernel_fwd(const at::Tensor& query, const at::Tensor& key_cm, double scale) {
+  at::Tensor out = at::empty({query.size(0), query.size(1), query.size(2), key_cm.size(3)},
+                             query.options().dtype(at::kFloat));
+  if (LaplaceKernel_forward(query, key_cm, out, scale)) return out;
+  at::Tensor dist = at::empty_like(out);
+  LaplaceSubtraction_forward(query.to(at::kFloat), key_cm.to(at::kFloat), dist);
+  return at::exp(dist * -scale);
+}
+
+// (grad_query, grad_key) of exp(-scale * L1(query, key_cm)) for the fp32 dL/dK = grad.
+std::pair<at::Tensor, at::Tensor> kernel_bwd(const at::Tensor& grad, const at::Tensor& kern, const at::Tensor& query,
+                                             const at::Tensor& key_cm, double scale) {
+  at::Tensor dq = at::empty_like(query), dk = at::empty_like(key_cm);
+  if (LaplaceKernel_backward(grad, kern, query, key_cm, dq, dk, scale)) return {dq, dk};
+  at::Tensor qa = query.to(at::kFloat), ka = key_cm.to(at::kFloat);
+  at::Tensor dqa = at::empty_like(qa), dka = at::empty_like(ka);
+  LaplaceSubtraction_backward(grad * kern * -scale, qa, ka, dqa, dka);
+  return {dqa.to(query.scalar_type()), dka.to(key_cm.scalar_type())};
+}
+
+// c[..., n, q] = sum_p a[..., n, p] * b_qp[..., q, p] in fp32, stored as `out`.
+at::Tensor mix_rows(const at::Tensor& a, const at::Tensor& b_qp, at::ScalarType out) {
+  std::vector<int64_t> shape(a.sizes().begin(), a.sizes().end());
+  shape.back() = b_qp.size(-2);
+  at::Tensor c = at::empty(shape, a.options().dtype(out));
+  MixRows(a.contiguous(), b_qp.to(at::kFloat), c);
+  return c;
+}
+
+// a^T b over the rows, fp32 [..., P, Q].
+at::Tensor tall_t(const at::Tensor& a, const at::Tensor& b) {
+  std::vector<int64_t> shape(a.sizes().begin(), a.sizes().end());
+  shape[shape.size() - 2] = a.size(-1);
+  shape.back() = b.size(-1);
+  at::Tensor c = at::empty(shape, a.options().dtype(at::kFloat));
+  TallT(a.contiguous(), b.contiguous(), c);
+  return c;
+}
+
+void check_layer(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t gh, int64_t gw,
+                 int64_t pool) {
+  TORCH_CHECK(q.dim() == 4 && k.sizes() == q.sizes() && v.sizes() == q.sizes(),
+              "laplacian attention: q, k, v must be [B,H,N,d] of one shape");
+  TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
+              "laplacian attention: q, k, v must have one type");
+  TORCH_CHECK(q.scalar_type() == at::kFloat || q.scalar_type() == at::kHalf || q.scalar_type() == at::kBFloat16,
+              "laplacian attention: float32, float16 or bfloat16 inputs");
+  TORCH_CHECK(pool > 0 && gh > 0 && gw > 0 && gh * gw == q.size(2) && gh % pool == 0 && gw % pool == 0,
+              "laplacian attention: token grid ", gh, "x", gw, " does not match N=", q.size(2), " or pool=", pool);
+  const int64_t M = (gh / pool) * (gw / pool);
+  TORCH_CHECK(q.size(3) <= 64 && M <= 64, "laplacian attention: d and the landmark count must be <= 64");
+}
+
+}  // namespace
+
+// Returns {out, km, km_cm, k_qm, k_mm, k_km, inv, kv, w}: the output and what
+// the backward reads.
+std::vector<at::Tensor> LaplacianAttention_forward(at::Tensor q, at::Tensor k, at::Tensor v, int64_t gh, int64_t gw,
+                                                   int64_t pool, int64_t iters) {
+  check_layer(q, k, v, gh, gw, pool);
+  const at::ScalarType in = q.scalar_type();
+  q = q.contiguous();
+  k = k.contiguous();
+  v = v.contiguous();
+  const int64_t B = q.size(0), H = q.size(1), d = q.size(3);
+  const double s = 1.0 / std::sqrt((double)d);
+  at::Tensor km = k.reshape({B, H, gh / pool, pool, gw / pool, pool, d})
+                      .mean({3, 5}, false, at::kFloat)
+                      .reshape({B, H, -1, d})
+                      .to(in);                                   // [B,H,M,d]
+  at::Tensor km_cm = km.transpose(-1, -2).contiguous();          // [B,H,d,M]
+  at::Tensor k_qm = kernel_fwd(q, km_cm, s);
+  at::Tensor k_mm = kernel_fwd(km, km_cm, s);
+  at::Tensor k_km = kernel_fwd(k, km_cm, s);
+  at::Tensor inv = at::empty_like(k_mm);
+  NewtonInverse_forward(k_mm, inv, iters);
+  at::Tensor kv = tall_t(k_km, v);                               // K_km^T V  [B,H,M,d]
+  at::Tensor w = at::matmul(inv, kv);                            // [B,H,M,d]
+  at::Tensor out = mix_rows(k_qm, w.transpose(-1, -2), in);      // K_qm W, rounded once
+  return {out, km, km_cm, k_qm, k_mm, k_km, inv, kv, w};
+}
+
+// saved = {q, k, v, km, km_cm, k_qm, k_mm, k_km, inv, kv, w}; returns {d_q, d_k, d_v}.
+std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at::Tensor> saved, int64_t gh,
+                                                    int64_t gw, int64_t pool) {
+  TORCH_CHECK(saved.size() == 11, "laplacian attention backward: 11 saved tensors expected");
+  const at::Tensor &q = saved[0], &k = saved[1], &v = saved[2], &km = saved[3], &km_cm = saved[4];
+  const at::Tensor &k_qm = saved[5], &k_mm = saved[6], &k_km = saved[7], &inv = saved[8], &kv = saved[9];
+  const at::Tensor& w = saved[10];
+  check_layer(q, k, v, gh, gw, pool);
+  TORCH_CHECK(g.sizes() == q.sizes(), "laplacian attention backward: grad_output must be [B,H,N,d]");
+  const int64_t B = k.size(0), H = k.size(1), dd = k.size(3);
+  const double s = 1.0 / std::sqrt((double)dd);
+  g = g.contiguous();
+  at::Tensor d_kqm = mix_rows(g, w, at::kFloat);                        // G W^T       [B,H,N,M]
+  at::Tensor d_w = tall_t(k_qm, g);                                      // K_qm^T G    [B,H,M,d]
+  at::Tensor d_inv = at::matmul(d_w, kv.transpose(-1, -2));              // [B,H,M,M]
+  at::Tensor d_kv = at::matmul(inv.transpose(-1, -2), d_w);              // [B,H,M,d]
+  at::Tensor d_kkm = mix_rows(v, d_kv, at::kFloat);                      // V dkv^T     [B,H,N,M]
+  at::Tensor d_v = mix_rows(k_km, d_kv.transpose(-1, -2), v.scalar_type());  // K_km dkv [B,H,N,d]
+  at::Tensor d_kmm = at::empty_like(k_mm);
+  NewtonInverse_backward(d_inv.contiguous(), inv, d_kmm);
+  auto [d_q, d_cm] = kernel_bwd(d_kqm, k_qm, q, km_cm, s);
+  auto [d_km, d_cm2] = kernel_bwd(d_kmm, k_mm, km, km_cm, s);
+  auto [d_k, d_cm3] = kernel_bwd(d_kkm, k_km, k, km_cm, s);
+  d_cm.add_(d_cm2);
+  d_cm.add_(d_cm3);
+  d_km.add_(d_cm.transpose(-1, -2));
+  // Pooling's backward: each landmark's gradient / pool^2 on its pool x pool
+  // patch (divided in fp32, rounded once), added to k's distance gradient.
+  at::Tensor gs = (d_km.to(at::kFloat) / (double)(pool * pool)).to(d_k.scalar_type());
+  d_k.view({B, H, gh / pool, pool, gw / pool, pool, dd}).add_(gs.view({B, H, gh / pool, 1, gw / pool, 1, dd}));
+  return {d_q, d_k, d_v};
+}
+
+}  // namespace laplace

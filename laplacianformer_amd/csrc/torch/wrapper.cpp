@@ -9,6 +9,7 @@
 
 #include "../../../include/laplacianformer_amd.h"
 #include "LaplaceSubtraction.h"
+#include "LaplacianAttention.h"
 #include "NewtonInverse.h"
 
 namespace laplace {
@@ -62,6 +63,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("MixRows", &MixRows,
         "MixRows (a, b, c): c[..., n, q] = sum_p a[..., n, p] * b[..., q, p] in float32, widths <= 64 "
         "(the attention layer's products; b is read through its strides)");
+  m.def("LaplacianAttention_forward", &LaplacianAttention_forward,
+        "LaplacianAttention_forward (q, k, v, gh, gw, pool, iters) -> [out, km, km_cm, k_qm, k_mm, k_km, inv, kv, w] "
+        "(the attention layer's forward; the rest is what its backward reads)");
+  m.def("LaplacianAttention_backward", &LaplacianAttention_backward,
+        "LaplacianAttention_backward (grad_out, saved, gh, gw, pool) -> [d_q, d_k, d_v]");
   m.def("TallT", &TallT,
         "TallT (a, b, c): c[..., p, q] = sum_n a[..., n, p] * b[..., n, q], a and c float32, widths <= 64 "
         "(the attention layer's K^T V products)");
