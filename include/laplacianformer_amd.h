@@ -204,6 +204,22 @@ size_t lfamd_tall_t_workspace_size(int64_t slices, int64_t rows);
 int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t slices, int64_t rows,
                  int inner, int cols, void* workspace, size_t workspace_bytes, void* stream);
 
+/* km[b][h][m][c] = (sum over the pool x pool patch m of k[b][h][n][c]) / pool^2, summed in fp32 and
+ * rounded once to `dtype` (F32, F16 or BF16), for k [B][H][gh*gw][d] on a gh x gw token grid
+ * (gh, gw multiples of pool; M = (gh/pool)*(gw/pool), patches row-major); written as km
+ * [B][H][M][d] and channel-major as km_cm [B][H][d][M], all contiguous. No reference counterpart:
+ * the attention layer's landmark pooling. */
+int lfamd_landmark_pool(int dtype, const void* k, void* km, void* km_cm, int64_t B, int64_t H, int gh,
+                        int gw, int pool, int d, void* stream);
+
+/* Backward of the pooling with the landmarks' gradient assembled from its parts: with every
+ * operation rounded to `dtype`, t = (dcm0 + dcm1) + dcm2 ([B][H][d][M]), u = dkm + t^T
+ * ([B][H][M][d]), and dk[b][h][n][c] += u[b][h][m(n)][c] / pool^2 in place ([B][H][gh*gw][d]).
+ * No reference counterpart (the attention layer's). */
+int lfamd_landmark_pool_backward(int dtype, void* dk, const void* dkm, const void* dcm0, const void* dcm1,
+                                 const void* dcm2, int64_t B, int64_t H, int gh, int gw, int pool, int d,
+                                 void* stream);
+
 /* ---- Runtime ------------------------------------------------------------ */
 
 /* HIP runtime version as major*100 + minor (e.g. 700 for 7.0), the convention

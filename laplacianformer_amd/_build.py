@@ -26,7 +26,7 @@ EXT_NAME = "Laplace_subtraction_cuda"
 EXT_PATH = os.path.join(PKG_DIR, EXT_NAME + ".so")
 
 HIP_SOURCES = ["laplace_kernels.hip", "laplace_bwd2.hip", "laplace_fwd2.hip", "newton_kernels.hip", "mix_kernels.hip",
-               "lf_runtime.hip", "laplace_noalloc.hip"]
+               "layer_kernels.hip", "lf_runtime.hip", "laplace_noalloc.hip"]
 TORCH_SOURCES = ["wrapper.cpp", "LaplaceSubtraction_hip.cpp", "NewtonInverse_hip.cpp", "LaplacianAttention_hip.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -1,10 +1,12 @@
 // The LaplacianFormer attention layer's forward and backward as two host
 // functions (no reference counterpart: the reference ships the two operators
-// only). They issue the same operations, in the same order, as the per-op
-// composition in attention.py (landmark pooling, three fused Laplacian-kernel
-// distances, NewtonInverse, the tall products and the M x M GEMMs), so that an
-// eager training step pays one Python call per direction instead of about
-// forty: at config 5 the host's per-op dispatch, not the GPU, bounded the step.
+// only). They issue the operations of the per-op composition in attention.py
+// (landmark pooling, three fused Laplacian-kernel distances, NewtonInverse,
+// the tall products and the M x M GEMMs), with the pooling and its backward
+// (including the sum of the landmarks' gradient parts) as one kernel each, so
+// that an eager training step pays one Python call per direction instead of
+// about forty: at config 5 the host's per-op dispatch, not the GPU, bounded
+// the step.
 //
 //   Km  = pool x pool mean of K over the gh x gw grid (fp32 sums, input type)
 //   K_xy = exp(-s L1(x, y)), s = 1 / sqrt(d), fp32
@@ -18,6 +20,7 @@
 #include "LaplaceSubtraction.h"
 #include "LaplacianAttention.h"
 #include "NewtonInverse.h"
+#include "torch_common.h"
 
 namespace laplace {
 
@@ -91,11 +94,13 @@ std::vector<at::Tensor> LaplacianAttention_forward(at::Tensor q, at::Tensor k, a
   v = v.contiguous();
   const int64_t B = q.size(0), H = q.size(1), d = q.size(3);
   const double s = 1.0 / std::sqrt((double)d);
-  at::Tensor km = k.reshape({B, H, gh / pool, pool, gw / pool, pool, d})
-                      .mean({3, 5}, false, at::kFloat)
-                      .reshape({B, H, -1, d})
-                      .to(in);                                   // [B,H,M,d]
-  at::Tensor km_cm = km.transpose(-1, -2).contiguous();          // [B,H,d,M]
+  const int64_t M = (gh / pool) * (gw / pool);
+  at::Tensor km = at::empty({B, H, M, d}, q.options());          // landmarks [B,H,M,d]
+  at::Tensor km_cm = at::empty({B, H, d, M}, q.options());       // and channel-major [B,H,d,M]
+  at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  detail::check_status(lfamd_landmark_pool(detail::abi_dtype(k, "laplacian attention"), k.data_ptr(),
+                                           km.data_ptr(), km_cm.data_ptr(), B, H, (int)gh, (int)gw, (int)pool,
+                                           (int)d, detail::stream_of(k)));
   at::Tensor k_qm = kernel_fwd(q, km_cm, s);
   at::Tensor k_mm = kernel_fwd(km, km_cm, s);
   at::Tensor k_km = kernel_fwd(k, km_cm, s);
@@ -130,13 +135,12 @@ std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at
   auto [d_q, d_cm] = kernel_bwd(d_kqm, k_qm, q, km_cm, s);
   auto [d_km, d_cm2] = kernel_bwd(d_kmm, k_mm, km, km_cm, s);
   auto [d_k, d_cm3] = kernel_bwd(d_kkm, k_km, k, km_cm, s);
-  d_cm.add_(d_cm2);
-  d_cm.add_(d_cm3);
-  d_km.add_(d_cm.transpose(-1, -2));
-  // Pooling's backward: each landmark's gradient / pool^2 on its pool x pool
-  // patch (divided in fp32, rounded once), added to k's distance gradient.
-  at::Tensor gs = (d_km.to(at::kFloat) / (double)(pool * pool)).to(d_k.scalar_type());
-  d_k.view({B, H, gh / pool, pool, gw / pool, pool, dd}).add_(gs.view({B, H, gh / pool, 1, gw / pool, 1, dd}));
+  // The landmarks' gradient, d_km + (d_cm + d_cm2 + d_cm3)^T, / pool^2 onto each
+  // pool x pool patch of k's distance gradient (every step rounded to the type).
+  at::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
+  detail::check_status(lfamd_landmark_pool_backward(
+      detail::abi_dtype(d_k, "laplacian attention backward"), d_k.data_ptr(), d_km.data_ptr(), d_cm.data_ptr(),
+      d_cm2.data_ptr(), d_cm3.data_ptr(), B, H, (int)gh, (int)gw, (int)pool, (int)dd, detail::stream_of(d_k)));
   return {d_q, d_k, d_v};
 }
 
