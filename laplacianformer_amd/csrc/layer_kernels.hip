@@ -16,8 +16,8 @@
 //   u   = cast(dkm + t^T)
 //   dk += cast(f32(u) * f32(1 / pool^2))   (dk += : cast(f32(dk) + f32(.)))
 // (a tensor divided by a scalar is multiplied by the scalar's fp32 reciprocal)
-// A workgroup per token row stages its landmark row's share in LDS, then adds
-// it to the row's gw * d gradient elements (contiguous).
+// A workgroup per landmark row stages the row's share in LDS, then adds it to
+// the pool token rows under it (one contiguous strip of K's gradient).
 #include <algorithm>
 
 #include "lf_common.h"
@@ -84,33 +84,42 @@ __device__ __forceinline__ void pool_bwd_stage(float* __restrict__ tt, float* __
   __syncthreads();
 }
 
-// Grid (gh token rows, B*H), 256 threads: the row's landmark gradient share
-// staged in LDS once (mw * d <= kPoolLds), then the row's gw * d elements of
-// K's gradient, eight loads per thread in flight.
+// Grid (gh / pool landmark rows, B*H), 256 threads: the landmark row's
+// gradient share staged in LDS once (mw * d <= kPoolLds) and spread to a token
+// row's gw * d elements (<= 8 * 256), then added to the pool token rows of K's
+// gradient under it (one contiguous strip), the next row's loads in flight.
 template <typename T>
 __global__ void __launch_bounds__(256)
 landmark_pool_bwd_kernel(T* __restrict__ dk, const T* __restrict__ dkm, const T* __restrict__ dcm0,
                          const T* __restrict__ dcm1, const T* __restrict__ dcm2, int gh, int gw, int pool, int d) {
-  __shared__ float tt[kPoolLds], gsm[kPoolLds];
-  const int y = blockIdx.x, mw = gw / pool, M = (gh / pool) * mw;
+  __shared__ float tt[kPoolLds], gsm[kPoolLds], gsx[8 * 256];
+  const int my = blockIdx.x, mw = gw / pool, M = (gh / pool) * mw;
   const int64_t bh = blockIdx.y;
-  pool_bwd_stage<T>(tt, gsm, dkm, dcm0, dcm1, dcm2, bh, y / pool, mw, M, d, 1.0f / (float)(pool * pool));
-  T* row = dk + (bh * gh + y) * (int64_t)gw * d;
-  const int total = gw * d;
-  for (int e0 = threadIdx.x; e0 < total; e0 += 8 * 256) {
-    T v[8];
+  const int R = gw * d;  // elements of one token row
+  T* strip = dk + (bh * gh + (int64_t)my * pool) * R;
+  T v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = row[min(e0 + 256 * i, total - 1)];
+  for (int k = 0; k < 8; ++k) v[k] = strip[min((int)threadIdx.x + 256 * k, R - 1)];  // row 0, during the staging
+  pool_bwd_stage<T>(tt, gsm, dkm, dcm0, dcm1, dcm2, bh, my, mw, M, d, 1.0f / (float)(pool * pool));
+  for (int e = threadIdx.x; e < R; e += 256) {
+    const int x = e / d, c = e - x * d;
+    gsx[e] = gsm[(x / pool) * d + c];
+  }
+  __syncthreads();
+  for (int i = 0; i < pool; ++i) {
+    T w[8];
+    const int in = min(i + 1, pool - 1);  // (the last row reloads itself)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(v[i]));  // (all eight loads before the stores)
+    for (int k = 0; k < 8; ++k) w[k] = strip[(int64_t)in * R + min((int)threadIdx.x + 256 * k, R - 1)];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = e0 + 256 * i;
-      if (e < total) {
-        const int x = e / d, c = e - x * d;
-        row[e] = from_acc<T>(to_acc(v[i]) + gsm[(x / pool) * d + c]);
-      }
+    for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(w[k]));  // (issued before this row's stores)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = threadIdx.x + 256 * k;
+      if (e < R) strip[(int64_t)i * R + e] = from_acc<T>(to_acc(v[k]) + gsx[e]);
     }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = w[k];
   }
 }
 
@@ -138,11 +147,14 @@ landmark_pool_bwd_any_kernel(T* __restrict__ dk, const T* __restrict__ dkm, cons
 template <typename T>
 void launch_pool_bwd(void* dk, const void* dkm, const void* dcm0, const void* dcm1, const void* dcm2, int64_t BH,
                      int gh, int gw, int pool, int d, hipStream_t st) {
-  const dim3 grid((unsigned)gh, (unsigned)BH);
-  auto kern = (int64_t)(gw / pool) * d <= kPoolLds ? landmark_pool_bwd_kernel<T> : landmark_pool_bwd_any_kernel<T>;
-  hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, static_cast<T*>(dk), static_cast<const T*>(dkm),
-                     static_cast<const T*>(dcm0), static_cast<const T*>(dcm1), static_cast<const T*>(dcm2), gh, gw,
-                     pool, d);
+  if ((int64_t)(gw / pool) * d <= kPoolLds && (int64_t)gw * d <= 8 * 256)
+    hipLaunchKernelGGL(landmark_pool_bwd_kernel<T>, dim3((unsigned)(gh / pool), (unsigned)BH), dim3(256), 0, st,
+                       static_cast<T*>(dk), static_cast<const T*>(dkm), static_cast<const T*>(dcm0),
+                       static_cast<const T*>(dcm1), static_cast<const T*>(dcm2), gh, gw, pool, d);
+  else
+    hipLaunchKernelGGL(landmark_pool_bwd_any_kernel<T>, dim3((unsigned)gh, (unsigned)BH), dim3(256), 0, st,
+                       static_cast<T*>(dk), static_cast<const T*>(dkm), static_cast<const T*>(dcm0),
+                       static_cast<const T*>(dcm1), static_cast<const T*>(dcm2), gh, gw, pool, d);
 }
 
 int check_pool(int dtype, int64_t B, int64_t H, int gh, int gw, int pool, int d, const char* what) {
