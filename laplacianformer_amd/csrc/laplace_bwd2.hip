@@ -56,6 +56,7 @@ namespace {
 constexpr int kB2Waves = 8;     // waves per workgroup (2 per SIMD)
 constexpr int kB2Unroll = 4;    // rows per iteration of the asm row loop (its query prefetch depth)
 constexpr int kB2MaxRows = 512;  // most grad rows of one workgroup (staged in LDS at once)
+constexpr int kB2SoloRows = 64;  // slices up to this many rows take one workgroup each
 constexpr int kB2Threads = 64 * kB2Waves;
 
 // Layout constants shared by the kernel and the host plan.
@@ -172,7 +173,7 @@ template <typename T, int M, bool DQ, bool DK, bool GK = false>
 __global__ void __launch_bounds__(kB2Threads, 1)
 laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, const float* __restrict__ kv,
                     float gscale, const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ dq,
-                    float* __restrict__ partial, int N, int C) {
+                    float* __restrict__ partial, T* __restrict__ dkOut, int N, int C) {
   constexpr B2Shape S{M};
   constexpr int JC = S.JC, HP = S.HP, PITCH = S.PITCH, NKK = S.NKK;
   static_assert(M >= 2, "M >= 2");
@@ -353,13 +354,17 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
     }
   }
   __syncthreads();
-  float* out = partial + (((size_t)bh * ncb + cb) * nx + x) * 64 * M;   // [64][M] channel-major
+  // [64][M] channel-major: the workgroup's partial, or with one workgroup per
+  // slice (dkOut) grad_key itself, rounded once.
   for (int t = tid; t < 64 * M; t += kB2Threads) {
     const int c = t / M, col = t - c * M;
     float s2 = red[col * 65 + c];
 #pragma unroll
     for (int w = 1; w < kB2Waves; ++w) s2 += red[w * M * 65 + col * 65 + c];
-    out[t] = s2;
+    if (dkOut)
+      dkOut[((size_t)bh * C + cb * 64) * M + t] = from_acc<T>(s2);
+    else
+      partial[(((size_t)bh * ncb + cb) * nx + x) * 64 * M + t] = s2;
   }
 }
 
@@ -399,12 +404,16 @@ B2Plan plan_b2(int64_t BH, int64_t N, int64_t M, int64_t C) {
   p.ncb = (int)(C / 64);
   const int64_t slices = BH * p.ncb;
   // One workgroup per CU where the rows allow (at least 8 rows each), and never
-  // more than kB2MaxRows rows per workgroup (its LDS holds that many).
-  p.nx = (int)std::max<int64_t>((N + kB2MaxRows - 1) / kB2MaxRows,
-                                std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
-                                                                       (N + kB2Waves - 1) / kB2Waves)));
+  // more than kB2MaxRows rows per workgroup (its LDS holds that many). Up to
+  // kB2SoloRows rows a slice takes one workgroup, which writes grad_key itself
+  // (no partials, no reduction launch).
+  p.nx = N <= kB2SoloRows
+             ? 1
+             : (int)std::max<int64_t>((N + kB2MaxRows - 1) / kB2MaxRows,
+                                      std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
+                                                                             (N + kB2Waves - 1) / kB2Waves)));
   p.lds = (size_t)B2Shape((int)M).lds_bytes();
-  p.partialElems = (size_t)slices * p.nx * 64 * (size_t)M;
+  p.partialElems = p.nx == 1 ? 0 : (size_t)slices * p.nx * 64 * (size_t)M;
   return p;
 }
 
@@ -412,16 +421,17 @@ template <typename T, int M, bool DQ, bool DK>
 int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, int64_t BH, int64_t N,
                 int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg) {
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
+  T* dkOut = DK && p.nx == 1 ? static_cast<T*>(dk) : nullptr;
   if (kg.gk)
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(kB2Threads), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)N, (int)C);
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
   else
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, false>), grid, dim3(kB2Threads), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)N, (int)C);
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
   int s = check_launch("laplace backward (column-split)");
-  if (s || !DK) return s;
+  if (s || !DK || dkOut) return s;
   dim3 rgrid((64 * M + 255) / 256, p.ncb, (unsigned)BH);
   hipLaunchKernelGGL(laplace_dk_reduce_t_kernel<T>, rgrid, dim3(256), 0, st, static_cast<const float*>(ws),
                      static_cast<T*>(dk), p.nx, M, (int)C);
@@ -465,7 +475,7 @@ size_t b2_workspace_elems(int64_t BH, int64_t N, int64_t M, int64_t C) {
 int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, size_t wsBytes,
               int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who, const B2Grad& kg) {
   const B2Plan p = plan_b2(BH, N, M, C);
-  if (dk && (!ws || wsBytes < p.partialElems * 4))
+  if (dk && p.partialElems && (!ws || wsBytes < p.partialElems * 4))
     return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, p.partialElems * 4, wsBytes);
   if (kg.gk && dtype != LFAMD_F16) return fail(LFAMD_ERR_UNSUPPORTED, "%s: fused kernel gradient needs fp16", who);
   if (dq && dk) return launch_b2<true, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);

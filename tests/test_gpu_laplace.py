@@ -31,6 +31,10 @@ SHAPES = [
     (2, 1, 131, 16, 80),
     (1, 1, 7, 49, 64),
     (1, 2, 1, 49, 128),
+    # Column-split backward (16-bit, M in {16, 32, 49}, C % 64 = 0) either side of one
+    # workgroup per slice (up to 64 rows: grad_key written without partials).
+    (1, 2, 64, 32, 128),
+    (2, 1, 65, 49, 64),
     # Odd M beyond the register-resident set: column blocks with 16-bit rows of odd length.
     (1, 2, 77, 81, 64),
     (2, 1, 50, 225, 40),
