@@ -105,7 +105,8 @@ def test_mix_rows_rejects(gpu):
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("shape", [(2, 64, 784, 49, 64), (1, 3, 100, 7, 64), (1, 1, 1, 1, 1), (3, 2, 65, 64, 64),
-                                   (1, 5, 129, 33, 17), (1, 2, 3000, 49, 64), (2, 1, 0, 49, 64)],
+                                   (1, 5, 129, 33, 17), (1, 2, 3000, 49, 64), (2, 1, 0, 49, 64),
+                                   (1, 2, 96, 49, 6)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_tall_t(gpu, dt, shape):
     """c = a^T b over the rows (lfamd_tall_t, torch export TallT) against an fp64 CPU product,
