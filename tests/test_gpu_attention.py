@@ -128,3 +128,24 @@ def test_attention_first_stage_grid(gpu, dtype):
     NewtonInverse on the batched-GEMM path at n = 196, library products for widths > 64)."""
     print(f"attention 56x56 grid {dtype}", flush=True)
     _run(gpu, 2, 1, (56, 56), 32, dtype, seed=70, iters=12)
+
+
+def test_attention_host_entry_rejects(gpu):
+    """The layer's two host calls check their arguments before any launch."""
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    q = torch.randn(1, 2, 64, 16, device=gpu, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="token grid"):
+        L.LaplacianAttention_forward(q, q, q, 8, 6, 4, 10)            # 8 x 6 != 64
+    with pytest.raises(RuntimeError, match="token grid"):
+        L.LaplacianAttention_forward(q, q, q, 8, 8, 3, 10)            # 8 % 3 != 0
+    with pytest.raises(RuntimeError, match="one shape"):
+        L.LaplacianAttention_forward(q, q[:, :, :32], q, 8, 8, 4, 10)
+    with pytest.raises(RuntimeError, match="one type"):
+        L.LaplacianAttention_forward(q, q.float(), q, 8, 8, 4, 10)
+    wide = torch.randn(1, 1, 16, 80, device=gpu, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="<= 64"):
+        L.LaplacianAttention_forward(wide, wide, wide, 4, 4, 2, 10)   # d = 80
+    with pytest.raises(RuntimeError, match="11 saved"):
+        L.LaplacianAttention_backward(q, [q, q], 8, 8, 4)
