@@ -71,8 +71,14 @@ def shape(M):
     return JC, HP, HP // 4, 2 * HP + 4
 
 
-def variant(dtype, M, DQ=True, DK=True):
-    """Returns (name, C++ source, info) of the row-loop block for key count M.
+def variant(dtype, M, DQ=True, DK=True, top=256):
+    """Returns (name, C++ source, info) of the row-loop block for key count M,
+    using VGPRs below `top` (256: two waves per SIMD; 168: three).
+
+    With top < 256 the grad_key accumulators and the per-lane inputs are
+    operands bound to the block's own registers ("{vN}" constraints) rather
+    than copied in and out, so that the compiler holds no second copy of them
+    around the block.
 
     DQ / DK select the grad_query and grad_key halves of the work: without DK
     there are no grad_key accumulators, without DQ no grad_query accumulation
@@ -97,7 +103,8 @@ def variant(dtype, M, DQ=True, DK=True):
     assert RSLOT // 4 == NG - 1 and NG >= 3
     bf16 = dtype == "bf16"
 
-    r = Regs()
+    phys = top < 256
+    r = Regs(top)
     KK = r.take(4 * ((2 * JC + 3) // 4), align=4)   # 0.5 - T(k): [c][j] packed, read as b128 groups
     DK_ = r.take(2 * JC, bank=1) if DK else None      # grad_key accumulators [c][j]
     G = r.take(16, align=4)                           # grad ring: 4 slots of 4 (bank k for element k)
@@ -114,7 +121,8 @@ def variant(dtype, M, DQ=True, DK=True):
     SHF = r.take(4)       # bit offsets in the query pair: c0 value, c0 sign, c1 value, c1 sign
     PADDR = r.take(1)     # ds_bpermute address of the partner lane
     lo = r.next
-    nmine = 256 - lo
+    assert lo >= 0
+    nmine = top - lo
 
     # SGPRs (clobbered).
     S = 72
@@ -182,17 +190,19 @@ def variant(dtype, M, DQ=True, DK=True):
     add(f"s_mov_b32 s{SPR}, %[wpar]")
     add(f"s_mov_b32 s{SPC}, 0")
     add(f"s_mov_b32 s{SFLAG}, 0")
-    add(f"v_mov_b32 v{RDA}, %[rda]")
-    add(f"v_mov_b32 v{VQ4}, %[vq4]")
-    add(f"v_mov_b32 v{VQS}, %[vqs]")
-    for c in range(4):
-        add(f"v_mov_b32 v{SHF + c}, %[shf{c}]")
-    add(f"v_mov_b32 v{PADDR}, %[paddr]")
-    for k in range(UNROLL):
-        add(f"v_mov_b32 v{QR + k}, %[q0_{k}]")
+    if not phys:
+        add(f"v_mov_b32 v{RDA}, %[rda]")
+        add(f"v_mov_b32 v{VQ4}, %[vq4]")
+        add(f"v_mov_b32 v{VQS}, %[vqs]")
+        for c in range(4):
+            add(f"v_mov_b32 v{SHF + c}, %[shf{c}]")
+        add(f"v_mov_b32 v{PADDR}, %[paddr]")
+        for k in range(UNROLL):
+            add(f"v_mov_b32 v{QR + k}, %[q0_{k}]")
+    kka = f"v{T0}" if phys else "%[kka]"
     for i in range((2 * JC + 3) // 4):
-        add(f"ds_read_b128 v[{KK + 4*i}:{KK + 4*i + 3}], %[kka] offset:{i * KK_GSTRIDE}")
-    if DK:
+        add(f"ds_read_b128 v[{KK + 4*i}:{KK + 4*i + 3}], {kka} offset:{i * KK_GSTRIDE}")
+    if DK and not phys:
         for j in range(2 * JC):
             add(f"v_mov_b32 v{DK_ + j}, %[dk{j}]")
     tmap(QR, TQ[0])
@@ -218,13 +228,19 @@ def variant(dtype, M, DQ=True, DK=True):
         add(f"ds_read_b128 v[{G + 4*(p % ring)}:{G + 4*(p % ring) + 3}], v{RDA} offset:{pos_addr(p)}")
 
     add("RL_%=:")
-    # Priority: the two waves sharing a SIMD take turns at the higher issue
-    # priority, 8 rows each, so that neither runs ahead and finishes alone.
+    # Priority: the waves sharing a SIMD (two, or three with top < 256; wpar =
+    # the wave's place among them) take turns at the higher issue priority, 8
+    # rows each, so that none runs ahead and finishes alone.
     add(f"s_sub_u32 s{SPC}, s{SPC}, 1")
     add(f"s_cmp_lt_i32 s{SPC}, 0")
     add("s_cbranch_scc0 PR_%=_d")
     add(f"s_mov_b32 s{SPC}, {8 // UNROLL - 1}")
-    add(f"s_xor_b32 s{SPR}, s{SPR}, 1")
+    if phys:
+        add(f"s_add_u32 s{SPR}, s{SPR}, 1")
+        add(f"s_cmp_ge_u32 s{SPR}, 3")
+        add(f"s_cselect_b32 s{SPR}, 0, s{SPR}")
+    else:
+        add(f"s_xor_b32 s{SPR}, s{SPR}, 1")
     add(f"s_cmp_eq_u32 s{SPR}, 0")
     add("s_cbranch_scc1 PR_%=_lo")
     add("s_setprio 2")
@@ -296,21 +312,39 @@ def variant(dtype, M, DQ=True, DK=True):
     add("RX_%=:")
     add("s_setprio 0")
     add("s_waitcnt vmcnt(0) lgkmcnt(0)")
-    if DK:
+    if DK and not phys:
         for j in range(2 * JC):
             add(f"v_mov_b32 %[dk{j}], v{DK_ + j}")
 
     # ---- C++ wrapper -----------------------------------------------------------
-    name = f"bwd2_rows_{dtype}_m{M}_{'q' if DQ else ''}{'k' if DK else ''}"
+    name = f"bwd2_rows_{dtype}_m{M}_{'q' if DQ else ''}{'k' if DK else ''}" + ("" if top == 256 else f"_v{top}")
     asm = "\n".join("      \"" + s + "\\n\"" for s in L)
-    outs = ", ".join([f"[dk{j}] \"+v\"(dk[{j}])" for j in range(2 * JC)]) if DK else ""
-    ins = ", ".join([
-        "[q3] \"s\"(q3)", "[ql] \"s\"(qlast)", "[dq] \"s\"(dq)", "[qs] \"s\"(qstride)", "[rows] \"s\"(rows)",
-        "[wpar] \"s\"(wpar)", "[rda] \"v\"(rda)", "[vq4] \"v\"(vq4)", "[vqs] \"v\"(vqs)", "[kka] \"v\"(kka)",
-        "[paddr] \"v\"(paddr)"] + [f"[shf{c}] \"v\"(shf[{c}])" for c in range(4)] +
-        [f"[q0_{k}] \"v\"(q0[{k}])" for k in range(UNROLL)])
-    clob = ", ".join([f"\"v{v}\"" for v in range(lo, 256)] +
+    sins = ["[q3] \"s\"(q3)", "[ql] \"s\"(qlast)", "[dq] \"s\"(dq)", "[qs] \"s\"(qstride)", "[rows] \"s\"(rows)",
+            "[wpar] \"s\"(wpar)"]
+    bound = set()
+    if phys:
+        # Operands in the block's registers: the accumulators, and the inputs the
+        # block consumes in place (declared read-write: their values change).
+        outl = [f"[dk{j}] \"+{{v{DK_ + j}}}\"(dk[{j}])" for j in range(2 * JC)] if DK else []
+        bound.update(range(DK_, DK_ + 2 * JC) if DK else [])
+        pairs = [("rda", RDA), ("vq4", VQ4), ("vqs", VQS), ("kka", T0), ("paddr", PADDR)] + \
+                [(f"shf[{c}]", SHF + c) for c in range(4)] + [(f"q0[{k}]", QR + k) for k in range(UNROLL)]
+        for var, reg in pairs:
+            outl.append(f"[i_{reg}] \"+{{v{reg}}}\"({var})")
+            bound.add(reg)
+        outs = ", ".join(outl)
+        ins = ", ".join(sins)
+    else:
+        outs = ", ".join([f"[dk{j}] \"+v\"(dk[{j}])" for j in range(2 * JC)]) if DK else ""
+        ins = ", ".join(sins + [
+            "[rda] \"v\"(rda)", "[vq4] \"v\"(vq4)", "[vqs] \"v\"(vqs)", "[kka] \"v\"(kka)",
+            "[paddr] \"v\"(paddr)"] + [f"[shf{c}] \"v\"(shf[{c}])" for c in range(4)] +
+            [f"[q0_{k}] \"v\"(q0[{k}])" for k in range(UNROLL)])
+    clob = ", ".join([f"\"v{v}\"" for v in range(lo, top) if v not in bound] +
                      [f"\"s{s}\"" for s in range(S, SREG_HI + 1)] + ["\"vcc\"", "\"memory\""])
+    # The block writes the bound inputs: it gets copies of the arrays.
+    copies = ("\n  unsigned shf[4] = {shf_[0], shf_[1], shf_[2], shf_[3]};\n  unsigned q0[" + str(UNROLL) + "] = {" +
+              ", ".join(f"q0_[{k}]" for k in range(UNROLL)) + "};") if phys else ""
     src = f"""
 // Row loop of one wave of the column-split backward, {dtype}, M = {M}, grad_query {DQ}, grad_key {DK}
 // (JC = {JC} columns per lane half, LDS row pitch {PITCH} floats, {nmine} private VGPRs).
@@ -322,7 +356,7 @@ def variant(dtype, M, DQ=True, DK=True):
 // paddr: 4 * (the partner lane).
 __device__ __forceinline__ void {name}(float (&dk)[{2*JC}], const void* q3, const void* qlast, void* dq,
     unsigned qstride, int rows, unsigned wpar, unsigned rda, unsigned vq4, unsigned vqs, unsigned kka,
-    unsigned paddr, const unsigned (&shf)[4], const unsigned (&q0)[{UNROLL}]) {{
+    unsigned paddr, {"const unsigned (&shf_)[4], const unsigned (&q0_)[" + str(UNROLL) + "]" if phys else "const unsigned (&shf)[4], const unsigned (&q0)[" + str(UNROLL) + "]"}) {{{copies}
   asm volatile(
 {asm}
       : {outs}
@@ -452,8 +486,11 @@ FWD3_RS = (3,)
 FWD_RS_V128 = (1, 2, 3)
 
 
-VARIANTS = [(dt, M, dq, dk) for dt in ("f16", "bf16") for M in (49, 32, 16)
+VARIANTS = [(dt, M, dq, dk) for dt in ("f16", "bf16") for M in (32, 16)
             for (dq, dk) in ((True, True), (True, False), (False, True))]
+# M = 49 runs in 12-wave workgroups (three waves per SIMD, 168 VGPRs).
+VARIANTS_V168 = [(dt, 49, dq, dk) for dt in ("f16", "bf16")
+                 for (dq, dk) in ((True, True), (True, False), (False, True))]
 
 
 def main(out_path):
@@ -461,6 +498,10 @@ def main(out_path):
              "// Do not edit by hand: edit the generator and rebuild.", "#pragma once", "namespace lfamd {"]
     for dt, M, dq, dk in VARIANTS:
         name, src, info = variant(dt, M, dq, dk)
+        parts.append(f"// {name}: {info}")
+        parts.append(src)
+    for dt, M, dq, dk in VARIANTS_V168:
+        name, src, info = variant(dt, M, dq, dk, top=168)
         parts.append(f"// {name}: {info}")
         parts.append(src)
     for R in FWD_RS:

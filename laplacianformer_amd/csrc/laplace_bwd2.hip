@@ -17,9 +17,12 @@
 // (A NaN pattern orders beyond the infinities, so its sign is +-1 where the
 // reference's sign of a NaN difference is 0.)
 //
-// Mapping. A workgroup is 8 waves (2 per SIMD: the register file holds two of
-// these waves, and the SIMD issues two VALU instructions per 4 cycles only from
-// an even number of waves), one per CU, and takes a contiguous range of at most
+// Mapping. A workgroup is WAVES waves, one workgroup per CU: 12 (3 per SIMD,
+// 168 VGPRs each) for M = 49, whose row loop keeps its grad_key sums and the
+// inputs it consumes in its own registers, else 8 (2 per SIMD, 256 VGPRs). A
+// SIMD issues two VALU instructions per 4 cycles only from two different
+// waves: the row loop reaches ~2.8 cycles per instruction with two waves and
+// about 10 % less with three. The workgroup takes a contiguous range of at most
 // 512 rows of one (b, h) slice and one channel block of 64 channels. Lane
 // (h, p), h = lane / 32, p = lane % 32, owns channels 2p + h and 2p + 1 - h (in
 // that order) and the key columns of parity h (column 2j + h, j < JC =
@@ -53,27 +56,47 @@ namespace lfamd {
 
 namespace {
 
-constexpr int kB2Waves = 8;     // waves per workgroup (2 per SIMD)
 constexpr int kB2Unroll = 4;    // rows per iteration of the asm row loop (its query prefetch depth)
 constexpr int kB2MaxRows = 512;  // most grad rows of one workgroup (staged in LDS at once)
 constexpr int kB2SoloRows = 64;  // slices up to this many rows take one workgroup each
-constexpr int kB2Threads = 64 * kB2Waves;
+
+// Waves per workgroup for key count M (12 needs the 168-VGPR row loops).
+__host__ __device__ constexpr int b2_waves(int M) { return M == 49 ? 12 : 8; }
+
+// Rows of a workgroup's range before wave w (w = WAVES: all n). With 12 waves
+// the youngest wave of each SIMD (waves 8-11: waves w, w + 4, w + 8 share SIMD
+// w % 4) gets 29 parts to the others' 35: it runs its rows at a lower issue
+// share (measured: with an even split it finishes ~25 % after the other two
+// and then runs alone at half rate).
+template <int WAVES>
+__device__ __forceinline__ int b2_wave_start(int w, int n) {
+  if constexpr (WAVES == 12) {
+    constexpr int kA = 35, kC = 29, kSum = 4 * (2 * kA + kC);
+    const int units = w <= 8 ? w * kA : 8 * kA + (w - 8) * kC;
+    return (int)((int64_t)units * n / kSum);
+  } else {
+    return (int)((int64_t)w * n / WAVES);
+  }
+}
+__host__ __device__ constexpr int b2_max_wave_rows(int waves) {
+  return waves == 12 ? (kB2MaxRows * 35 + 4 * 99 - 1) / (4 * 99) + 1 : (kB2MaxRows + waves - 1) / waves;
+}
 
 // Layout constants shared by the kernel and the host plan.
 struct B2Shape {
-  int M, JC, HP, PITCH, NKK;
-  __host__ __device__ constexpr B2Shape(int m)
-      : M(m), JC((m + 1) / 2), HP((((m + 1) / 2) + 1 + 3) / 4 * 4), PITCH(2 * ((((m + 1) / 2) + 1 + 3) / 4 * 4) + 4),
-        NKK((2 * ((m + 1) / 2) + 3) / 4) {}
-  // LDS: the waves' column sums of 2g [kB2Waves][M] | key-term table
-  // [NKK][65][4] (lane-major 16-byte groups, one spare group per table row so
-  // that the scatter into it spreads over the banks) | staged rows
-  // [kB2MaxRows + 1][PITCH]. After the row loops the waves' grad_key sums
-  // ([kB2Waves][M][65], channel fastest, padded) overwrite the table and rows.
-  __host__ __device__ constexpr int colsum_bytes() const { return (kB2Waves * M * 4 + 15) / 16 * 16; }
+  int M, W, JC, HP, PITCH, NKK;
+  __host__ __device__ constexpr B2Shape(int m, int w)
+      : M(m), W(w), JC((m + 1) / 2), HP((((m + 1) / 2) + 1 + 3) / 4 * 4),
+        PITCH(2 * ((((m + 1) / 2) + 1 + 3) / 4 * 4) + 4), NKK((2 * ((m + 1) / 2) + 3) / 4) {}
+  // LDS: the waves' column sums of 2g [W][M] | key-term table [NKK][65][4]
+  // (lane-major 16-byte groups, one spare group per table row so that the
+  // scatter into it spreads over the banks) | staged rows [kB2MaxRows + 1][PITCH].
+  // After the row loops the waves' grad_key sums ([W][M][65], channel fastest,
+  // padded) overwrite the table and rows.
+  __host__ __device__ constexpr int colsum_bytes() const { return (W * M * 4 + 15) / 16 * 16; }
   __host__ __device__ constexpr int kk_off() const { return colsum_bytes(); }
   __host__ __device__ constexpr int rows_off() const { return kk_off() + NKK * 65 * 16; }
-  __host__ __device__ constexpr int red_bytes() const { return kB2Waves * M * 65 * 4; }
+  __host__ __device__ constexpr int red_bytes() const { return W * M * 65 * 4; }
   __host__ __device__ constexpr int lds_bytes() const {
     return rows_off() + (kB2MaxRows + 1) * PITCH * 4 > colsum_bytes() + red_bytes()
                ? rows_off() + (kB2MaxRows + 1) * PITCH * 4
@@ -88,10 +111,11 @@ template <> __device__ __forceinline__ float g2f<bf16s>(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
-// Dispatch to the generated row loops (grad_query and grad_key together or alone).
-template <typename T, int M, bool DQ, bool DK> struct B2Rows;
-#define LFAMD_B2ROWS(TY, MM, DQ_, DK_, FN)                                                               \
-  template <> struct B2Rows<TY, MM, DQ_, DK_> {                                                           \
+// Dispatch to the generated row loops (grad_query and grad_key together or
+// alone; the _v168 forms for 12-wave workgroups).
+template <typename T, int M, bool DQ, bool DK, int WAVES> struct B2Rows;
+#define LFAMD_B2ROWS(TY, MM, DQ_, DK_, WW, FN)                                                           \
+  template <> struct B2Rows<TY, MM, DQ_, DK_, WW> {                                                       \
     __device__ static void run(float (&dk)[2 * ((MM + 1) / 2)], const void* q3, const void* ql, void* dq,  \
                                unsigned qs, int rows, unsigned wpar, unsigned rda, unsigned vq4,           \
                                unsigned vqs, unsigned kka, unsigned paddr, const unsigned (&shf)[4],       \
@@ -99,32 +123,37 @@ template <typename T, int M, bool DQ, bool DK> struct B2Rows;
       FN(dk, q3, ql, dq, qs, rows, wpar, rda, vq4, vqs, kka, paddr, shf, q0);                             \
     }                                                                                                     \
   };
-#define LFAMD_B2ALL(TY, TN, MM)                                    \
-  LFAMD_B2ROWS(TY, MM, true, true, bwd2_rows_##TN##_m##MM##_qk)     \
-  LFAMD_B2ROWS(TY, MM, true, false, bwd2_rows_##TN##_m##MM##_q)     \
-  LFAMD_B2ROWS(TY, MM, false, true, bwd2_rows_##TN##_m##MM##_k)
-LFAMD_B2ALL(f16s, f16, 49)
-LFAMD_B2ALL(bf16s, bf16, 49)
+#define LFAMD_B2ALL(TY, TN, MM)                                        \
+  LFAMD_B2ROWS(TY, MM, true, true, 8, bwd2_rows_##TN##_m##MM##_qk)      \
+  LFAMD_B2ROWS(TY, MM, true, false, 8, bwd2_rows_##TN##_m##MM##_q)      \
+  LFAMD_B2ROWS(TY, MM, false, true, 8, bwd2_rows_##TN##_m##MM##_k)
+#define LFAMD_B2ALL12(TY, TN, MM)                                       \
+  LFAMD_B2ROWS(TY, MM, true, true, 12, bwd2_rows_##TN##_m##MM##_qk_v168) \
+  LFAMD_B2ROWS(TY, MM, true, false, 12, bwd2_rows_##TN##_m##MM##_q_v168) \
+  LFAMD_B2ROWS(TY, MM, false, true, 12, bwd2_rows_##TN##_m##MM##_k_v168)
+LFAMD_B2ALL12(f16s, f16, 49)
+LFAMD_B2ALL12(bf16s, bf16, 49)
 LFAMD_B2ALL(f16s, f16, 32)
 LFAMD_B2ALL(bf16s, bf16, 32)
 LFAMD_B2ALL(f16s, f16, 16)
 LFAMD_B2ALL(bf16s, bf16, 16)
+#undef LFAMD_B2ALL12
 #undef LFAMD_B2ALL
 #undef LFAMD_B2ROWS
 
 // Loads `count` >= 1 16-bit elements from `src` as 4-byte words: word b of the
-// workgroup in thread b % kB2Threads, slot b / kB2Threads. The first word may
+// workgroup in thread b % THREADS, slot b / THREADS. The first word may
 // start one element before `src` and the last end one after the span (never
 // outside the 4-byte-aligned words holding the span's own bytes); slots past
 // the last word load it again. Returns the number of elements before `src` in
 // word 0 (0 or 1).
-template <int MAXW>
+template <int THREADS, int MAXW>
 __device__ __forceinline__ int load_words(const uint16_t* src, int count, int tid, uint32_t (&wd)[MAXW]) {
   const int skew = (int)(reinterpret_cast<uintptr_t>(src) & 3) >> 1;
   const uint32_t* base = reinterpret_cast<const uint32_t*>(src - skew);
   const int last = ((count + skew + 1) >> 1) - 1;
 #pragma unroll
-  for (int i = 0; i < MAXW; ++i) wd[i] = base[min(tid + i * kB2Threads, last)];
+  for (int i = 0; i < MAXW; ++i) wd[i] = base[min(tid + i * THREADS, last)];
   return skew;
 }
 
@@ -142,9 +171,9 @@ __device__ __forceinline__ int select_lanes(bool c, int a, int b) {
 // valid = e in [0, count) (f is to route an invalid element to a dummy
 // location). (row, col) advance incrementally from word to word; there are no
 // branches. In each call of a wave the lanes hold elements two apart.
-template <int M, int MAXW, typename F>
+template <int M, int THREADS, int MAXW, typename F>
 __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int skew, int count, int tid, F f) {
-  constexpr int kStep = 2 * kB2Threads, kDR = kStep / M, kDC = kStep % M;
+  constexpr int kStep = 2 * THREADS, kDR = kStep / M, kDC = kStep % M;
   int e = 2 * tid - skew;            // >= -1
   int row = (e + M) / M - 1;         // -1 for e = -1
   int col = e - row * M;
@@ -164,17 +193,18 @@ __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int sk
 
 // Grid: (nx workgroups per slice, channel blocks, B*H). Workgroup x takes rows
 // [x*N/nx, (x+1)*N/nx) of its slice, at most kB2MaxRows of them (the host
-// plan sizes nx for that), split evenly over the 8 waves.
+// plan sizes nx for that), split evenly over the WAVES = b2_waves(M) waves.
 //
 // GK: the gradient is that of the fused Laplacian kernel K = exp(-s * distance)
 // (fp32 gk = dL/dK and kv = K instead of gout): the staged 2g is
 // (-2s * gk) * kv, i.e. 2 * fl(fl(-s * gk) * kv) exactly.
 template <typename T, int M, bool DQ, bool DK, bool GK = false>
-__global__ void __launch_bounds__(kB2Threads, 1)
+__global__ void __launch_bounds__(64 * b2_waves(M), 1)
 laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, const float* __restrict__ kv,
                     float gscale, const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ dq,
                     float* __restrict__ partial, T* __restrict__ dkOut, int N, int C) {
-  constexpr B2Shape S{M};
+  constexpr int WAVES = b2_waves(M), THREADS = 64 * WAVES;
+  constexpr B2Shape S{M, WAVES};
   constexpr int JC = S.JC, HP = S.HP, PITCH = S.PITCH, NKK = S.NKK;
   static_assert(M >= 2, "M >= 2");
   const int tid = threadIdx.x;
@@ -185,7 +215,7 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
 
   extern __shared__ __align__(16) unsigned char smem[];
   const unsigned ldsBase = (unsigned)(uintptr_t)smem;
-  float* colsum = reinterpret_cast<float*>(smem);                     // [kB2Waves][M]: column sums of 2g
+  float* colsum = reinterpret_cast<float*>(smem);                     // [WAVES][M]: column sums of 2g
   float* kkt = reinterpret_cast<float*>(smem + S.kk_off());           // [NKK][65][4]
   float* rowsA = reinterpret_cast<float*>(smem + S.rows_off());       // [rows + 1][PITCH]
   const unsigned rowsBase = ldsBase + S.rows_off();
@@ -197,14 +227,15 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   // All loads first: the key block [64][M] of the channel block (the whole
   // workgroup), this wave's own grad rows (lane = column: RPI rows of M
   // columns per load) and the first query pairs of its row loop.
-  constexpr int kKeyW = (64 * M + 2 + 2 * kB2Threads - 1) / (2 * kB2Threads);
+  constexpr int kKeyW = (64 * M + 2 + 2 * THREADS - 1) / (2 * THREADS);
   uint32_t kwd[kKeyW];
-  const int kskew = load_words(reinterpret_cast<const uint16_t*>(key) + ((size_t)bh * C + cb * 64) * M, 64 * M, tid, kwd);
-  const int w0 = uniform((int)((int64_t)wave * n / kB2Waves)), w1 = uniform((int)((int64_t)(wave + 1) * n / kB2Waves));
-  const int rows = w1 - w0;  // at most kB2MaxRows / kB2Waves = 64
+  const int kskew = load_words<THREADS>(reinterpret_cast<const uint16_t*>(key) + ((size_t)bh * C + cb * 64) * M, 64 * M, tid, kwd);
+  const int w0 = uniform(b2_wave_start<WAVES>(wave, n)), w1 = uniform(b2_wave_start<WAVES>(wave + 1, n));
+  const int rows = w1 - w0;  // at most b2_max_wave_rows(WAVES)
   const int h = lane >> 5, p = lane & 31;
   constexpr int RPI = 64 / M;                                         // rows per load instruction
-  constexpr int kOwnLoads = (kB2MaxRows / kB2Waves + RPI - 1) / RPI;
+  constexpr int kOwnLoads = (b2_max_wave_rows(WAVES) + RPI - 1) / RPI;
+  constexpr int kGkSplit = (2 * kOwnLoads + 2) / 3;
   const int lrow = lane / M, lcol = lane - lrow * M;
   uint16_t gv[GK ? 1 : kOwnLoads];
   float ga[GK ? kOwnLoads : 1], ka[GK ? kOwnLoads : 1];
@@ -215,20 +246,20 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
     const size_t e0 = ((size_t)bh * N + P0 + w0) * M + lcol;
     const int rlast = max(rows, 1) - 1;
     if constexpr (GK) {
-      // Two fp32 loads per element: the first half of the rows is combined
-      // into 2g before the second half is loaded (the register file holds
-      // one half's pairs at a time).
+      // Two fp32 loads per element: the first two thirds of the rows are
+      // combined into 2g before the rest is loaded (so that the register file
+      // never holds more than about two thirds of the rows' pairs).
 #pragma unroll
-      for (int i = 0; i < kOwnLoads / 2; ++i) {
+      for (int i = 0; i < kGkSplit; ++i) {
         const size_t e = e0 + (size_t)min(i * RPI + lrow, rlast) * M;
         ga[i] = gk[e];
         ka[i] = kv[e];
       }
 #pragma unroll
-      for (int i = 0; i < kOwnLoads / 2; ++i) ga[i] = (-2.0f * gscale * ga[i]) * ka[i];
+      for (int i = 0; i < kGkSplit; ++i) ga[i] = (-2.0f * gscale * ga[i]) * ka[i];
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = kOwnLoads / 2; i < kOwnLoads; ++i) {
+      for (int i = kGkSplit; i < kOwnLoads; ++i) {
         const size_t e = e0 + (size_t)min(i * RPI + lrow, rlast) * M;
         ga[i] = gk[e];
         ka[i] = kv[e];
@@ -250,7 +281,7 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   // (channel 2p + (c ^ h): the lane's own channel first, column 2j + h) at
   // kkt[((e / 4) * 65 + lane) * 4 + e % 4], e = c*JC + j; entries without a
   // key column are zero. (Invalid elements go to the spare entry [0][64][0].)
-  scatter_words<M>(kwd, kskew, 64 * M, tid, [&](int ch, int col, bool valid, uint16_t bits) {
+  scatter_words<M, THREADS>(kwd, kskew, 64 * M, tid, [&](int ch, int col, bool valid, uint16_t bits) {
     const int hc = col & 1;
     const int l = (ch >> 1) + 32 * hc, e = ((ch & 1) ^ hc) * JC + (col >> 1);
     const int a = ((e >> 2) * 65 + l) * 4 + (e & 3);
@@ -280,7 +311,7 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
       if (i * RPI < rows) {  // wave-uniform; lanes past the last row rewrite it with its own value
         float v2;
         if constexpr (GK) {
-          v2 = i < kOwnLoads / 2 ? ga[i] : (-2.0f * gscale * ga[i]) * ka[i];
+          v2 = i < kGkSplit ? ga[i] : (-2.0f * gscale * ga[i]) * ka[i];
         } else {
           const float v = g2f<T>(gv[i]);
           v2 = v + v;
@@ -330,9 +361,11 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
     uint16_t* dqrow = uniform_ptr(reinterpret_cast<uint16_t*>(dq) + ((size_t)bh * N + P0 + w0) * C + cb * 64);
     // Bit offsets of the lane's channels in a query pair (own channel 2p + h first).
     const unsigned shf[4] = {16u * h, 16u * h + 15u, 16u - 16u * h, 31u - 16u * h};
-    B2Rows<T, M, DQ, DK>::run(dk, q3, ql, dqrow, (unsigned)C * 2, rows, (unsigned)uniform(wave >= 4 ? 1 : 0), rda,
-                              (unsigned)p * 4, (unsigned)(2 * p + h) * 2, ldsBase + S.kk_off() + (unsigned)lane * 16,
-                              (unsigned)(lane ^ 32) * 4, shf, q0);
+    // wpar: the wave's place among the waves of its SIMD (wave w runs on SIMD w % 4).
+    B2Rows<T, M, DQ, DK, WAVES>::run(dk, q3, ql, dqrow, (unsigned)C * 2, rows, (unsigned)uniform(wave >> 2), rda,
+                                     (unsigned)p * 4, (unsigned)(2 * p + h) * 2,
+                                     ldsBase + S.kk_off() + (unsigned)lane * 16, (unsigned)(lane ^ 32) * 4, shf,
+                                     q0);
   }
   if constexpr (!DK) return;
 
@@ -340,7 +373,7 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   // accumulated 2g y; summed over the waves in wave order and written
   // channel-major. (A wave's column sums were written by its own lanes.)
   __syncthreads();
-  float* red = reinterpret_cast<float*>(smem + S.colsum_bytes());   // [kB2Waves][M][65]
+  float* red = reinterpret_cast<float*>(smem + S.colsum_bytes());   // [WAVES][M][65]
   {
     float* buf = red + wave * M * 65;
 #pragma unroll
@@ -356,11 +389,11 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   __syncthreads();
   // [64][M] channel-major: the workgroup's partial, or with one workgroup per
   // slice (dkOut) grad_key itself, rounded once.
-  for (int t = tid; t < 64 * M; t += kB2Threads) {
+  for (int t = tid; t < 64 * M; t += THREADS) {
     const int c = t / M, col = t - c * M;
     float s2 = red[col * 65 + c];
 #pragma unroll
-    for (int w = 1; w < kB2Waves; ++w) s2 += red[w * M * 65 + col * 65 + c];
+    for (int w = 1; w < WAVES; ++w) s2 += red[w * M * 65 + col * 65 + c];
     if (dkOut)
       dkOut[((size_t)bh * C + cb * 64) * M + t] = from_acc<T>(s2);
     else
@@ -411,8 +444,8 @@ B2Plan plan_b2(int64_t BH, int64_t N, int64_t M, int64_t C) {
              ? 1
              : (int)std::max<int64_t>((N + kB2MaxRows - 1) / kB2MaxRows,
                                       std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
-                                                                             (N + kB2Waves - 1) / kB2Waves)));
-  p.lds = (size_t)B2Shape((int)M).lds_bytes();
+                                                                             (N + 7) / 8)));
+  p.lds = (size_t)B2Shape((int)M, b2_waves((int)M)).lds_bytes();
   p.partialElems = p.nx == 1 ? 0 : (size_t)slices * p.nx * 64 * (size_t)M;
   return p;
 }
@@ -423,11 +456,11 @@ int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk,
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
   T* dkOut = DK && p.nx == 1 ? static_cast<T*>(dk) : nullptr;
   if (kg.gk)
-    hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(kB2Threads), p.lds, st,
+    hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
                        static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
   else
-    hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, false>), grid, dim3(kB2Threads), p.lds, st,
+    hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, false>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
                        static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
   int s = check_launch("laplace backward (column-split)");
