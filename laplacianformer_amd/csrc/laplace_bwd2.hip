@@ -372,17 +372,25 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   // Workgroup grad_key partial: per wave, half its column sums of 2g minus its
   // accumulated 2g y; summed over the waves in wave order and written
   // channel-major. (A wave's column sums were written by its own lanes.)
+  // Channel c sits at slot (c >> 1) + 32 (c & 1) of its column's 65: the
+  // lanes of each half-wave write 32 consecutive slots (the own and the
+  // partner channel of lane (h, p) are both at slot p of a half), and the
+  // final sum reads consecutive columns at stride 65, without bank conflicts.
   __syncthreads();
   float* red = reinterpret_cast<float*>(smem + S.colsum_bytes());   // [WAVES][M][65]
   {
+    // All column sums first: the stores below may alias them as far as the
+    // compiler knows, and would otherwise wait for one read each.
+    float cs[JC];
+#pragma unroll
+    for (int j = 0; j < JC; ++j) cs[j] = colsum[wave * M + min(2 * j + h, M - 1)];
     float* buf = red + wave * M * 65;
 #pragma unroll
     for (int j = 0; j < JC; ++j) {
       const int col = 2 * j + h;
       if (col < M) {
-        const float cs = 0.5f * colsum[wave * M + col];
-        buf[col * 65 + 2 * p + h] = cs - dk[j];            // own channel
-        buf[col * 65 + 2 * p + 1 - h] = cs - dk[JC + j];   // partner's channel
+        buf[col * 65 + p + 32 * h] = 0.5f * cs[j] - dk[j];            // own channel 2p + h
+        buf[col * 65 + p + 32 - 32 * h] = 0.5f * cs[j] - dk[JC + j];  // partner's channel 2p + 1 - h
       }
     }
   }
@@ -391,9 +399,10 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   // slice (dkOut) grad_key itself, rounded once.
   for (int t = tid; t < 64 * M; t += THREADS) {
     const int c = t / M, col = t - c * M;
-    float s2 = red[col * 65 + c];
+    const int slot = col * 65 + (c >> 1) + 32 * (c & 1);
+    float s2 = red[slot];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) s2 += red[w * M * 65 + col * 65 + c];
+    for (int w = 1; w < WAVES; ++w) s2 += red[w * M * 65 + slot];
     if (dkOut)
       dkOut[((size_t)bh * C + cb * 64) * M + t] = from_acc<T>(s2);
     else
