@@ -64,22 +64,30 @@ constexpr int kB2SoloRows = 64;  // slices up to this many rows take one workgro
 __host__ __device__ constexpr int b2_waves(int M) { return M == 49 ? 12 : 8; }
 
 // Rows of a workgroup's range before wave w (w = WAVES: all n). With 12 waves
-// the youngest wave of each SIMD (waves 8-11: waves w, w + 4, w + 8 share SIMD
-// w % 4) gets 29 parts to the others' 35: it runs its rows at a lower issue
-// share (measured: with an even split it finishes ~25 % after the other two
-// and then runs alone at half rate).
+// (waves w, w + 4, w + 8 share SIMD w % 4) the three places of a SIMD get
+// kB2P0, kB2P1, kB2P2 parts of its rows: with an even split the youngest wave
+// of each SIMD finished ~25 % after the others and then ran alone at half
+// rate. (Per place, the middle wave runs its rows ~10 % faster than the oldest,
+// but giving it more rows, 34 / 37 / 28, changed the kernel by < 0.2 %.)
+constexpr int kB2P0 = 35, kB2P1 = 35, kB2P2 = 29, kB2PSum = 4 * (kB2P0 + kB2P1 + kB2P2);
 template <int WAVES>
 __device__ __forceinline__ int b2_wave_start(int w, int n) {
   if constexpr (WAVES == 12) {
-    constexpr int kA = 35, kC = 29, kSum = 4 * (2 * kA + kC);
-    const int units = w <= 8 ? w * kA : 8 * kA + (w - 8) * kC;
-    return (int)((int64_t)units * n / kSum);
+    const int pl = w >> 2, k = w & 3;  // w = 12: pl = 3, k = 0
+    int units = k * (pl == 0 ? kB2P0 : pl == 1 ? kB2P1 : kB2P2);
+    if (pl > 0) units += 4 * kB2P0;
+    if (pl > 1) units += 4 * kB2P1;
+    if (pl > 2) units += 4 * kB2P2;
+    return (int)((int64_t)units * n / kB2PSum);
   } else {
     return (int)((int64_t)w * n / WAVES);
   }
 }
 __host__ __device__ constexpr int b2_max_wave_rows(int waves) {
-  return waves == 12 ? (kB2MaxRows * 35 + 4 * 99 - 1) / (4 * 99) + 1 : (kB2MaxRows + waves - 1) / waves;
+  // floor(u1 n / S) - floor(u0 n / S) <= ceil((u1 - u0) n / S)
+  return waves == 12 ? (kB2MaxRows * (kB2P0 > kB2P1 ? (kB2P0 > kB2P2 ? kB2P0 : kB2P2) : (kB2P1 > kB2P2 ? kB2P1 : kB2P2)) +
+                        kB2PSum - 1) / kB2PSum
+                     : (kB2MaxRows + waves - 1) / waves;
 }
 
 // Layout constants shared by the kernel and the host plan.
