@@ -563,8 +563,10 @@ int f3_launch(int dtype, const void* q, const void* k, void* o, int64_t BH, int6
 
 int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,
               float scale, hipStream_t st) {
-  // The plan's schedule search is cached per shape (per host thread; the CU
-  // count is per device, so the device is part of the key).
+  // The plan's schedule search (~80 us of host time for six row sets) is
+  // cached per shape, per host thread, for the last kPlanCache shapes (a layer
+  // step alternates three; the CU count is per device, so the device is part
+  // of the key).
   struct Key {
     int64_t BH, N, C;
     size_t ob;
@@ -573,16 +575,23 @@ int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, 
       return BH == o.BH && N == o.N && C == o.C && ob == o.ob && dev == o.dev && cus == o.cus;
     }
   };
-  static thread_local Key lastKey{-1, -1, -1, 0, -1, -1};
-  static thread_local F2Plan lastPlan{};
+  constexpr int kPlanCache = 8;
+  static thread_local Key keys[kPlanCache] = {};
+  static thread_local F2Plan plans[kPlanCache];
+  static thread_local int used = 0, next = 0;
   int dev = 0;
   (void)hipGetDevice(&dev);
   const Key key{BH, N, C, kernelEpi ? 4 : dtype_size(dtype), dev, num_cus()};
-  if (!(key == lastKey)) {
-    lastPlan = plan_f2(BH, N, C, key.ob);
-    lastKey = key;
+  int slot = -1;
+  for (int i = 0; i < used; ++i)
+    if (keys[i] == key) slot = i;
+  if (slot < 0) {
+    slot = used < kPlanCache ? used++ : next;
+    next = (slot + 1) % kPlanCache;
+    plans[slot] = plan_f2(BH, N, C, key.ob);
+    keys[slot] = key;
   }
-  const F2Plan& p = lastPlan;
+  const F2Plan& p = plans[slot];
   if (p.lds > (size_t)max_lds_bytes()) return fail(LFAMD_ERR_UNSUPPORTED, "laplace forward: LDS plan too large");
   if (kernelEpi) {
     if (dtype == LFAMD_F32) return launch_f2_t<float, kF2Exp>(q, k, o, BH, N, C, scale, p, st);
