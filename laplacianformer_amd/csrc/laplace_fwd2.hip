@@ -375,7 +375,22 @@ F2Plan plan_f2(int64_t BH, int64_t N, int64_t C, size_t outBytes) {
   if (!tail && part > 0) ++full;
   p.lds = f2_lds_bytes((int)C, rows, outBytes);
   p.sched.full = full;
-  if (f2_schedule16(full, tail, 3, p.sched)) {
+  // The schedule depends on (full, tail) only: searched once per pair and host thread.
+  struct Memo {
+    bool done, ok;
+    F2Sched s;
+  };
+  constexpr int kMemo = kF2MaxRows / 64 + 2;
+  static thread_local Memo memo[kMemo][2] = {};
+  Memo local{};
+  Memo& m = full < kMemo ? memo[full][tail ? 1 : 0] : local;
+  if (!m.done) {
+    m.s = p.sched;
+    m.ok = f2_schedule16(full, tail, 3, m.s);
+    m.done = true;
+  }
+  if (m.ok) {
+    for (int w = 0; w < 16; ++w) p.sched.w[w] = m.s.w[w];
     p.waves = 16;
     return p;
   }
