@@ -406,9 +406,8 @@ int launch_f2_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, in
                 const F2Plan& p, hipStream_t st) {
   using O = typename F2Out<T, EPI>::type;
   auto kern = laplace_fwd2_kernel<T, EPI, WAVES>;
-  if (p.lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds) != hipSuccess)
-    return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
+  if (p.lds > 65536)
+    if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
   hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<O*>(o), (int)N, (int)C, scale, p.sched);
   return check_launch("laplace forward (row-staged)");
@@ -533,9 +532,8 @@ template <typename T, int WAVES>
 int launch_f3_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
   auto kern = laplace_fwd3_kernel<T, WAVES>;
   const size_t lds = f3_lds_bytes((int)C);
-  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
+  if (lds > 65536)
+    if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), lds, "laplace forward")) return s;
   const int64_t nx = (N + kF3Rows - 1) / kF3Rows;
   hipLaunchKernelGGL(kern, dim3((unsigned)nx, (unsigned)BH), dim3(64 * WAVES), lds, st, static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<T*>(o), (int)N, (int)M, (int)C);

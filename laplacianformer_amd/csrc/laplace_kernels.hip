@@ -1461,10 +1461,8 @@ int launch_fwd_bcast_jb(const void* q, const void* k, void* o, const Dims& d, fl
   const int W = ceil_div(mg, JB);
   const size_t lds = fb_lds_bytes_g(dtype_of<T>(), d, sizeof(O), mg);
   auto kern = laplace_fwd_bcast_kernel<T, JB, kFbR, EPI>;
-  if (lds > 65536 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)lds) != hipSuccess)
-    return fail(LFAMD_ERR_HIP, "laplace forward: hipFuncSetAttribute failed");
+  if (lds > 65536)
+    if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), lds, "laplace forward")) return s;
   dim3 grid(ceil_div((int)d.N, 64 * kFbR) * ceil_div((int)d.M, mg), (unsigned)d.BH());
   hipLaunchKernelGGL(kern, grid, dim3(64 * W), lds, st, static_cast<const T*>(q), static_cast<const T*>(k),
                      static_cast<O*>(o), (int)d.N, mg, (int)d.M, (int)d.C, scale);
@@ -1675,10 +1673,8 @@ template <typename T, int CB, bool DQ, bool DK, int GSRC = kGradF16>
 int launch_mb_cb(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, const Dims& d,
                  const MbPlan& p, hipStream_t st, KernGrad kg = {}) {
   auto kern = laplace_bwd_mb_kernel<T, CB, DQ, DK, GSRC>;
-  if (p.lds > 65536 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)p.lds) != hipSuccess)
-    return fail(LFAMD_ERR_HIP, "laplace backward: hipFuncSetAttribute failed");
+  if (p.lds > 65536)
+    if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace backward")) return s;
   dim3 grid(p.nx, p.ncb, (unsigned)d.BH());
   hipLaunchKernelGGL(kern, grid, dim3(64 * p.W), p.lds, st, static_cast<const T*>(g), static_cast<const T*>(q),
                      static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), (int)d.N, (int)d.C,

@@ -24,6 +24,11 @@ int max_lds_bytes();
 // Compute units of the current device (cached per device; 256 if unknown).
 int num_cus();
 
+// Raises kernel `fn`'s dynamic LDS limit on the current device to at least
+// `bytes` (hipFuncSetAttribute once per kernel, device and size; later calls
+// with no larger size are a lookup). LFAMD_OK or LFAMD_ERR_HIP with `what`.
+int set_dyn_lds(const void* fn, size_t bytes, const char* what);
+
 // Column-split fused backward of 16-bit LaplaceSubtraction (laplace_bwd2.hip).
 // With B2Grad::gk set, the gradient is that of the fused kernel exp(-scale * distance):
 // fp32 gk = dL/dK and kv = K replace g (fp16 only).

@@ -51,6 +51,20 @@ int max_lds_bytes() {
   return v;
 }
 
+int set_dyn_lds(const void* fn, size_t bytes, const char* what) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> done;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lk(mu);
+  size_t& have = done[{fn, dev}];
+  if (have >= bytes) return LFAMD_OK;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
+    return fail(LFAMD_ERR_HIP, "%s: hipFuncSetAttribute failed", what);
+  have = bytes;
+  return LFAMD_OK;
+}
+
 int num_cus() {
   static std::mutex mu;
   static std::map<int, int> cache;

@@ -802,9 +802,7 @@ template <typename Kern>
 int set_lds(Kern k, size_t bytes) {
   if (bytes > (size_t)max_lds_bytes())
     return fail(LFAMD_ERR_UNSUPPORTED, "NewtonInverse needs %zu bytes of LDS, device allows %d", bytes, max_lds_bytes());
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
-    return fail(LFAMD_ERR_HIP, "hipFuncSetAttribute failed");
-  return LFAMD_OK;
+  return set_dyn_lds(reinterpret_cast<const void*>(k), bytes, "NewtonInverse");
 }
 
 // Waves per 16-row strip: the most (up to 4) that split the strip's tiles evenly
