@@ -106,6 +106,22 @@ def test_laplace_integer_ties(gpu, dt, M):
         assert_bitwise(got, ref, dt, "integer exact")
 
 
+def test_laplace_full_workgroups(gpu):
+    """fp16, M = 49, 512 rows per workgroup (B=32, N=4096: eight workgroups per slice): the
+    column-split backward's waves take their largest row counts (up to 46 rows for the two older
+    waves of a SIMD); every slice against the oracle."""
+    B, H, N, M, C = 32, 1, 4096, 49, 64
+    print("laplace 512-row workgroups", flush=True)
+    q = gen((B, H, N, C), 1101, "f16")
+    k = gen((B, H, M, C), 1102, "f16").transpose(-1, -2).contiguous()
+    g = gen((B, H, N, M), 1103, "f16")
+    out, dq, dk, dq2, dk2 = (t.cpu() for t in _run(gpu, q, k, g))
+    assert torch.equal(dq, dq2)
+    refs = l1_refs(q, k, g, "f16")
+    check_l1(out, dq, dk, refs, "f16", "separate ")
+    check_l1(out, dq2, dk2, refs, "f16", "fused ")
+
+
 def test_laplace_config2_full(gpu):
     """B=32 H=1 N=3136 M=49 d=64 fp16, fwd + bwd."""
     B, H, N, M, C = 32, 1, 3136, 49, 64

@@ -36,6 +36,7 @@ BWD_SHAPES = [
     (2, 1, 200, 32, 64),
     (1, 1, 97, 32, 130),
     (2, 1, 3136, 49, 64),
+    (32, 1, 4096, 49, 64),  # 512 rows per workgroup: the 12-wave kernel's largest wave row counts
     (1, 2, 150, 64, 64),
     (1, 1, 77, 81, 40),
     (2, 1, 130, 196, 64),
