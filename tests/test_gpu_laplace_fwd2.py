@@ -95,3 +95,25 @@ def test_fwd2_kernel_epilogue(gpu, shape):
     got = out.cpu().double().numpy()
     lim = ref * (2.0 ** -21) * (1.0 + s * d32) + 1e-38
     assert not (np.abs(got - ref) > lim).any(), what
+
+
+def test_fwd2_plan_cache_rotation(gpu):
+    """Host plan cache (eight shapes per thread): ten shapes with different plans, called in
+    turn three times (each call past the eighth evicts one), every result bit-identical to
+    the oracle, so a stale or mismatched plan cannot go unnoticed."""
+    import laplacianformer_amd as lf
+
+    L = lf.ext()
+    shapes = [(1, 4, n, 49, 64) for n in (1, 17, 64, 65, 130, 200, 272, 300, 392, 448)]
+    data = []
+    for i, (B, H, N, M, C) in enumerate(shapes):
+        q = gen((B, H, N, C), 900 + i, "f16")
+        k = gen((B, H, C, M), 950 + i, "f16")
+        data.append((q, k, q.to(gpu), k.to(gpu), oracle.laplace_forward(q, k, "f16")))
+    for rnd in range(3):
+        print(f"fwd2 plan cache round {rnd}", flush=True)
+        for (q, k, qd, kd, ref), shape in zip(data, shapes):
+            out = torch.empty(shape[:3] + (shape[3],), dtype=torch.float16, device=gpu)
+            L.LaplaceSubtraction_forward(qd, kd, out)
+            torch.cuda.synchronize()
+            assert_bitwise(out, ref, "f16", f"forward bits {shape} round {rnd}")
