@@ -145,6 +145,26 @@ int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const flo
                                   int64_t channels, float scale, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/* lfamd_laplace_kernel_backward for up to three row sources that share one key,
+ * in one launch: source i has q_lens[i] >= 1 rows per (b, h) slice with fp32
+ * grad_kernels[i] and kernels[i] [B,H,q_lens[i],M], fp16 queries[i]
+ * [B,H,q_lens[i],C] and grad_queries[i] (its grad_query); grad_key [B,H,C,M]
+ * is the sum over all sources (one rounding). Fused path only: LFAMD_F16,
+ * M = 49, C % 64 == 0, 4-byte aligned queries; LFAMD_ERR_UNSUPPORTED elsewhere
+ * (callers then make one call per source). The workspace is
+ * lfamd_laplace_kernel_backward_multi_workspace_size bytes (0 when the path does
+ * not apply). No reference counterpart: for callers with several kernel
+ * matrices against one landmark key (the LaplacianFormer layer's K_qm, K_km
+ * and K_mm), whose grad_key parts are summed anyway. */
+size_t lfamd_laplace_kernel_backward_multi_workspace_size(int num_sources, const int64_t* q_lens, int64_t batch,
+                                                          int64_t heads, int64_t k_len, int64_t channels);
+int lfamd_laplace_kernel_backward_multi(int dtype, int num_sources, const float* const* grad_kernels,
+                                        const float* const* kernels, const void* const* queries,
+                                        const int64_t* q_lens, const void* key, void* const* grad_queries,
+                                        void* grad_key, int64_t batch, int64_t heads, int64_t k_len,
+                                        int64_t channels, float scale, void* workspace, size_t workspace_bytes,
+                                        void* stream);
+
 /* ---- NewtonInverse ------------------------------------------------------ */
 
 /* Bytes of device workspace lfamd_newton_forward / lfamd_newton_backward need:
@@ -215,7 +235,8 @@ int lfamd_landmark_pool(int dtype, const void* k, void* km, void* km_cm, int64_t
 /* Backward of the pooling with the landmarks' gradient assembled from its parts: with every
  * operation rounded to `dtype`, t = (dcm0 + dcm1) + dcm2 ([B][H][d][M]), u = dkm + t^T
  * ([B][H][M][d]), and dk[b][h][n][c] += u[b][h][m(n)][c] / pool^2 in place ([B][H][gh*gw][d]).
- * No reference counterpart (the attention layer's). */
+ * dcm1 and dcm2 may be NULL (taken as zero: t = dcm0). No reference counterpart (the attention
+ * layer's). */
 int lfamd_landmark_pool_backward(int dtype, void* dk, const void* dkm, const void* dcm0, const void* dcm1,
                                  const void* dcm2, int64_t B, int64_t H, int gh, int gw, int pool, int d,
                                  void* stream);

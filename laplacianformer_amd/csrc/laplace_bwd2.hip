@@ -206,11 +206,25 @@ __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int sk
 // GK: the gradient is that of the fused Laplacian kernel K = exp(-s * distance)
 // (fp32 gk = dL/dK and kv = K instead of gout): the staged 2g is
 // (-2s * gk) * kv, i.e. 2 * fl(fl(-s * gk) * kv) exactly.
+// Up to three row sources sharing one key in one launch (fused-kernel gradient
+// only): the slice's workgroups are segments of nx[i] workgroups over source
+// i's N[i] rows (gk[i], kv[i], query q[i], grad_query dq[i]); every workgroup
+// writes a partial, so grad_key sums all sources' rows. count = 0: one source,
+// the plain arguments.
+struct B2Seg {
+  int count;
+  int nx[3], N[3];
+  const float* gk[3];
+  const float* kv[3];
+  const void* q[3];
+  void* dq[3];
+};
+
 template <typename T, int M, bool DQ, bool DK, bool GK = false>
 __global__ void __launch_bounds__(64 * b2_waves(M), 1)
-laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, const float* __restrict__ kv,
-                    float gscale, const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ dq,
-                    float* __restrict__ partial, T* __restrict__ dkOut, int N, int C) {
+laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gkIn, const float* __restrict__ kvIn,
+                    float gscale, const T* __restrict__ queryIn, const T* __restrict__ key, T* __restrict__ dqIn,
+                    float* __restrict__ partial, T* __restrict__ dkOut, int NIn, int C, B2Seg sg) {
   constexpr int WAVES = b2_waves(M), THREADS = 64 * WAVES;
   constexpr B2Shape S{M, WAVES};
   constexpr int JC = S.JC, HP = S.HP, PITCH = S.PITCH, NKK = S.NKK;
@@ -218,8 +232,36 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
   const int tid = threadIdx.x;
   const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
-  const int x = blockIdx.x, nx = gridDim.x, cb = blockIdx.y, bh = blockIdx.z;
-  const int ncb = gridDim.y;
+  const int nxg = gridDim.x, ncb = gridDim.y;
+  int xg = blockIdx.x, cb = blockIdx.y, bh = blockIdx.z;
+  // This workgroup's source and its place among that source's workgroups.
+  int x = xg, nx = nxg, N = NIn;
+  const float* gk = gkIn;
+  const float* kv = kvIn;
+  const T* query = queryIn;
+  T* dq = dqIn;
+  if (sg.count > 0) {
+    // Source-major order of the linear workgroup id (dispatch order): all of
+    // source 0's workgroups, then source 1's, then source 2's. (Slice-major
+    // order left a third round of big workgroups on half the CUs; callers put
+    // a small source first, whose workgroups end early and let the big ones in.)
+    const int S = ncb * (int)gridDim.z;
+    const int L = xg + nxg * (cb + ncb * bh);
+    const int e1 = S * sg.nx[0], e2 = e1 + S * sg.nx[1];
+    const int si = L < e1 ? 0 : (L < e2 ? 1 : 2);
+    nx = si == 0 ? sg.nx[0] : si == 1 ? sg.nx[1] : sg.nx[2];
+    const int Ls = L - (si == 0 ? 0 : si == 1 ? e1 : e2);
+    const int slice = Ls / nx;
+    x = Ls - slice * nx;
+    cb = slice % ncb;
+    bh = slice / ncb;
+    xg = x + (si == 0 ? 0 : si == 1 ? sg.nx[0] : sg.nx[0] + sg.nx[1]);  // the slice's partial slot
+    N = si == 0 ? sg.N[0] : si == 1 ? sg.N[1] : sg.N[2];
+    gk = si == 0 ? sg.gk[0] : si == 1 ? sg.gk[1] : sg.gk[2];
+    kv = si == 0 ? sg.kv[0] : si == 1 ? sg.kv[1] : sg.kv[2];
+    query = static_cast<const T*>(si == 0 ? sg.q[0] : si == 1 ? sg.q[1] : sg.q[2]);
+    dq = static_cast<T*>(si == 0 ? sg.dq[0] : si == 1 ? sg.dq[1] : sg.dq[2]);
+  }
 
   extern __shared__ __align__(16) unsigned char smem[];
   const unsigned ldsBase = (unsigned)(uintptr_t)smem;
@@ -414,7 +456,7 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, co
     if (dkOut)
       dkOut[((size_t)bh * C + cb * 64) * M + t] = from_acc<T>(s2);
     else
-      partial[(((size_t)bh * ncb + cb) * nx + x) * 64 * M + t] = s2;
+      partial[(((size_t)bh * ncb + cb) * nxg + xg) * 64 * M + t] = s2;
   }
 }
 
@@ -469,17 +511,19 @@ B2Plan plan_b2(int64_t BH, int64_t N, int64_t M, int64_t C) {
 
 template <typename T, int M, bool DQ, bool DK>
 int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, int64_t BH, int64_t N,
-                int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg) {
+                int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg, const B2Seg& sg = B2Seg{}) {
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
-  T* dkOut = DK && p.nx == 1 ? static_cast<T*>(dk) : nullptr;
+  T* dkOut = DK && p.nx == 1 && sg.count == 0 ? static_cast<T*>(dk) : nullptr;
   if (kg.gk)
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C,
+                       sg);
   else
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, false>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C,
+                       sg);
   int s = check_launch("laplace backward (column-split)");
   if (s || !DK || dkOut) return s;
   dim3 rgrid((64 * M + 255) / 256, p.ncb, (unsigned)BH);
@@ -531,6 +575,46 @@ int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, 
   if (dq && dk) return launch_b2<true, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
   if (dq) return launch_b2<true, false>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
   return launch_b2<false, true>(dtype, g, q, k, dq, dk, ws, BH, N, M, C, p, st, kg);
+}
+
+namespace {
+// Workgroups per source of a segmented launch and the partials they write.
+B2Plan plan_b2_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C, B2Seg& sg) {
+  B2Plan p{};
+  sg.count = nsrc;
+  for (int i = 0; i < nsrc; ++i) {
+    const B2Plan pi = plan_b2(BH, n[i], 49, C);
+    sg.nx[i] = pi.nx;
+    sg.N[i] = (int)n[i];
+    p.nx += pi.nx;
+    p.ncb = pi.ncb;
+    p.lds = pi.lds;
+  }
+  p.partialElems = (size_t)BH * p.ncb * p.nx * 64 * 49;
+  return p;
+}
+}  // namespace
+
+size_t b2_workspace_elems_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C) {
+  B2Seg sg{};
+  return plan_b2_multi(nsrc, n, BH, C, sg).partialElems;
+}
+
+int b2_launch_multi(int nsrc, const float* const* gk, const float* const* kv, const void* const* q, void* const* dq,
+                    const int64_t* n, const void* k, void* dk, void* ws, size_t wsBytes, int64_t BH, int64_t C, float scale,
+                    hipStream_t st, const char* who) {
+  B2Seg sg{};
+  const B2Plan p = plan_b2_multi(nsrc, n, BH, C, sg);
+  for (int i = 0; i < nsrc; ++i) {
+    sg.gk[i] = gk[i];
+    sg.kv[i] = kv[i];
+    sg.q[i] = q[i];
+    sg.dq[i] = dq[i];
+  }
+  if (!ws || wsBytes < p.partialElems * 4)
+    return fail(LFAMD_ERR_ARG, "%s: workspace of %zu bytes needed, %zu given", who, p.partialElems * 4, wsBytes);
+  return launch_b2_m<f16s, 49, true, true>(nullptr, nullptr, k, nullptr, dk, ws, BH, 0, C, p, st,
+                                           B2Grad{gk[0], kv[0], scale}, sg);
 }
 
 }  // namespace lfamd

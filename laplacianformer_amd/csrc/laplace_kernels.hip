@@ -1930,6 +1930,54 @@ int lfamd_laplace_kernel_forward(int dtype, const void* query, const void* key, 
   }
 }
 
+namespace {
+// The segmented fused-kernel backward applies: fp16, M = 49, C % 64 == 0,
+// 1 to 3 sources of at least one row, 4-byte aligned queries.
+int multi_bwd_check(int dtype, int nsrc, const int64_t* q_lens, const void* const* queries, const Dims& d,
+                    const char* who) {
+  if (nsrc < 1 || nsrc > 3 || !q_lens) return fail(LFAMD_ERR_ARG, "%s: 1 to 3 sources expected", who);
+  for (int i = 0; i < nsrc; ++i)
+    if (q_lens[i] < 1) return fail(LFAMD_ERR_ARG, "%s: source %d has no rows", who, i);
+  if (dtype != LFAMD_F16 || d.M != 49 || d.C <= 0 || d.C % 64 != 0 || d.BH() < 1 || d.C / 64 > 65535)
+    return fail(LFAMD_ERR_UNSUPPORTED, "%s: no single-launch path (dtype %d, M=%lld, C=%lld)", who, dtype,
+                (long long)d.M, (long long)d.C);
+  if (queries)
+    for (int i = 0; i < nsrc; ++i)
+      if (reinterpret_cast<uintptr_t>(queries[i]) & 3)
+        return fail(LFAMD_ERR_UNSUPPORTED, "%s: query %d not 4-byte aligned", who, i);
+  return LFAMD_OK;
+}
+}  // namespace
+
+size_t lfamd_laplace_kernel_backward_multi_workspace_size(int num_sources, const int64_t* q_lens, int64_t batch,
+                                                          int64_t heads, int64_t k_len, int64_t channels) {
+  const Dims d{batch, heads, 1, k_len, channels};
+  if (check_dims(d, "laplace kernel backward (several sources)") ||
+      multi_bwd_check(LFAMD_F16, num_sources, q_lens, nullptr, d, "laplace kernel backward (several sources)"))
+    return 0;
+  return b2_workspace_elems_multi(num_sources, q_lens, d.BH(), d.C) * 4;
+}
+
+int lfamd_laplace_kernel_backward_multi(int dtype, int num_sources, const float* const* grad_kernels,
+                                        const float* const* kernels, const void* const* queries,
+                                        const int64_t* q_lens, const void* key, void* const* grad_queries,
+                                        void* grad_key, int64_t batch, int64_t heads, int64_t k_len,
+                                        int64_t channels, float scale, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  const char* who = "laplace kernel backward (several sources)";
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dtype);
+  const Dims d{batch, heads, 1, k_len, channels};
+  int s = check_dims(d, who);
+  if (s) return s;
+  if (!grad_kernels || !kernels || !queries || !grad_queries || !key || !grad_key)
+    return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
+  if ((s = multi_bwd_check(dtype, num_sources, q_lens, queries, d, who))) return s;
+  for (int i = 0; i < num_sources; ++i)
+    if (!grad_kernels[i] || !kernels[i] || !grad_queries[i]) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
+  return b2_launch_multi(num_sources, grad_kernels, kernels, queries, grad_queries, q_lens, key, grad_key, workspace,
+                         workspace_bytes, d.BH(), d.C, scale, static_cast<hipStream_t>(stream), who);
+}
+
 int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const float* kernel,
                                   const void* query, const void* key, void* grad_query, void* grad_key,
                                   int64_t batch, int64_t heads, int64_t q_len, int64_t k_len,

@@ -73,7 +73,8 @@ __device__ __forceinline__ void pool_bwd_stage(float* __restrict__ tt, float* __
   for (int e = threadIdx.x; e < total; e += 256) {
     const int c = e / mw, mx = e - c * mw;
     const int64_t cm = (bh * d + c) * M + (int64_t)my * mw + mx;
-    tt[c * mw + mx] = to_acc(from_acc<T>(to_acc(from_acc<T>(to_acc(dcm0[cm]) + to_acc(dcm1[cm]))) + to_acc(dcm2[cm])));
+    tt[c * mw + mx] = to_acc(from_acc<T>(to_acc(from_acc<T>(to_acc(dcm0[cm]) + (dcm1 ? to_acc(dcm1[cm]) : 0.0f))) +
+                                         (dcm2 ? to_acc(dcm2[cm]) : 0.0f)));
   }
   __syncthreads();
   for (int e = threadIdx.x; e < total; e += 256) {
@@ -137,7 +138,8 @@ landmark_pool_bwd_any_kernel(T* __restrict__ dk, const T* __restrict__ dkm, cons
     const int x = e / d, c = e - x * d;
     const int m = (y / pool) * mw + x / pool;
     const int64_t cm = (bh * d + c) * M + m;
-    const T t = from_acc<T>(to_acc(from_acc<T>(to_acc(dcm0[cm]) + to_acc(dcm1[cm]))) + to_acc(dcm2[cm]));
+    const T t = from_acc<T>(to_acc(from_acc<T>(to_acc(dcm0[cm]) + (dcm1 ? to_acc(dcm1[cm]) : 0.0f))) +
+                            (dcm2 ? to_acc(dcm2[cm]) : 0.0f));
     const T u = from_acc<T>(to_acc(dkm[(bh * M + m) * d + c]) + to_acc(t));
     const T gs = from_acc<T>(to_acc(u) * inv);
     row[e] = from_acc<T>(to_acc(row[e]) + to_acc(gs));
@@ -201,7 +203,7 @@ extern "C" int lfamd_landmark_pool_backward(int dtype, void* dk, const void* dkm
                                             void* stream) {
   if (int s = check_pool(dtype, B, H, gh, gw, pool, d, "landmark pool backward")) return s;
   if (B * H == 0) return ok();
-  if (!dk || !dkm || !dcm0 || !dcm1 || !dcm2) return fail(LFAMD_ERR_ARG, "landmark pool backward: null pointer");
+  if (!dk || !dkm || !dcm0) return fail(LFAMD_ERR_ARG, "landmark pool backward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case LFAMD_F32: launch_pool_bwd<float>(dk, dkm, dcm0, dcm1, dcm2, B * H, gh, gw, pool, d, st); break;

@@ -42,6 +42,13 @@ size_t b2_workspace_elems(int64_t BH, int64_t N, int64_t M, int64_t C);
 int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, void* dk, void* ws, size_t wsBytes,
               int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st, const char* who,
               const B2Grad& kg = B2Grad{});
+// The fused-kernel gradient (fp16, M = 49, C % 64 == 0) of up to three row
+// sources sharing one key in one launch: per source n[i] rows, gk[i], kv[i],
+// query q[i] (4-byte aligned) and grad_query dq[i]; grad_key dk sums them all.
+size_t b2_workspace_elems_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C);
+int b2_launch_multi(int nsrc, const float* const* gk, const float* const* kv, const void* const* q, void* const* dq,
+                    const int64_t* n, const void* k, void* dk, void* ws, size_t wsBytes, int64_t BH, int64_t C,
+                    float scale, hipStream_t st, const char* who);
 
 // Row-staged forward of LaplaceSubtraction at M = 49 (laplace_fwd2.hip); kernelEpi:
 // exp(-scale * distance) in fp32 instead of the distance in the element type.

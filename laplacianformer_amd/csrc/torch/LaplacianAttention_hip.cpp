@@ -15,6 +15,7 @@
 #include <torch/types.h>
 
 #include <cmath>
+#include <tuple>
 #include <vector>
 
 #include "LaplaceSubtraction.h"
@@ -132,15 +133,42 @@ std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at
   at::Tensor d_v = mix_rows(k_km, d_kv.transpose(-1, -2), v.scalar_type());  // K_km dkv [B,H,N,d]
   at::Tensor d_kmm = at::empty_like(k_mm);
   NewtonInverse_backward(d_inv.contiguous(), inv, d_kmm);
-  auto [d_q, d_cm] = kernel_bwd(d_kqm, k_qm, q, km_cm, s);
-  auto [d_km, d_cm2] = kernel_bwd(d_kmm, k_mm, km, km_cm, s);
-  auto [d_k, d_cm3] = kernel_bwd(d_kkm, k_km, k, km_cm, s);
-  // The landmarks' gradient, d_km + (d_cm + d_cm2 + d_cm3)^T, / pool^2 onto each
-  // pool x pool patch of k's distance gradient (every step rounded to the type).
   at::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
+  const int dt = detail::abi_dtype(k, "laplacian attention backward");
+  // The three distances' gradients (K_qm, K_km, K_mm share the key km_cm): one
+  // launch whose grad_key is their sum where the fused path takes it (K_mm's
+  // 49-row slices first: their workgroups end early and let the others in).
+  at::Tensor d_q = at::empty_like(q), d_k = at::empty_like(k), d_km = at::empty_like(km);
+  at::Tensor d_cm = at::empty_like(km_cm), d_cm2, d_cm3;
+  {
+    const float* gks[3] = {d_kmm.data_ptr<float>(), d_kqm.data_ptr<float>(), d_kkm.data_ptr<float>()};
+    const float* kvs[3] = {k_mm.data_ptr<float>(), k_qm.data_ptr<float>(), k_km.data_ptr<float>()};
+    const void* qs[3] = {km.data_ptr(), q.data_ptr(), k.data_ptr()};
+    void* dqs[3] = {d_km.data_ptr(), d_q.data_ptr(), d_k.data_ptr()};
+    const int64_t ns[3] = {km.size(2), q.size(2), k.size(2)};
+    const size_t wsb = lfamd_laplace_kernel_backward_multi_workspace_size(3, ns, B, H, km_cm.size(3), dd);
+    int st = LFAMD_ERR_UNSUPPORTED;
+    if (wsb > 0 && d_kqm.is_contiguous() && d_kkm.is_contiguous() && d_kmm.is_contiguous()) {
+      at::Tensor ws = at::empty({(int64_t)wsb}, k.options().dtype(at::kByte));
+      st = lfamd_laplace_kernel_backward_multi(dt, 3, gks, kvs, qs, ns, km_cm.data_ptr(), dqs, d_cm.data_ptr(), B, H,
+                                               km_cm.size(3), dd, (float)s, ws.data_ptr(), wsb,
+                                               detail::stream_of(k));
+    }
+    if (st == LFAMD_ERR_UNSUPPORTED) {
+      std::tie(d_q, d_cm) = kernel_bwd(d_kqm, k_qm, q, km_cm, s);
+      std::tie(d_km, d_cm2) = kernel_bwd(d_kmm, k_mm, km, km_cm, s);
+      std::tie(d_k, d_cm3) = kernel_bwd(d_kkm, k_km, k, km_cm, s);
+    } else {
+      detail::check_status(st);
+    }
+  }
+  // The landmarks' gradient, d_km + (d_cm + d_cm2 + d_cm3)^T (the last two absent
+  // when the one launch summed them into d_cm), / pool^2 onto each pool x pool
+  // patch of k's distance gradient (every step rounded to the type).
   detail::check_status(lfamd_landmark_pool_backward(
-      detail::abi_dtype(d_k, "laplacian attention backward"), d_k.data_ptr(), d_km.data_ptr(), d_cm.data_ptr(),
-      d_cm2.data_ptr(), d_cm3.data_ptr(), B, H, (int)gh, (int)gw, (int)pool, (int)dd, detail::stream_of(d_k)));
+      dt, d_k.data_ptr(), d_km.data_ptr(), d_cm.data_ptr(), d_cm2.defined() ? d_cm2.data_ptr() : nullptr,
+      d_cm3.defined() ? d_cm3.data_ptr() : nullptr, B, H, (int)gh, (int)gw, (int)pool, (int)dd,
+      detail::stream_of(d_k)));
   return {d_q, d_k, d_v};
 }
 

@@ -167,3 +167,73 @@ def test_kernel_gradcheck_f64(gpu):
     q = torch.randn(1, 2, 5, 3, dtype=torch.float64, device=gpu, requires_grad=True)
     k = torch.randn(1, 2, 3, 4, dtype=torch.float64, device=gpu, requires_grad=True)
     assert torch.autograd.gradcheck(lambda a, b: lf.laplace_kernel(a, b, 0.7), (q, k), eps=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("lens", [(784, 784, 49), (65, 1, 200), (130, 7)], ids=lambda s: "-".join(map(str, s)))
+def test_kernel_backward_multi(gpu, lens):
+    """lfamd_laplace_kernel_backward_multi: up to three row sources against one key in one launch.
+    Each source's grad_query is bit-identical to its own lfamd_laplace_kernel_backward call (the
+    same rows per workgroup and wave); grad_key, the sum over the sources, is held to the oracle's
+    fp64 sum with the usual bound."""
+    import ctypes
+
+    import laplacianformer_amd as lf
+
+    B, H, M, C = 2, 2, 49, 64
+    print(f"laplace kernel backward multi {lens}", flush=True)
+    lib = lf.capi()
+    s = 1.0 / math.sqrt(C)
+    k = gen((B, H, C, M), 831, "f16")
+    srcs = []
+    for i, n in enumerate(lens):
+        q = gen((B, H, n, C), 840 + i, "f16")
+        gk = gen((B, H, n, M), 850 + i, "f32")
+        kern = torch.exp(-torch.rand((B, H, n, M), generator=torch.Generator().manual_seed(860 + i)) * 4)
+        srcs.append((q, gk, kern))
+    kd = k.to(gpu)
+    qd = [q.to(gpu) for q, _, _ in srcs]
+    gkd = [gk.to(gpu) for _, gk, _ in srcs]
+    kvd = [kv.to(gpu) for _, _, kv in srcs]
+    dqs = [torch.empty_like(q) for q in qd]
+    dk = torch.empty_like(kd)
+    ns = len(lens)
+    nl = (ctypes.c_int64 * ns)(*lens)
+    P = lambda ts: (ctypes.c_void_p * ns)(*[t.data_ptr() for t in ts])  # noqa: E731
+    wsb = lib.lfamd_laplace_kernel_backward_multi_workspace_size(ns, nl, B, H, M, C)
+    assert wsb > 0
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lf.check(lib.lfamd_laplace_kernel_backward_multi(lf.dtype_code(kd), ns, P(gkd), P(kvd), P(qd), nl, kd.data_ptr(),
+                                                      P(dqs), dk.data_ptr(), B, H, M, C, ctypes.c_float(s),
+                                                      ws.data_ptr(), wsb, stream))
+    L = lf.ext()
+    rk = 0.0
+    scale = 0.0
+    for (q, gk, kern), q1, g1, kv1, dq in zip(srcs, qd, gkd, kvd, dqs):
+        ref_dq = torch.empty_like(q1)
+        assert L.LaplaceKernel_backward(g1, kv1, q1, kd, ref_dq, None, s) is True
+        torch.cuda.synchronize()
+        assert torch.equal(dq, ref_dq), "grad_query differs from the single-source call"
+        g64 = -s * gk.double().numpy() * kern.double().numpy()
+        rk = rk + oracle.laplace_backward_key(g64, q, k, "f64")
+        scale = scale + np.abs(g64).sum(axis=2, keepdims=True)
+    assert_l1_close(dk, rk, "f16", "dk (sum over the sources)", np.broadcast_to(scale, rk.shape))
+
+
+def test_kernel_backward_multi_rejects(gpu):
+    import ctypes
+
+    import laplacianformer_amd as lf
+
+    lib = lf.capi()
+    null = ctypes.c_void_p(0)
+    one = (ctypes.c_int64 * 1)(4)
+    ptrs = (ctypes.c_void_p * 1)(16)
+    call = lambda dt, ns, m, c: lib.lfamd_laplace_kernel_backward_multi(  # noqa: E731
+        dt, ns, ptrs, ptrs, ptrs, one, ctypes.c_void_p(16), ptrs, ctypes.c_void_p(16), 1, 1, m, c, ctypes.c_float(1.0),
+        null, 0, null)
+    assert call(1, 0, 49, 64) == 1 and call(1, 4, 49, 64) == 1   # 1 to 3 sources
+    assert call(1, 1, 48, 64) == 3                               # M != 49 (LFAMD_ERR_UNSUPPORTED)
+    assert call(2, 1, 49, 64) == 3 and call(1, 1, 49, 40) == 3   # bf16; C % 64 != 0
+    assert call(1, 1, 49, 64) == 1                               # no workspace
+    assert lib.lfamd_laplace_kernel_backward_multi_workspace_size(1, one, 1, 1, 48, 64) == 0
