@@ -145,6 +145,20 @@ int lfamd_laplace_kernel_backward(int dtype, const float* grad_kernel, const flo
                                   int64_t channels, float scale, void* workspace,
                                   size_t workspace_bytes, void* stream);
 
+/* lfamd_laplace_kernel_forward for up to three queries that share one key, in
+ * one launch: source i has q_lens[i] >= 1 rows per (b, h) slice, query
+ * queries[i] [B,H,q_lens[i],C] and fp32 output outputs[i] [B,H,q_lens[i],M];
+ * each output is what lfamd_laplace_kernel_forward gives for that query alone
+ * (the same bits). No reference counterpart: for callers with several kernel
+ * matrices against one landmark key (the LaplacianFormer layer's K_qm, K_km and
+ * K_mm). LFAMD_ERR_UNSUPPORTED unless M = 49, 8 <= C <= 64 with C % 8 == 0, a
+ * float dtype other than fp64 and 16-byte aligned queries; callers then make
+ * one call per source. */
+int lfamd_laplace_kernel_forward_multi(int dtype, int num_sources, const void* const* queries,
+                                       const int64_t* q_lens, const void* key, float* const* outputs,
+                                       int64_t batch, int64_t heads, int64_t k_len, int64_t channels,
+                                       float scale, void* stream);
+
 /* lfamd_laplace_kernel_backward for up to three row sources that share one key,
  * in one launch: source i has q_lens[i] >= 1 rows per (b, h) slice with fp32
  * grad_kernels[i] and kernels[i] [B,H,q_lens[i],M], fp16 queries[i]

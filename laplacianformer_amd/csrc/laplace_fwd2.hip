@@ -103,14 +103,28 @@ struct F2Sched {
   int full;  // full row sets of the workgroup (the tail starts at row 64 * full)
 };
 
+// Up to three row sources sharing one key in one launch (count > 0): source i
+// has N[i] rows per slice (query q[i], output o[i]) split over nx[i]
+// workgroups per slice with its own schedule sched[i]; the linear workgroup id
+// runs source-major (all of source 0's workgroups first). count = 0: one
+// source, the plain arguments.
+struct F2Seg {
+  int count;
+  int nx[3], N[3];
+  const void* q[3];
+  void* o[3];
+  F2Sched sched[3];
+};
+
 // Grid: (nx workgroups per slice, B*H). Workgroup x takes rows
 // [x*N/nx, (x+1)*N/nx) of its slice (at most kF2MaxRows); WAVES waves (2 or 4
 // per SIMD) run the schedule. Rows past the workgroup's end are computed on
 // clamped rows and not stored.
 template <typename T, int EPI, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES, 1)
-laplace_fwd2_kernel(const T* __restrict__ query, const T* __restrict__ key, typename F2Out<T, EPI>::type* __restrict__ out,
-                    int N, int C, float scale, F2Sched sched) {
+laplace_fwd2_kernel(const T* __restrict__ queryIn, const T* __restrict__ key,
+                    typename F2Out<T, EPI>::type* __restrict__ outIn, int NIn, int C, float scale, F2Sched sched,
+                    F2Seg sg) {
   using O = typename F2Out<T, EPI>::type;
   constexpr int THREADS = 64 * WAVES;
   constexpr int OCC = WAVES / 8;            // asm register budget: 256 (8 waves) or 128 (16) VGPRs
@@ -119,7 +133,22 @@ laplace_fwd2_kernel(const T* __restrict__ query, const T* __restrict__ key, type
   const int tid = threadIdx.x;
   const int wave = uniform(tid >> 6);
   const int lane = tid & 63;
-  const int x = blockIdx.x, nx = gridDim.x, bh = blockIdx.y;
+  int x = blockIdx.x, nx = gridDim.x, bh = blockIdx.y, N = NIn, si = -1;
+  const T* query = queryIn;
+  O* out = outIn;
+  if (sg.count > 0) {
+    const int L = x + nx * bh, S = (int)gridDim.y;
+    const int e1 = S * sg.nx[0], e2 = e1 + S * sg.nx[1];
+    si = L < e1 ? 0 : (L < e2 ? 1 : 2);
+    nx = si == 0 ? sg.nx[0] : si == 1 ? sg.nx[1] : sg.nx[2];
+    const int Ls = L - (si == 0 ? 0 : si == 1 ? e1 : e2);
+    bh = Ls / nx;
+    x = Ls - bh * nx;
+    N = si == 0 ? sg.N[0] : si == 1 ? sg.N[1] : sg.N[2];
+    query = static_cast<const T*>(si == 0 ? sg.q[0] : si == 1 ? sg.q[1] : sg.q[2]);
+    out = static_cast<O*>(si == 0 ? sg.o[0] : si == 1 ? sg.o[1] : sg.o[2]);
+  }
+  const int sfull = si < 0 ? sched.full : si == 0 ? sg.sched[0].full : si == 1 ? sg.sched[1].full : sg.sched[2].full;
   const int P0 = (int)((int64_t)x * N / nx), P1 = (int)((int64_t)(x + 1) * N / nx);
   const int n = P1 - P0;
   const int QP = C + 4;
@@ -171,10 +200,14 @@ laplace_fwd2_kernel(const T* __restrict__ query, const T* __restrict__ key, type
   __syncthreads();
 
   const unsigned kBase = (unsigned)(uintptr_t)ktile, qBase = (unsigned)(uintptr_t)qtile;
-  const uint32_t me = wave < 16 ? sched.w[wave] : 0u;
+  const uint32_t me = wave >= 16 ? 0u
+                      : si < 0  ? sched.w[wave]
+                      : si == 0 ? sg.sched[0].w[wave]
+                      : si == 1 ? sg.sched[1].w[wave]
+                                : sg.sched[2].w[wave];
   const int b = uniform((int)(me & 7)), s0 = uniform((int)((me >> 3) & 7)), R = uniform((int)((me >> 6) & 7));
   const bool hasTail = (me >> 9) & 1;
-  const int trows = n - 64 * sched.full;  // tail rows of this workgroup (may be <= 0)
+  const int trows = n - 64 * sfull;  // tail rows of this workgroup (may be <= 0)
   float acc[RMAX][kF2JB];
   float acct[1][kF2JB];
   unsigned qa[RMAX];
@@ -199,7 +232,7 @@ laplace_fwd2_kernel(const T* __restrict__ query, const T* __restrict__ key, type
   }
   // The tail: one lane per (row, column block), lanes [0, 7 * trows).
   const int bt = lane % kF2NB;
-  const int rowt = 64 * sched.full + min(lane / kF2NB, max(trows, 1) - 1);
+  const int rowt = 64 * sfull + min(lane / kF2NB, max(trows, 1) - 1);
   if (hasTail && trows > 0) {
     const unsigned qt[1] = {qBase + (unsigned)(min(rowt, n - 1) * QP) * 4};
     F2Sums<1, OCC>::run(acct, qt, kBase + (unsigned)bt * 32, C / 8);
@@ -403,21 +436,21 @@ F2Plan plan_f2(int64_t BH, int64_t N, int64_t C, size_t outBytes) {
 
 template <typename T, int EPI, int WAVES>
 int launch_f2_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C, float scale,
-                const F2Plan& p, hipStream_t st) {
+                const F2Plan& p, hipStream_t st, const F2Seg& sg) {
   using O = typename F2Out<T, EPI>::type;
   auto kern = laplace_fwd2_kernel<T, EPI, WAVES>;
   if (p.lds > 65536)
     if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
   hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(q),
-                     static_cast<const T*>(k), static_cast<O*>(o), (int)N, (int)C, scale, p.sched);
+                     static_cast<const T*>(k), static_cast<O*>(o), (int)N, (int)C, scale, p.sched, sg);
   return check_launch("laplace forward (row-staged)");
 }
 
 template <typename T, int EPI>
 int launch_f2_t(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C, float scale,
-                const F2Plan& p, hipStream_t st) {
-  if (p.waves == 16) return launch_f2_w<T, EPI, 16>(q, k, o, BH, N, C, scale, p, st);
-  return launch_f2_w<T, EPI, 8>(q, k, o, BH, N, C, scale, p, st);
+                const F2Plan& p, hipStream_t st, const F2Seg& sg = F2Seg{}) {
+  if (p.waves == 16) return launch_f2_w<T, EPI, 16>(q, k, o, BH, N, C, scale, p, st, sg);
+  return launch_f2_w<T, EPI, 8>(q, k, o, BH, N, C, scale, p, st, sg);
 }
 
 // ---------------------------------------------------------------------------
@@ -574,8 +607,8 @@ int f3_launch(int dtype, const void* q, const void* k, void* o, int64_t BH, int6
   return launch_f3<bf16s>(q, k, o, BH, N, M, C, st);
 }
 
-int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,
-              float scale, hipStream_t st) {
+namespace {
+const F2Plan& f2_plan_cached(int dtype, bool kernelEpi, int64_t BH, int64_t N, int64_t C) {
   // The plan's schedule search (~80 us of host time for six row sets) is
   // cached per shape, per host thread, for the last kPlanCache shapes (a layer
   // step alternates three; the CU count is per device, so the device is part
@@ -604,7 +637,13 @@ int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, 
     plans[slot] = plan_f2(BH, N, C, key.ob);
     keys[slot] = key;
   }
-  const F2Plan& p = plans[slot];
+  return plans[slot];
+}
+}  // namespace
+
+int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,
+              float scale, hipStream_t st) {
+  const F2Plan& p = f2_plan_cached(dtype, kernelEpi, BH, N, C);
   if (p.lds > (size_t)max_lds_bytes()) return fail(LFAMD_ERR_UNSUPPORTED, "laplace forward: LDS plan too large");
   if (kernelEpi) {
     if (dtype == LFAMD_F32) return launch_f2_t<float, kF2Exp>(q, k, o, BH, N, C, scale, p, st);
@@ -614,6 +653,34 @@ int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, 
   if (dtype == LFAMD_F32) return launch_f2_t<float, kF2Dist>(q, k, o, BH, N, C, scale, p, st);
   if (dtype == LFAMD_F16) return launch_f2_t<f16s, kF2Dist>(q, k, o, BH, N, C, scale, p, st);
   return launch_f2_t<bf16s, kF2Dist>(q, k, o, BH, N, C, scale, p, st);
+}
+
+// The fused-kernel forward over up to three row sources sharing one key, one
+// launch: each source keeps its own plan (workgroups per slice, wave schedule);
+// LFAMD_ERR_UNSUPPORTED when their wave counts differ or the LDS plan is too
+// large. Needs f2_ok for every source.
+int f2_launch_multi(int dtype, int nsrc, const void* const* q, const int64_t* n, const void* k, float* const* o,
+                    int64_t BH, int64_t C, float scale, hipStream_t st) {
+  F2Seg sg{};
+  F2Plan p{};
+  sg.count = nsrc;
+  for (int i = 0; i < nsrc; ++i) {
+    const F2Plan& pi = f2_plan_cached(dtype, true, BH, n[i], C);
+    if (i > 0 && pi.waves != p.waves)
+      return fail(LFAMD_ERR_UNSUPPORTED, "laplace kernel forward (several sources): plans of different widths");
+    p.waves = pi.waves;
+    p.lds = std::max(p.lds, pi.lds);
+    p.nx += pi.nx;
+    sg.nx[i] = pi.nx;
+    sg.N[i] = (int)n[i];
+    sg.q[i] = q[i];
+    sg.o[i] = o[i];
+    sg.sched[i] = pi.sched;
+  }
+  if (p.lds > (size_t)max_lds_bytes()) return fail(LFAMD_ERR_UNSUPPORTED, "laplace forward: LDS plan too large");
+  if (dtype == LFAMD_F32) return launch_f2_t<float, kF2Exp>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
+  if (dtype == LFAMD_F16) return launch_f2_t<f16s, kF2Exp>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
+  return launch_f2_t<bf16s, kF2Exp>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
 }
 
 }  // namespace lfamd

@@ -1930,6 +1930,29 @@ int lfamd_laplace_kernel_forward(int dtype, const void* query, const void* key, 
   }
 }
 
+int lfamd_laplace_kernel_forward_multi(int dtype, int num_sources, const void* const* queries,
+                                       const int64_t* q_lens, const void* key, float* const* outputs,
+                                       int64_t batch, int64_t heads, int64_t k_len, int64_t channels,
+                                       float scale, void* stream) {
+  const char* who = "laplace kernel forward (several sources)";
+  if (!valid_dtype(dtype)) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dtype);
+  if (num_sources < 1 || num_sources > 3 || !queries || !q_lens || !outputs)
+    return fail(LFAMD_ERR_ARG, "%s: 1 to 3 sources with their arrays expected", who);
+  for (int i = 0; i < num_sources; ++i)
+    if (q_lens[i] < 1 || !queries[i] || !outputs[i]) return fail(LFAMD_ERR_ARG, "%s: source %d empty or null", who, i);
+  const Dims d{batch, heads, 1, k_len, channels};
+  int s = check_dims(d, who);
+  if (s) return s;
+  if (d.BH() == 0) return ok();
+  if (!key) return fail(LFAMD_ERR_ARG, "%s: null pointer", who);
+  for (int i = 0; i < num_sources; ++i)
+    if (!f2_ok(dtype, d.BH(), q_lens[i], d.M, d.C, queries[i]))
+      return fail(LFAMD_ERR_UNSUPPORTED, "%s: no single-launch path (dtype %d, M=%lld, C=%lld, source %d)", who,
+                  dtype, (long long)d.M, (long long)d.C, i);
+  return f2_launch_multi(dtype, num_sources, queries, q_lens, key, outputs, d.BH(), d.C, scale,
+                         static_cast<hipStream_t>(stream));
+}
+
 namespace {
 // The segmented fused-kernel backward applies: fp16, M = 49, C % 64 == 0,
 // 1 to 3 sources of at least one row, 4-byte aligned queries.

@@ -59,6 +59,10 @@ int f3_launch(int dtype, const void* q, const void* k, void* o, int64_t BH, int6
               hipStream_t st);
 int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C,
               float scale, hipStream_t st);
+// exp(-scale * distance) over up to three row sources (n[i] rows per slice,
+// query q[i], fp32 output o[i]) sharing one key, in one launch.
+int f2_launch_multi(int dtype, int nsrc, const void* const* q, const int64_t* n, const void* k, float* const* o,
+                    int64_t BH, int64_t C, float scale, hipStream_t st);
 
 inline bool valid_dtype(int dt) {
   return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;

@@ -38,6 +38,34 @@ at::Tensor kernel_fwd(const at::Tensor& query, const at::Tensor& key_cm, double 
   return at::exp(dist * -scale);
 }
 
+// exp(-scale * L1(x, key_cm)) for the layer's row sets x = km, q, k in one
+// launch where the fused path takes them all (K_mm's 49-row slices first: their
+// workgroups end early and let the others in); else one call each. Returns
+// {K_mm, K_qm, K_km}.
+std::vector<at::Tensor> kernel_fwd3(const at::Tensor& km, const at::Tensor& q, const at::Tensor& k,
+                                    const at::Tensor& key_cm, double scale) {
+  const int64_t B = q.size(0), H = q.size(1), C = q.size(3), M = key_cm.size(3);
+  const at::Tensor* xs[3] = {&km, &q, &k};
+  std::vector<at::Tensor> outs;
+  const void* qp[3];
+  float* op[3];
+  int64_t n[3];
+  for (int i = 0; i < 3; ++i) {
+    outs.push_back(at::empty({B, H, xs[i]->size(2), M}, q.options().dtype(at::kFloat)));
+    qp[i] = xs[i]->data_ptr();
+    op[i] = outs[i].data_ptr<float>();
+    n[i] = xs[i]->size(2);
+  }
+  at::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int st = lfamd_laplace_kernel_forward_multi(detail::abi_dtype(q, "laplacian attention"), 3, qp, n,
+                                                    key_cm.data_ptr(), op, B, H, M, C, (float)scale,
+                                                    detail::stream_of(q));
+  if (st == LFAMD_ERR_UNSUPPORTED)
+    return {kernel_fwd(km, key_cm, scale), kernel_fwd(q, key_cm, scale), kernel_fwd(k, key_cm, scale)};
+  detail::check_status(st);
+  return outs;
+}
+
 // (grad_query, grad_key) of exp(-scale * L1(query, key_cm)) for the fp32 dL/dK = grad.
 std::pair<at::Tensor, at::Tensor> kernel_bwd(const at::Tensor& grad, const at::Tensor& kern, const at::Tensor& query,
                                              const at::Tensor& key_cm, double scale) {
@@ -102,9 +130,8 @@ std::vector<at::Tensor> LaplacianAttention_forward(at::Tensor q, at::Tensor k, a
   detail::check_status(lfamd_landmark_pool(detail::abi_dtype(k, "laplacian attention"), k.data_ptr(),
                                            km.data_ptr(), km_cm.data_ptr(), B, H, (int)gh, (int)gw, (int)pool,
                                            (int)d, detail::stream_of(k)));
-  at::Tensor k_qm = kernel_fwd(q, km_cm, s);
-  at::Tensor k_mm = kernel_fwd(km, km_cm, s);
-  at::Tensor k_km = kernel_fwd(k, km_cm, s);
+  const std::vector<at::Tensor> kk = kernel_fwd3(km, q, k, km_cm, s);
+  const at::Tensor &k_mm = kk[0], &k_qm = kk[1], &k_km = kk[2];
   at::Tensor inv = at::empty_like(k_mm);
   NewtonInverse_forward(k_mm, inv, iters);
   at::Tensor kv = tall_t(k_km, v);                               // K_km^T V  [B,H,M,d]

@@ -237,3 +237,49 @@ def test_kernel_backward_multi_rejects(gpu):
     assert call(2, 1, 49, 64) == 3 and call(1, 1, 49, 40) == 3   # bf16; C % 64 != 0
     assert call(1, 1, 49, 64) == 1                               # no workspace
     assert lib.lfamd_laplace_kernel_backward_multi_workspace_size(1, one, 1, 1, 48, 64) == 0
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("lens", [(49, 784, 784), (1, 130, 49), (300, 5), (449,)], ids=lambda s: "-".join(map(str, s)))
+def test_kernel_forward_multi(gpu, dt, lens):
+    """lfamd_laplace_kernel_forward_multi: up to three row sources against one key in one launch
+    (each with its own workgroup plan) give each source's lfamd_laplace_kernel_forward result,
+    bit for bit."""
+    import ctypes
+
+    import laplacianformer_amd as lf
+
+    B, H, M, C = 2, 2, 49, 64
+    print(f"laplace kernel forward multi {lens} {dt}", flush=True)
+    lib = lf.capi()
+    k = gen((B, H, C, M), 811, dt).to(gpu)
+    qs = [gen((B, H, n, C), 820 + i, dt).to(gpu) for i, n in enumerate(lens)]
+    s = 1.0 / math.sqrt(C)
+    outs = [torch.empty((B, H, n, M), dtype=torch.float32, device=gpu) for n in lens]
+    ns = len(lens)
+    P = lambda ts: (ctypes.c_void_p * ns)(*[t.data_ptr() for t in ts])  # noqa: E731
+    nl = (ctypes.c_int64 * ns)(*lens)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lf.check(lib.lfamd_laplace_kernel_forward_multi(lf.dtype_code(k), ns, P(qs), nl, k.data_ptr(), P(outs), B, H, M,
+                                                     C, ctypes.c_float(s), stream))
+    for q, o in zip(qs, outs):
+        ref = torch.empty_like(o)
+        assert lf.ext().LaplaceKernel_forward(q, k, ref, s) is True
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref)
+
+
+def test_kernel_forward_multi_rejects(gpu):
+    import ctypes
+
+    import laplacianformer_amd as lf
+
+    lib = lf.capi()
+    null = ctypes.c_void_p(0)
+    one = (ctypes.c_int64 * 1)(4)
+    ptrs = (ctypes.c_void_p * 1)(16)
+    f = lambda dt, ns, m: lib.lfamd_laplace_kernel_forward_multi(dt, ns, ptrs, one, ctypes.c_void_p(16), ptrs, 1, 1,  # noqa: E731
+                                                                 m, 64, ctypes.c_float(1.0), null)
+    assert f(1, 0, 49) == 1 and f(1, 4, 49) == 1   # 1 to 3 sources
+    assert f(1, 1, 48) == 3                        # M != 49 (LFAMD_ERR_UNSUPPORTED)
+    assert f(3, 1, 49) == 3                        # fp64
