@@ -209,8 +209,8 @@ __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int sk
 // Up to three row sources sharing one key in one launch (fused-kernel gradient
 // only): the slice's workgroups are segments of nx[i] workgroups over source
 // i's N[i] rows (gk[i], kv[i], query q[i], grad_query dq[i]); every workgroup
-// writes a partial, so grad_key sums all sources' rows. count = 0: one source,
-// the plain arguments.
+// writes a partial, so grad_key sums all sources' rows. Read only by the SEG
+// instantiations.
 struct B2Seg {
   int count;
   int nx[3], N[3];
@@ -220,7 +220,7 @@ struct B2Seg {
   void* dq[3];
 };
 
-template <typename T, int M, bool DQ, bool DK, bool GK = false>
+template <typename T, int M, bool DQ, bool DK, bool GK = false, bool SEG = false>
 __global__ void __launch_bounds__(64 * b2_waves(M), 1)
 laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gkIn, const float* __restrict__ kvIn,
                     float gscale, const T* __restrict__ queryIn, const T* __restrict__ key, T* __restrict__ dqIn,
@@ -240,7 +240,7 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gkIn, 
   const float* kv = kvIn;
   const T* query = queryIn;
   T* dq = dqIn;
-  if (sg.count > 0) {
+  if constexpr (SEG) {
     // Source-major order of the linear workgroup id (dispatch order): all of
     // source 0's workgroups, then source 1's, then source 2's. (Slice-major
     // order left a third round of big workgroups on half the CUs; callers put
@@ -514,7 +514,15 @@ int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk,
                 int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg, const B2Seg& sg = B2Seg{}) {
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
   T* dkOut = DK && p.nx == 1 && sg.count == 0 ? static_cast<T*>(dk) : nullptr;
-  if (kg.gk)
+  if (kg.gk && sg.count > 0) {
+    if constexpr (M == 49 && DQ && DK)
+      hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true, true>), grid, dim3(64 * b2_waves(M)), p.lds, st,
+                         static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
+                         static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N,
+                         (int)C, sg);
+    else
+      return fail(LFAMD_ERR_UNSUPPORTED, "laplace backward: several sources need M = 49 with dq and dk");
+  } else if (kg.gk)
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
                        static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C,

@@ -106,8 +106,8 @@ struct F2Sched {
 // Up to three row sources sharing one key in one launch (count > 0): source i
 // has N[i] rows per slice (query q[i], output o[i]) split over nx[i]
 // workgroups per slice with its own schedule sched[i]; the linear workgroup id
-// runs source-major (all of source 0's workgroups first). count = 0: one
-// source, the plain arguments.
+// runs source-major (all of source 0's workgroups first). Read only by the
+// SEG instantiations (the plain ones take the plain arguments).
 struct F2Seg {
   int count;
   int nx[3], N[3];
@@ -120,11 +120,10 @@ struct F2Seg {
 // [x*N/nx, (x+1)*N/nx) of its slice (at most kF2MaxRows); WAVES waves (2 or 4
 // per SIMD) run the schedule. Rows past the workgroup's end are computed on
 // clamped rows and not stored.
-template <typename T, int EPI, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES, 1)
-laplace_fwd2_kernel(const T* __restrict__ queryIn, const T* __restrict__ key,
-                    typename F2Out<T, EPI>::type* __restrict__ outIn, int NIn, int C, float scale, F2Sched sched,
-                    F2Seg sg) {
+template <typename T, int EPI, int WAVES, bool SEG>
+__device__ __forceinline__ void fwd2_body(const T* __restrict__ queryIn, const T* __restrict__ key,
+                                          typename F2Out<T, EPI>::type* __restrict__ outIn, int NIn, int C,
+                                          float scale, const F2Sched& sched, const F2Seg& sg) {
   using O = typename F2Out<T, EPI>::type;
   constexpr int THREADS = 64 * WAVES;
   constexpr int OCC = WAVES / 8;            // asm register budget: 256 (8 waves) or 128 (16) VGPRs
@@ -136,7 +135,7 @@ laplace_fwd2_kernel(const T* __restrict__ queryIn, const T* __restrict__ key,
   int x = blockIdx.x, nx = gridDim.x, bh = blockIdx.y, N = NIn, si = -1;
   const T* query = queryIn;
   O* out = outIn;
-  if (sg.count > 0) {
+  if constexpr (SEG) {
     const int L = x + nx * bh, S = (int)gridDim.y;
     const int e1 = S * sg.nx[0], e2 = e1 + S * sg.nx[1];
     si = L < e1 ? 0 : (L < e2 ? 1 : 2);
@@ -148,7 +147,7 @@ laplace_fwd2_kernel(const T* __restrict__ queryIn, const T* __restrict__ key,
     query = static_cast<const T*>(si == 0 ? sg.q[0] : si == 1 ? sg.q[1] : sg.q[2]);
     out = static_cast<O*>(si == 0 ? sg.o[0] : si == 1 ? sg.o[1] : sg.o[2]);
   }
-  const int sfull = si < 0 ? sched.full : si == 0 ? sg.sched[0].full : si == 1 ? sg.sched[1].full : sg.sched[2].full;
+  const int sfull = !SEG ? sched.full : si == 0 ? sg.sched[0].full : si == 1 ? sg.sched[1].full : sg.sched[2].full;
   const int P0 = (int)((int64_t)x * N / nx), P1 = (int)((int64_t)(x + 1) * N / nx);
   const int n = P1 - P0;
   const int QP = C + 4;
@@ -201,7 +200,7 @@ laplace_fwd2_kernel(const T* __restrict__ queryIn, const T* __restrict__ key,
 
   const unsigned kBase = (unsigned)(uintptr_t)ktile, qBase = (unsigned)(uintptr_t)qtile;
   const uint32_t me = wave >= 16 ? 0u
-                      : si < 0  ? sched.w[wave]
+                      : !SEG    ? sched.w[wave]
                       : si == 0 ? sg.sched[0].w[wave]
                       : si == 1 ? sg.sched[1].w[wave]
                                 : sg.sched[2].w[wave];
@@ -277,6 +276,21 @@ laplace_fwd2_kernel(const T* __restrict__ queryIn, const T* __restrict__ key,
     done = nv * 2;
   }
   for (int t = done + tid; t < total; t += THREADS) dst[t] = otile[t];
+}
+
+// The plain kernel (one row source) and the segmented one (up to three sources
+// sharing the key, F2Seg); both run fwd2_body.
+template <typename T, int EPI, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, 1)
+laplace_fwd2_kernel(const T* __restrict__ query, const T* __restrict__ key, typename F2Out<T, EPI>::type* __restrict__ out,
+                    int N, int C, float scale, F2Sched sched) {
+  fwd2_body<T, EPI, WAVES, false>(query, key, out, N, C, scale, sched, F2Seg{});
+}
+
+template <typename T, int EPI, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, 1)
+laplace_fwd2_seg_kernel(const T* __restrict__ key, int C, float scale, F2Seg sg) {
+  fwd2_body<T, EPI, WAVES, true>(nullptr, key, nullptr, 0, C, scale, sg.sched[0], sg);
 }
 
 struct F2Plan {
@@ -434,23 +448,31 @@ F2Plan plan_f2(int64_t BH, int64_t N, int64_t C, size_t outBytes) {
   return p;
 }
 
-template <typename T, int EPI, int WAVES>
+template <typename T, int EPI, int WAVES, bool SEG>
 int launch_f2_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C, float scale,
                 const F2Plan& p, hipStream_t st, const F2Seg& sg) {
   using O = typename F2Out<T, EPI>::type;
-  auto kern = laplace_fwd2_kernel<T, EPI, WAVES>;
-  if (p.lds > 65536)
-    if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
-  hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(q),
-                     static_cast<const T*>(k), static_cast<O*>(o), (int)N, (int)C, scale, p.sched, sg);
+  if constexpr (SEG) {
+    auto kern = laplace_fwd2_seg_kernel<T, EPI, WAVES>;
+    if (p.lds > 65536)
+      if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
+    hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(k),
+                       (int)C, scale, sg);
+  } else {
+    auto kern = laplace_fwd2_kernel<T, EPI, WAVES>;
+    if (p.lds > 65536)
+      if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
+    hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(q),
+                       static_cast<const T*>(k), static_cast<O*>(o), (int)N, (int)C, scale, p.sched);
+  }
   return check_launch("laplace forward (row-staged)");
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool SEG = false>
 int launch_f2_t(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t C, float scale,
                 const F2Plan& p, hipStream_t st, const F2Seg& sg = F2Seg{}) {
-  if (p.waves == 16) return launch_f2_w<T, EPI, 16>(q, k, o, BH, N, C, scale, p, st, sg);
-  return launch_f2_w<T, EPI, 8>(q, k, o, BH, N, C, scale, p, st, sg);
+  if (p.waves == 16) return launch_f2_w<T, EPI, 16, SEG>(q, k, o, BH, N, C, scale, p, st, sg);
+  return launch_f2_w<T, EPI, 8, SEG>(q, k, o, BH, N, C, scale, p, st, sg);
 }
 
 // ---------------------------------------------------------------------------
@@ -678,9 +700,9 @@ int f2_launch_multi(int dtype, int nsrc, const void* const* q, const int64_t* n,
     sg.sched[i] = pi.sched;
   }
   if (p.lds > (size_t)max_lds_bytes()) return fail(LFAMD_ERR_UNSUPPORTED, "laplace forward: LDS plan too large");
-  if (dtype == LFAMD_F32) return launch_f2_t<float, kF2Exp>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
-  if (dtype == LFAMD_F16) return launch_f2_t<f16s, kF2Exp>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
-  return launch_f2_t<bf16s, kF2Exp>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
+  if (dtype == LFAMD_F32) return launch_f2_t<float, kF2Exp, true>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
+  if (dtype == LFAMD_F16) return launch_f2_t<f16s, kF2Exp, true>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
+  return launch_f2_t<bf16s, kF2Exp, true>(nullptr, k, nullptr, BH, 0, C, scale, p, st, sg);
 }
 
 }  // namespace lfamd
