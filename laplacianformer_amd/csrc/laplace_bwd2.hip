@@ -220,11 +220,11 @@ struct B2Seg {
   void* dq[3];
 };
 
-template <typename T, int M, bool DQ, bool DK, bool GK = false, bool SEG = false>
-__global__ void __launch_bounds__(64 * b2_waves(M), 1)
-laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gkIn, const float* __restrict__ kvIn,
-                    float gscale, const T* __restrict__ queryIn, const T* __restrict__ key, T* __restrict__ dqIn,
-                    float* __restrict__ partial, T* __restrict__ dkOut, int NIn, int C, B2Seg sg) {
+template <typename T, int M, bool DQ, bool DK, bool GK, bool SEG>
+__device__ __forceinline__ void bwd2_body(const T* __restrict__ gout, const float* __restrict__ gkIn,
+                                          const float* __restrict__ kvIn, float gscale, const T* __restrict__ queryIn,
+                                          const T* __restrict__ key, T* __restrict__ dqIn, float* __restrict__ partial,
+                                          T* __restrict__ dkOut, int NIn, int C, const B2Seg& sg) {
   constexpr int WAVES = b2_waves(M), THREADS = 64 * WAVES;
   constexpr B2Shape S{M, WAVES};
   constexpr int JC = S.JC, HP = S.HP, PITCH = S.PITCH, NKK = S.NKK;
@@ -460,6 +460,23 @@ laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gkIn, 
   }
 }
 
+// The plain kernel (one row source) and the segmented one (up to three sources
+// sharing the key, B2Seg; fused-kernel gradient, dq and dk); both run bwd2_body.
+template <typename T, int M, bool DQ, bool DK, bool GK = false>
+__global__ void __launch_bounds__(64 * b2_waves(M), 1)
+laplace_bwd2_kernel(const T* __restrict__ gout, const float* __restrict__ gk, const float* __restrict__ kv,
+                    float gscale, const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ dq,
+                    float* __restrict__ partial, T* __restrict__ dkOut, int N, int C) {
+  bwd2_body<T, M, DQ, DK, GK, false>(gout, gk, kv, gscale, query, key, dq, partial, dkOut, N, C, B2Seg{});
+}
+
+template <typename T, int M>
+__global__ void __launch_bounds__(64 * b2_waves(M), 1)
+laplace_bwd2_seg_kernel(const T* __restrict__ key, float* __restrict__ partial, int C, float gscale, B2Seg sg) {
+  bwd2_body<T, M, true, true, true, true>(nullptr, nullptr, nullptr, gscale, nullptr, key, nullptr, partial, nullptr,
+                                          0, C, sg);
+}
+
 // grad_key[c][j] = sum over the slice's nx workgroup partials (workgroup order),
 // rounded once. Partials and grad_key are both channel-major [C][M], so reads
 // and writes are contiguous.
@@ -516,22 +533,18 @@ int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk,
   T* dkOut = DK && p.nx == 1 && sg.count == 0 ? static_cast<T*>(dk) : nullptr;
   if (kg.gk && sg.count > 0) {
     if constexpr (M == 49 && DQ && DK)
-      hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true, true>), grid, dim3(64 * b2_waves(M)), p.lds, st,
-                         static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                         static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N,
-                         (int)C, sg);
+      hipLaunchKernelGGL((laplace_bwd2_seg_kernel<T, M>), grid, dim3(64 * b2_waves(M)), p.lds, st,
+                         static_cast<const T*>(k), static_cast<float*>(ws), (int)C, kg.scale, sg);
     else
       return fail(LFAMD_ERR_UNSUPPORTED, "laplace backward: several sources need M = 49 with dq and dk");
   } else if (kg.gk)
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, true>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C,
-                       sg);
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
   else
     hipLaunchKernelGGL((laplace_bwd2_kernel<T, M, DQ, DK, false>), grid, dim3(64 * b2_waves(M)), p.lds, st,
                        static_cast<const T*>(g), kg.gk, kg.kv, kg.scale, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C,
-                       sg);
+                       static_cast<const T*>(k), static_cast<T*>(dq), static_cast<float*>(ws), dkOut, (int)N, (int)C);
   int s = check_launch("laplace backward (column-split)");
   if (s || !DK || dkOut) return s;
   dim3 rgrid((64 * M + 255) / 256, p.ncb, (unsigned)BH);
