@@ -167,11 +167,13 @@ int lfamd_laplace_kernel_forward_multi(int dtype, int num_sources, const void* c
  * M = 49, C % 64 == 0, 4-byte aligned queries; LFAMD_ERR_UNSUPPORTED elsewhere
  * (callers then make one call per source). The workspace is
  * lfamd_laplace_kernel_backward_multi_workspace_size bytes (0 when the path does
- * not apply). No reference counterpart: for callers with several kernel
+ * not apply to that dtype and shape, e.g. any dtype but LFAMD_F16, or a source
+ * of more than INT32_MAX / 2 rows). No reference counterpart: for callers with several kernel
  * matrices against one landmark key (the LaplacianFormer layer's K_qm, K_km
  * and K_mm), whose grad_key parts are summed anyway. */
-size_t lfamd_laplace_kernel_backward_multi_workspace_size(int num_sources, const int64_t* q_lens, int64_t batch,
-                                                          int64_t heads, int64_t k_len, int64_t channels);
+size_t lfamd_laplace_kernel_backward_multi_workspace_size(int dtype, int num_sources, const int64_t* q_lens,
+                                                          int64_t batch, int64_t heads, int64_t k_len,
+                                                          int64_t channels);
 int lfamd_laplace_kernel_backward_multi(int dtype, int num_sources, const float* const* grad_kernels,
                                         const float* const* kernels, const void* const* queries,
                                         const int64_t* q_lens, const void* key, void* const* grad_queries,

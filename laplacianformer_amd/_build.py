@@ -39,6 +39,10 @@ HIP_FLAGS = [
     "-mcode-object-version=5",
     # Packed fp32 VALU ops are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Inline asm naming a register above what a kernel's launch bounds allow
+    # only draws a warning, and gives a kernel whose workgroup cannot be
+    # dispatched: make it a build error.
+    "-Werror=inline-asm",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -37,7 +37,7 @@ CAPI_PROTOTYPES = [
     ("lfamd_laplace_kernel_forward", _I, [_I, _P, _P, _P] + _DIMS + [ctypes.c_float, _P]),
     ("lfamd_laplace_kernel_backward", _I, [_I, _P, _P, _P, _P, _P, _P] + _DIMS + [ctypes.c_float, _P, _SZ, _P]),
     ("lfamd_laplace_kernel_forward_multi", _I, [_I, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.c_float, _P]),
-    ("lfamd_laplace_kernel_backward_multi_workspace_size", _SZ, [_I, _P, _I64, _I64, _I64, _I64]),
+    ("lfamd_laplace_kernel_backward_multi_workspace_size", _SZ, [_I, _I, _P, _I64, _I64, _I64, _I64]),
     ("lfamd_laplace_kernel_backward_multi", _I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                                   ctypes.c_float, _P, _SZ, _P]),
     ("lfamd_newton_workspace_size", _SZ, [_I, _I64, _I64]),

@@ -103,7 +103,7 @@ def laplacian_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, grid:
     if gh * gw != N or gh % pool or gw % pool:
         raise ValueError(f"token grid {gh}x{gw} does not match N={N} or pool={pool}")
     M = (gh // pool) * (gw // pool)
-    if in_dtype in (torch.float16, torch.bfloat16, torch.float32) and d <= 64 and M <= 64:
+    if q.is_cuda and in_dtype in (torch.float16, torch.bfloat16, torch.float32) and d <= 64 and M <= 64:
         return _AttentionFunction.apply(q, k, v, (gh, gw), pool, iters)
     ct = _acc_type(q.dtype)
     km = _PooledLandmarks.apply(k, grid, pool, ct)

@@ -28,7 +28,9 @@ the schedule and the register map:
 * the loop heads are aligned to 64 bytes (``.p2align 6``): the forward lost
   ~0.1 us when an unrelated change to its kernel moved its loop head;
 * nothing needs software wait states (the compiler does not insert them
-  inside inline asm): there are no DPP, permlane or VALU-written SGPR reads.
+  inside inline asm): there are no DPP, permlane or VALU-written SGPR reads;
+* every block names what it writes besides its operands in its clobber list,
+  SCC included (its loop control compares and branches on it).
 
 The backward arithmetic per (row i, key column j, channel c), with T() the
 order-preserving map of a 16-bit float pattern onto the fp32 values
@@ -344,7 +346,7 @@ def variant(dtype, M, DQ=True, DK=True, top=256):
             "[paddr] \"v\"(paddr)"] + [f"[shf{c}] \"v\"(shf[{c}])" for c in range(4)] +
             [f"[q0_{k}] \"v\"(q0[{k}])" for k in range(UNROLL)])
     clob = ", ".join([f"\"v{v}\"" for v in range(lo, top) if v not in bound] +
-                     [f"\"s{s}\"" for s in range(S, SREG_HI + 1)] + ["\"vcc\"", "\"memory\""])
+                     [f"\"s{s}\"" for s in range(S, SREG_HI + 1)] + ["\"vcc\"", "\"scc\"", "\"memory\""])
     # The block writes the bound inputs: it gets copies of the arrays.
     copies = ("\n  unsigned shf[4] = {shf_[0], shf_[1], shf_[2], shf_[3]};\n  unsigned q0[" + str(UNROLL) + "] = {" +
               ", ".join(f"q0_[{k}]" for k in range(UNROLL)) + "};") if phys else ""
@@ -464,7 +466,7 @@ def fwd_variant(R, top=256, jb=FWD_JB, kp=FWD_KP, prefix="fwd2"):
     asm = "\n".join("      \"" + x + "\\n\"" for x in L)
     outs = ", ".join(f"[a{s_}_{j}] \"=v\"(acc[{s_}][{j}])" for s_ in range(R) for j in range(jb))
     ins = ", ".join(["[iters] \"s\"(iters)", "[ka] \"v\"(ka)"] + [f"[qa{s_}] \"v\"(qa[{s_}])" for s_ in range(R)])
-    clob = ", ".join([f"\"v{v}\"" for v in range(lo, top)] + [f"\"s{SC}\"", "\"memory\""])
+    clob = ", ".join([f"\"v{v}\"" for v in range(lo, top)] + [f"\"s{SC}\"", "\"scc\"", "\"memory\""])
     if top != 256:
         name += f"_v{top}"
     src = f"""

@@ -531,6 +531,10 @@ int launch_b2_m(const void* g, const void* q, const void* k, void* dq, void* dk,
                 int64_t C, const B2Plan& p, hipStream_t st, const B2Grad& kg, const B2Seg& sg = B2Seg{}) {
   dim3 grid(p.nx, p.ncb, (unsigned)BH);
   T* dkOut = DK && p.nx == 1 && sg.count == 0 ? static_cast<T*>(dk) : nullptr;
+  const void* fn = kg.gk && sg.count > 0 ? reinterpret_cast<const void*>(laplace_bwd2_seg_kernel<T, M>)
+                   : kg.gk              ? reinterpret_cast<const void*>(laplace_bwd2_kernel<T, M, DQ, DK, true>)
+                                        : reinterpret_cast<const void*>(laplace_bwd2_kernel<T, M, DQ, DK, false>);
+  if (int s = check_fit(fn, 64 * b2_waves(M), p.lds, "laplace backward (column-split)")) return s;
   if (kg.gk && sg.count > 0) {
     if constexpr (M == 49 && DQ && DK)
       hipLaunchKernelGGL((laplace_bwd2_seg_kernel<T, M>), grid, dim3(64 * b2_waves(M)), p.lds, st,
@@ -619,6 +623,12 @@ B2Plan plan_b2_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C, B2Seg& s
 size_t b2_workspace_elems_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C) {
   B2Seg sg{};
   return plan_b2_multi(nsrc, n, BH, C, sg).partialElems;
+}
+
+int64_t b2_multi_workgroups(int nsrc, const int64_t* n, int64_t BH, int64_t C) {
+  int64_t total = 0;
+  for (int i = 0; i < nsrc; ++i) total += (int64_t)plan_b2(BH, n[i], 49, C).nx;
+  return total * (C / 64) * BH;
 }
 
 int b2_launch_multi(int nsrc, const float* const* gk, const float* const* kv, const void* const* q, void* const* dq,

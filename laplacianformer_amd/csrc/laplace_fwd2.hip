@@ -454,12 +454,14 @@ int launch_f2_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, in
   using O = typename F2Out<T, EPI>::type;
   if constexpr (SEG) {
     auto kern = laplace_fwd2_seg_kernel<T, EPI, WAVES>;
+    if (int s = check_fit(reinterpret_cast<const void*>(kern), 64 * WAVES, p.lds, "laplace forward")) return s;
     if (p.lds > 65536)
       if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
     hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(k),
                        (int)C, scale, sg);
   } else {
     auto kern = laplace_fwd2_kernel<T, EPI, WAVES>;
+    if (int s = check_fit(reinterpret_cast<const void*>(kern), 64 * WAVES, p.lds, "laplace forward")) return s;
     if (p.lds > 65536)
       if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), p.lds, "laplace forward")) return s;
     hipLaunchKernelGGL(kern, dim3(p.nx, (unsigned)BH), dim3(64 * WAVES), p.lds, st, static_cast<const T*>(q),
@@ -587,6 +589,7 @@ template <typename T, int WAVES>
 int launch_f3_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
   auto kern = laplace_fwd3_kernel<T, WAVES>;
   const size_t lds = f3_lds_bytes((int)C);
+  if (int s = check_fit(reinterpret_cast<const void*>(kern), 64 * WAVES, lds, "laplace forward")) return s;
   if (lds > 65536)
     if (int s = set_dyn_lds(reinterpret_cast<const void*>(kern), lds, "laplace forward")) return s;
   const int64_t nx = (N + kF3Rows - 1) / kF3Rows;

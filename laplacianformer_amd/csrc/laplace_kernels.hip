@@ -1964,6 +1964,13 @@ int multi_bwd_check(int dtype, int nsrc, const int64_t* q_lens, const void* cons
   if (dtype != LFAMD_F16 || d.M != 49 || d.C <= 0 || d.C % 64 != 0 || d.BH() < 1 || d.C / 64 > 65535)
     return fail(LFAMD_ERR_UNSUPPORTED, "%s: no single-launch path (dtype %d, M=%lld, C=%lld)", who, dtype,
                 (long long)d.M, (long long)d.C);
+  // The kernel holds row counts and its linear workgroup id in 32-bit ints.
+  for (int i = 0; i < nsrc; ++i)
+    if (q_lens[i] > INT32_MAX / 2)
+      return fail(LFAMD_ERR_UNSUPPORTED, "%s: source %d has %lld rows (at most %d)", who, i, (long long)q_lens[i],
+                  INT32_MAX / 2);
+  if (b2_multi_workgroups(nsrc, q_lens, d.BH(), d.C) > INT32_MAX)
+    return fail(LFAMD_ERR_UNSUPPORTED, "%s: too many workgroups for one launch", who);
   if (queries)
     for (int i = 0; i < nsrc; ++i)
       if (reinterpret_cast<uintptr_t>(queries[i]) & 3)
@@ -1972,11 +1979,12 @@ int multi_bwd_check(int dtype, int nsrc, const int64_t* q_lens, const void* cons
 }
 }  // namespace
 
-size_t lfamd_laplace_kernel_backward_multi_workspace_size(int num_sources, const int64_t* q_lens, int64_t batch,
-                                                          int64_t heads, int64_t k_len, int64_t channels) {
+size_t lfamd_laplace_kernel_backward_multi_workspace_size(int dtype, int num_sources, const int64_t* q_lens,
+                                                          int64_t batch, int64_t heads, int64_t k_len,
+                                                          int64_t channels) {
   const Dims d{batch, heads, 1, k_len, channels};
   if (check_dims(d, "laplace kernel backward (several sources)") ||
-      multi_bwd_check(LFAMD_F16, num_sources, q_lens, nullptr, d, "laplace kernel backward (several sources)"))
+      multi_bwd_check(dtype, num_sources, q_lens, nullptr, d, "laplace kernel backward (several sources)"))
     return 0;
   return b2_workspace_elems_multi(num_sources, q_lens, d.BH(), d.C) * 4;
 }

@@ -21,6 +21,12 @@ int check_launch(const char* what);
 // Max dynamic LDS bytes per workgroup on the current device (cached per device).
 int max_lds_bytes();
 
+// Checks, once per kernel and device (cached), that kernel `fn` fits a
+// workgroup of `threads` threads with `dynLds` bytes of dynamic LDS on one CU:
+// its VGPRs times the waves each SIMD must hold, its LDS and its launch bound.
+// LFAMD_OK, or LFAMD_ERR_HIP with `what` before anything is dispatched.
+int check_fit(const void* fn, unsigned threads, size_t dynLds, const char* what);
+
 // Compute units of the current device (cached per device; 256 if unknown).
 int num_cus();
 
@@ -46,6 +52,8 @@ int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, 
 // sources sharing one key in one launch: per source n[i] rows, gk[i], kv[i],
 // query q[i] (4-byte aligned) and grad_query dq[i]; grad_key dk sums them all.
 size_t b2_workspace_elems_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C);
+// Workgroups of that launch (its linear workgroup id must fit an int).
+int64_t b2_multi_workgroups(int nsrc, const int64_t* n, int64_t BH, int64_t C);
 int b2_launch_multi(int nsrc, const float* const* gk, const float* const* kv, const void* const* q, void* const* dq,
                     const int64_t* n, const void* k, void* dk, void* ws, size_t wsBytes, int64_t BH, int64_t C,
                     float scale, hipStream_t st, const char* who);

@@ -65,6 +65,39 @@ int set_dyn_lds(const void* fn, size_t bytes, const char* what) {
   return LFAMD_OK;
 }
 
+int check_fit(const void* fn, unsigned threads, size_t dynLds, const char* what) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, hipFuncAttributes> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  hipFuncAttributes a{};
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find({fn, dev});
+    if (it != cache.end()) {
+      a = it->second;
+    } else {
+      if (hipFuncGetAttributes(&a, fn) != hipSuccess)
+        return fail(LFAMD_ERR_HIP, "%s: hipFuncGetAttributes failed", what);
+      cache[{fn, dev}] = a;
+    }
+  }
+  // A workgroup of W waves puts ceil(W / 4) of them on each of the CU's four
+  // SIMDs at once, and a SIMD holds 512 VGPRs per lane, allocated in granules
+  // of 8. Inline asm that names registers above what the launch bounds allow
+  // only draws a compiler warning, and a dispatch that cannot fit aborts the
+  // queue (HSA_STATUS_ERROR_INVALID_ISA), so the fit is checked before it.
+  const int waves = (int)((threads + 63) / 64), perSimd = (waves + 3) / 4;
+  const int regs = (a.numRegs + 7) / 8 * 8;
+  if ((int)threads > a.maxThreadsPerBlock || regs * perSimd > 512 ||
+      a.sharedSizeBytes + dynLds > (size_t)max_lds_bytes())
+    return fail(LFAMD_ERR_HIP,
+                "%s: the kernel (%d VGPRs, %zu + %zu bytes of LDS, at most %d threads) does not fit a %u-thread "
+                "workgroup on one CU",
+                what, a.numRegs, (size_t)a.sharedSizeBytes, dynLds, a.maxThreadsPerBlock, threads);
+  return LFAMD_OK;
+}
+
 int num_cus() {
   static std::mutex mu;
   static std::map<int, int> cache;

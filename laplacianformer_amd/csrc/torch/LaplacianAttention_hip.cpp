@@ -98,6 +98,10 @@ at::Tensor tall_t(const at::Tensor& a, const at::Tensor& b) {
 
 void check_layer(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t gh, int64_t gw,
                  int64_t pool) {
+  // Every launch below takes raw device pointers: inputs on the CPU or on two
+  // different GPUs are rejected here, before any of them.
+  TORCH_CHECK(q.is_cuda() && k.device() == q.device() && v.device() == q.device(),
+              "laplacian attention: q, k, v must be on one GPU");
   TORCH_CHECK(q.dim() == 4 && k.sizes() == q.sizes() && v.sizes() == q.sizes(),
               "laplacian attention: q, k, v must be [B,H,N,d] of one shape");
   TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
@@ -149,6 +153,9 @@ std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at
   const at::Tensor& w = saved[10];
   check_layer(q, k, v, gh, gw, pool);
   TORCH_CHECK(g.sizes() == q.sizes(), "laplacian attention backward: grad_output must be [B,H,N,d]");
+  TORCH_CHECK(g.device() == q.device(), "laplacian attention backward: grad_output must be on the inputs' GPU");
+  for (const at::Tensor& t : saved)
+    TORCH_CHECK(t.device() == q.device(), "laplacian attention backward: saved tensors must be on the inputs' GPU");
   const int64_t B = k.size(0), H = k.size(1), dd = k.size(3);
   const double s = 1.0 / std::sqrt((double)dd);
   g = g.contiguous();
@@ -173,7 +180,7 @@ std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at
     const void* qs[3] = {km.data_ptr(), q.data_ptr(), k.data_ptr()};
     void* dqs[3] = {d_km.data_ptr(), d_q.data_ptr(), d_k.data_ptr()};
     const int64_t ns[3] = {km.size(2), q.size(2), k.size(2)};
-    const size_t wsb = lfamd_laplace_kernel_backward_multi_workspace_size(3, ns, B, H, km_cm.size(3), dd);
+    const size_t wsb = lfamd_laplace_kernel_backward_multi_workspace_size(dt, 3, ns, B, H, km_cm.size(3), dd);
     int st = LFAMD_ERR_UNSUPPORTED;
     if (wsb > 0 && d_kqm.is_contiguous() && d_kkm.is_contiguous() && d_kmm.is_contiguous()) {
       at::Tensor ws = at::empty({(int64_t)wsb}, k.options().dtype(at::kByte));

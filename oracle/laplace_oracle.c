@@ -21,11 +21,21 @@
  * Parallel over (bh, row) with OpenMP; each output is still summed serially in
  * the order above, so the result does not depend on the thread count.
  */
+#include <float.h>
+#include <math.h>
 #include <stdint.h>
 
 #define SGN(v) (((v) > 0) - ((v) < 0))
 
-#define DEFINE_ORACLE(T, SUF)                                                          \
+/* The reference is built with nvcc --use_fast_math (setup.py:29), which implies
+ * -ftz=true: single-precision instructions read denormal operands as zero and
+ * flush denormal results to zero (sign kept). The f32ftz entry points restate
+ * that build: every fp32 input and every operation's result passes FTZ. The
+ * plain f32 / f64 entry points are IEEE (fast math does not flush fp64). */
+static inline float ftz_f(float x) { return fabsf(x) < FLT_MIN ? copysignf(0.0f, x) : x; }
+#define ID(x) (x)
+
+#define DEFINE_ORACLE(T, SUF, FZ)                                                      \
   void lf_oracle_forward_##SUF(const T* q, const T* k, T* out, int64_t BH, int64_t N,  \
                                int64_t M, int64_t C) {                                 \
     _Pragma("omp parallel for collapse(2) schedule(static)")                           \
@@ -37,8 +47,8 @@
         for (int64_t j = 0; j < M; ++j) {                                              \
           T acc = 0;                                                                   \
           for (int64_t c = 0; c < C; ++c) {                                            \
-            T d = qi[c] - kb[c * M + j];                                               \
-            acc += d < 0 ? -d : d;                                                     \
+            T d = FZ(FZ(qi[c]) - FZ(kb[c * M + j]));                                   \
+            acc = FZ(acc + (d < 0 ? -d : d));                                          \
           }                                                                            \
           oi[j] = acc;                                                                 \
         }                                                                              \
@@ -55,7 +65,8 @@
         const T* kb = k + b * C * M;                                                   \
         for (int64_t c = 0; c < C; ++c) {                                              \
           T acc = 0;                                                                   \
-          for (int64_t j = 0; j < M; ++j) acc += gi[j] * (T)SGN(qi[c] - kb[c * M + j]); \
+          for (int64_t j = 0; j < M; ++j)                                              \
+            acc = FZ(acc + FZ(gi[j]) * (T)SGN(FZ(FZ(qi[c]) - FZ(kb[c * M + j]))));     \
           dq[(b * N + i) * C + c] = acc;                                               \
         }                                                                              \
       }                                                                                \
@@ -74,13 +85,15 @@
         for (int64_t i = 0; i < N; ++i) {                                              \
           const T qv = q[(b * N + i) * C + c];                                         \
           const T* gi = g + (b * N + i) * M;                                           \
-          for (int64_t j = 0; j < M; ++j) acc[j] -= gi[j] * (T)SGN(qv - kc[j]);        \
+          for (int64_t j = 0; j < M; ++j)                                              \
+            acc[j] = FZ(acc[j] - FZ(gi[j]) * (T)SGN(FZ(FZ(qv) - FZ(kc[j]))));          \
         }                                                                              \
       }                                                                                \
   }
 
-DEFINE_ORACLE(float, f32)
-DEFINE_ORACLE(double, f64)
+DEFINE_ORACLE(float, f32, ID)
+DEFINE_ORACLE(float, f32ftz, ftz_f)
+DEFINE_ORACLE(double, f64, ID)
 
 int lf_oracle_max_threads(void) {
 #ifdef _OPENMP

@@ -43,7 +43,7 @@ def _load():
     if _lib is None:
         build()
         lib = ctypes.CDLL(_LIB_PATH)
-        for suf in ("f32", "f64"):
+        for suf in ("f32", "f32ftz", "f64"):
             for name, nptr in (("forward", 3), ("backward_query", 4), ("backward_key", 4)):
                 fn = getattr(lib, f"lf_oracle_{name}_{suf}")
                 fn.argtypes = [ctypes.c_void_p] * nptr + [ctypes.c_int64] * 4
@@ -94,9 +94,9 @@ def round_to(acc: np.ndarray, dtype: str):
     raise ValueError(dtype)
 
 
-def _call(name, dtype, arrays, out_shape, dims):
+def _call(name, dtype, arrays, out_shape, dims, ftz=False):
     lib = _load()
-    suf = "f64" if dtype == "f64" else "f32"
+    suf = "f64" if dtype == "f64" else ("f32ftz" if ftz else "f32")
     arrs = [widen(a, dtype) for a in arrays]
     out = np.empty(out_shape, dtype=arrs[0].dtype)
     getattr(lib, f"lf_oracle_{name}_{suf}")(*[a.ctypes.data for a in arrs], out.ctypes.data, *dims)
@@ -106,34 +106,38 @@ def _call(name, dtype, arrays, out_shape, dims):
 # ---------------------------------------------------------------------------
 # LaplaceSubtraction
 # ---------------------------------------------------------------------------
-def laplace_forward(q, k, dtype: str = "f32") -> np.ndarray:
+def laplace_forward(q, k, dtype: str = "f32", ftz: bool = False) -> np.ndarray:
     """out[b,h,i,j] = sum_c |q[b,h,i,c] - k[b,h,c,j]|, c ascending, fp32 accumulator.
 
     Reference src/LaplaceSubtraction_cuda_kernel.cu:84-125 (loop order), :137 (store).
+    ``ftz``: the reference's fast-math build (setup.py:29: fp32 denormal operands and
+    results flushed to zero); fp32 accumulation only.
     """
     B, H, N, C = q.shape
     M = k.shape[3]
-    return _call("forward", dtype, [q, k], (B, H, N, M), (B * H, N, M, C))
+    return _call("forward", dtype, [q, k], (B, H, N, M), (B * H, N, M, C), ftz)
 
 
-def laplace_backward_query(g, q, k, dtype: str = "f32") -> np.ndarray:
+def laplace_backward_query(g, q, k, dtype: str = "f32", ftz: bool = False) -> np.ndarray:
     """dq[b,h,i,c] = sum_j g[b,h,i,j] * sgn(q[b,h,i,c] - k[b,h,c,j]), j ascending.
 
     Reference src/LaplaceSubtraction_cuda_kernel.cu:206-249 (unsplit order), sgn :34-38.
+    ``ftz`` as in laplace_forward.
     """
     B, H, N, C = q.shape
     M = k.shape[3]
-    return _call("backward_query", dtype, [g, q, k], (B, H, N, C), (B * H, N, M, C))
+    return _call("backward_query", dtype, [g, q, k], (B, H, N, C), (B * H, N, M, C), ftz)
 
 
-def laplace_backward_key(g, q, k, dtype: str = "f32") -> np.ndarray:
+def laplace_backward_key(g, q, k, dtype: str = "f32", ftz: bool = False) -> np.ndarray:
     """dk[b,h,c,j] = -sum_i g[b,h,i,j] * sgn(q[b,h,i,c] - k[b,h,c,j]), i ascending.
 
     Reference src/LaplaceSubtraction_cuda_kernel.cu:332-375 (unsplit order).
+    ``ftz`` as in laplace_forward.
     """
     B, H, N, C = q.shape
     M = k.shape[3]
-    return _call("backward_key", dtype, [g, q, k], (B, H, C, M), (B * H, N, M, C))
+    return _call("backward_key", dtype, [g, q, k], (B, H, C, M), (B * H, N, M, C), ftz)
 
 
 def _native(x, dtype):

@@ -61,6 +61,13 @@ def test_no_cpu_fallback_in_functional():
         lf.laplace_subtraction(q, k)
     with pytest.raises(RuntimeError, match="mat must be on GPU"):
         lf.newton_inverse(torch.randn(1, 1, 4, 4), 3)
+    # The attention layer: CPU inputs take the per-op composition, whose first distance
+    # raises; the single-node entry rejects them before any launch.
+    x = torch.randn(1, 1, 64, 16)
+    with pytest.raises(RuntimeError, match="Not implemented on the CPU"):
+        lf.laplacian_attention(x, x, x, grid=(8, 8), pool=4)
+    with pytest.raises(RuntimeError, match="one GPU"):
+        lf.ext().LaplacianAttention_forward(x, x, x, 8, 8, 4, 10)
 
 
 def test_product_never_imports_the_oracle():

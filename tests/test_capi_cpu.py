@@ -95,3 +95,21 @@ def test_argument_errors_without_device(lib):
     assert kb(1, null, null, null, null, null, null, 1, 1, 8, 49, 64, 0.5, null, 0, null) == 0  # nothing asked
     assert lib.lfamd_laplace_backward_workspace_size(1, 32, 1, 3136, 49, 64) > 0
     assert lib.lfamd_laplace_backward_workspace_size(1, 0, 1, 3136, 49, 64) == 0
+
+
+def test_multi_backward_bounds_without_device(lib):
+    """The segmented fused-kernel backward keeps row counts and its linear workgroup id in
+    32-bit ints: a source longer than INT32_MAX / 2 rows, or a dtype the path does not take,
+    gives no workspace size and an LFAMD_ERR_UNSUPPORTED call, before any device query."""
+    n = (ctypes.c_int64 * 3)(49, 2 ** 31, 784)
+    ws = lib.lfamd_laplace_kernel_backward_multi_workspace_size
+    assert ws(1, 3, n, 64, 2, 49, 64) == 0
+    assert ws(1, 3, (ctypes.c_int64 * 3)(49, 2 ** 30, 784), 64, 2, 49, 64) == 0
+    assert ws(0, 1, (ctypes.c_int64 * 1)(784), 64, 2, 49, 64) == 0   # fp32: the path is fp16 only
+    assert ws(2, 1, (ctypes.c_int64 * 1)(784), 64, 2, 49, 64) == 0   # bf16
+    dummy = ctypes.c_void_p(16)
+    ptrs = (ctypes.c_void_p * 3)(16, 16, 16)
+    st = lib.lfamd_laplace_kernel_backward_multi(1, 3, ptrs, ptrs, ptrs, n, dummy, ptrs, dummy, 64, 2, 49, 64,
+                                                 ctypes.c_float(0.125), dummy, 1 << 20, ctypes.c_void_p(0))
+    assert st == 3
+    assert b"rows" in lib.lfamd_last_error()

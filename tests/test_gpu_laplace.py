@@ -231,6 +231,47 @@ def test_laplace_nonfinite_backward(gpu, dt, M):
     assert_l1_close(dk, refs["dk"][0], dt, f"{dt} dk non-finite", refs["dk"][1])
 
 
+# fp32 denormals (pinned, IEEE): every fp32 kernel keeps denormal operands and results, so a
+# query/key pair whose difference is an fp32 denormal has sgn +-1 and adds that exact
+# difference to the forward sum, as IEEE arithmetic and the fp32 oracle give. The
+# reference's fast-math build (setup.py:29, -ftz) flushes them and gives sgn 0 and no
+# contribution: the oracle's ftz mode restates that build, and the test checks that
+# ours departs from it exactly at those pairs (by sum_j g over them in grad_query).
+@pytest.mark.parametrize("M,C", [(49, 64), (64, 64), (5, 3)], ids=["m49", "m64", "m5c3"])
+def test_laplace_f32_denormal_differences(gpu, M, C):
+    import laplacianformer_amd as lf
+
+    B, H, N = 1, 2, 64
+    print(f"laplace fp32 denormal differences M={M} C={C}", flush=True)
+    q, k, g = _inputs(B, H, N, M, C, "f32", seed=95)
+    a, b = np.float32(1.5e-38), np.float32(1.2e-38)          # a - b is an exact fp32 denormal
+    q[..., :, 0] = float(a)
+    k[..., 0, 0::2] = float(b)                                # even columns: denormal difference
+    k[..., 0, 1::4] = float(a)                                # ties
+    q[..., 0:N:3, C - 1] = 1e-40                              # denormal query values
+    k[..., C - 1, 0:M:3] = 0.0
+    L = lf.ext()
+    qd, kd, gd = q.to(gpu), k.to(gpu), g.to(gpu)
+    out = torch.empty((B, H, N, M), device=gpu)
+    dq, dk = torch.empty_like(qd), torch.empty_like(kd)
+    L.LaplaceSubtraction_forward(qd, kd, out)
+    L.LaplaceSubtraction_backward(gd, qd, kd, dq, dk)
+    dq1, dk1 = torch.empty_like(qd), torch.empty_like(kd)
+    L.LaplaceSubtraction_backward_query(gd, qd, kd, dq1)
+    L.LaplaceSubtraction_backward_key(gd, qd, kd, dk1)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.laplace_forward(q, k, "f32"), "f32", "forward (IEEE, denormals kept)")
+    refs = l1_refs(q, k, g, "f32")
+    for got, key in ((dq, "dq"), (dk, "dk"), (dq1, "dq"), (dk1, "dk")):
+        assert_l1_close(got, refs[key][0], "f32", f"{key} (IEEE signs of denormal differences)", refs[key][1])
+    # Where the flushing build differs: channel 0 of every row loses sum over the even
+    # columns of g (sgn +1 there, 0 when flushed).
+    rq_z = oracle.laplace_backward_query(g, q, k, "f32", ftz=True)
+    gap = (dq.cpu().double()[..., 0] - torch.from_numpy(rq_z[..., 0]).double())
+    want = g.double()[..., 0::2].sum(-1)
+    assert torch.allclose(gap, want, rtol=1e-5, atol=1e-5 * g.abs().double().sum(-1).max().item())
+
+
 @pytest.mark.parametrize("M", [49, 300])
 def test_laplace_misaligned_grad(gpu, M):
     """fp16 grad_output that is a contiguous view at an odd element offset (its

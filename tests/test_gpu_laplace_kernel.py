@@ -199,7 +199,7 @@ def test_kernel_backward_multi(gpu, lens):
     ns = len(lens)
     nl = (ctypes.c_int64 * ns)(*lens)
     P = lambda ts: (ctypes.c_void_p * ns)(*[t.data_ptr() for t in ts])  # noqa: E731
-    wsb = lib.lfamd_laplace_kernel_backward_multi_workspace_size(ns, nl, B, H, M, C)
+    wsb = lib.lfamd_laplace_kernel_backward_multi_workspace_size(1, ns, nl, B, H, M, C)
     assert wsb > 0
     ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -236,7 +236,8 @@ def test_kernel_backward_multi_rejects(gpu):
     assert call(1, 1, 48, 64) == 3                               # M != 49 (LFAMD_ERR_UNSUPPORTED)
     assert call(2, 1, 49, 64) == 3 and call(1, 1, 49, 40) == 3   # bf16; C % 64 != 0
     assert call(1, 1, 49, 64) == 1                               # no workspace
-    assert lib.lfamd_laplace_kernel_backward_multi_workspace_size(1, one, 1, 1, 48, 64) == 0
+    assert lib.lfamd_laplace_kernel_backward_multi_workspace_size(1, 1, one, 1, 1, 48, 64) == 0
+    assert lib.lfamd_laplace_kernel_backward_multi_workspace_size(2, 1, one, 1, 1, 49, 64) == 0  # bf16
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])

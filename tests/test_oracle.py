@@ -142,6 +142,37 @@ def test_laplace_invariants():
     assert np.array_equal(dq.sum(axis=2) + dk.sum(axis=3), np.zeros((1, 2, 8)))
 
 
+def test_laplace_ftz_mode_known_answers():
+    """The f32ftz restatement of the reference's fast-math build (setup.py:29, -ftz=true):
+    hand-computed cases. Sterbenz: 1.5e-38 - 1.2e-38 is exact in fp32, a denormal, so the
+    IEEE oracle keeps it (sgn +1, forward = the difference) and the flushing one gives 0;
+    a denormal operand (1e-40) counts as 0 only in the flushing one; normal values agree."""
+    f = np.float32
+    a, b, tiny = f(1.5e-38), f(1.2e-38), f(1e-40)
+    assert 0 < a - b < np.finfo(np.float32).tiny and tiny < np.finfo(np.float32).tiny
+    q = np.array([[[[a, tiny, f(2.0)]]]], dtype=np.float32)          # [1,1,1,3]
+    k = np.array([[[[b, a], [f(0.0), f(0.0)], [f(1.0), f(3.0)]]]], dtype=np.float32)  # [1,1,3,2]
+    g = np.array([[[[f(1.0), f(1.0)]]]], dtype=np.float32)
+    fwd = oracle.laplace_forward(q, k, "f32")
+    fwd_z = oracle.laplace_forward(q, k, "f32", ftz=True)
+    # column 0: |a-b| + |tiny| + 1; column 1: 0 + |tiny| + 1
+    assert fwd[0, 0, 0, 0] == f(f(f(a - b) + tiny) + f(1.0)) and fwd_z[0, 0, 0, 0] == f(1.0)
+    assert fwd_z[0, 0, 0, 1] == f(1.0)
+    dq = oracle.laplace_backward_query(g, q, k, "f32")[0, 0, 0]
+    dq_z = oracle.laplace_backward_query(g, q, k, "f32", ftz=True)[0, 0, 0]
+    assert dq.tolist() == [1.0, 2.0, 0.0] and dq_z.tolist() == [0.0, 0.0, 0.0]
+    dk = oracle.laplace_backward_key(g, q, k, "f32")[0, 0]
+    dk_z = oracle.laplace_backward_key(g, q, k, "f32", ftz=True)[0, 0]
+    assert dk.tolist() == [[-1.0, 0.0], [-1.0, -1.0], [-1.0, 1.0]]
+    assert dk_z.tolist() == [[0.0, 0.0], [0.0, 0.0], [-1.0, 1.0]]
+    # Away from the denormal range both modes are the same function.
+    qn, kn, gn = (np.random.default_rng(5).standard_normal(s).astype(np.float32)
+                  for s in ((1, 2, 7, 5), (1, 2, 5, 4), (1, 2, 7, 4)))
+    assert np.array_equal(oracle.laplace_forward(qn, kn, "f32"), oracle.laplace_forward(qn, kn, "f32", ftz=True))
+    assert np.array_equal(oracle.laplace_backward_key(gn, qn, kn, "f32"),
+                          oracle.laplace_backward_key(gn, qn, kn, "f32", ftz=True))
+
+
 def test_round_to():
     x = np.array([1.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 65504.0, 1e-8], dtype=np.float64)
     assert oracle.round_to(x, "f16").tolist() == [1.0, 1.0, 1.0 + 2 ** -9, 65504.0, 0.0]
