@@ -389,12 +389,14 @@ bool f2_schedule16(int F, bool tail, int maxR, F2Sched& out) {
     out.w[w] = (uint32_t)r.b | (uint32_t)r.s0 << 3 | (uint32_t)r.R << 6 | (r.tail ? 1u << 9 : 0u);
     slotOf[nslots++] = w;
   }
-  if (tail && bestTailMode == 1) {  // attach to the least loaded SIMD's shortest run of <= 2
+  if (tail && bestTailMode == 1) {
+    // Attach to the oldest wave (lowest index) of the least loaded SIMD: a SIMD
+    // issues its oldest ready waves first, so its youngest wave runs last and
+    // partly alone, and should hold the least work.
     int bw = -1, bl = 1 << 30;
     for (int i = 0; i < nslots; ++i) {
       const int w = slotOf[i];
-      const int R = (out.w[w] >> 6) & 7;
-      if (R <= 2 && load[w % 4] < bl) {
+      if (load[w % 4] < bl || (load[w % 4] == bl && w < bw)) {
         bl = load[w % 4];
         bw = w;
       }

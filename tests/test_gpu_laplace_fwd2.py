@@ -2,10 +2,10 @@
 
 Each shape is chosen (for 256 CUs) to reach one plan of the kernel: 16 waves with
 runs of 1-3 row sets and a tail wave, 16 waves with workgroups one row apart (the
-tail length differs between them), and 8 waves with 7-set runs (full and partial
-last set). The distance must be bit-identical to the fp32 serial oracle (the
-kernel sums the channels in the reference's order); the fused exp(-s * distance)
-variant is held to the fp32 rounding of s * d and expf.
+tail length differs between them, 0 to 9 rows), and 8 waves with 7-set runs (full
+and partial last set), at C from 8 to 64. The distance must be bit-identical to the
+fp32 serial oracle (the kernel sums the channels in the reference's order); the
+fused exp(-s * distance) variant is held to the fp32 rounding of s * d and expf.
 """
 import math
 
@@ -27,6 +27,9 @@ SHAPES = [
     (32, 1, 3141, 49, 64, "16 waves, 6 sets + 8/9-row tails (workgroups one row apart)"),
     (1, 8, 13440, 49, 40, "8 waves, 7 sets (last partial)"),
     (1, 8, 14336, 49, 8, "8 waves, 7 full sets"),
+    (32, 1, 3073, 49, 64, "16 waves, 6 sets + 0/1-row tails"),
+    (8, 5, 1200, 49, 16, "16 waves, 3 sets + 8-row tail, C = 16"),
+    (1, 256, 420, 49, 64, "one workgroup per slice, 7 sets (last partial)"),
 ]
 
 
