@@ -316,7 +316,7 @@ def bench_small_d(args, dev):
     gbs = nbytes / (t["median"] * 1e-3) / 1e9
     return {"workload": "LaplaceSubtraction forward B=16 H=8 N=4096 M=256 d=8 bf16 (output-write-bound)",
             "ms": t, "bytes": nbytes, "gb_per_s": gbs, "frac_hbm_peak": gbs / PEAK_HBM_GBS,
-            "kernel": "laplace_fwd3_kernel<bf16s> (16-byte stores from registers)"}
+            "kernel": "laplace_fwd4_kernel<bf16s, 8, 4> (whole-line stores from registers)"}
 
 
 def reference_figure(args, dev):

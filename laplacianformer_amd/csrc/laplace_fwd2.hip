@@ -587,6 +587,104 @@ laplace_fwd3_kernel(const T* __restrict__ query, const T* __restrict__ key, T* _
   }
 }
 
+// Small channel counts (C in {8, 16}) with M = 64 MG landmarks, where the
+// output (2 bytes per (i, j) against 2 C VALU instructions) bounds the time:
+// every store instruction writes whole 128-byte lines. Lane (rsub, chunk) =
+// (lane / 16, lane % 16) computes 4 consecutive columns [4 chunk, 4 chunk + 4)
+// of a 64-column group for row rsub of each 4-row step, so the 16 lanes of a
+// row write 64 consecutive outputs (one line of 16-bit outputs, two of fp32).
+// Wave w of the 4-wave workgroup takes column group w % MG and, for MG = 2, one
+// half of the workgroup's rows; each lane keeps its columns' keys for all C
+// channels in registers (from the workgroup's fp32 key tile) and reads the query
+// row of each step as a broadcast from the fp32 query tile. Sums over c
+// ascending in fp32: the reference's order, bit-identical to the serial oracle.
+constexpr int kF4Rows = 256;   // rows per workgroup
+
+// Two fp32 values rounded to nearest even into one word of 16-bit outputs, as
+// one v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 (the same rounding as from_acc; a
+// NaN comes out as a quiet NaN of its own sign where from_acc writes 0x7fc0 for
+// bf16).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<f16s>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack2<bf16s>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+template <typename T, int C, int MG>
+__global__ void __launch_bounds__(256)
+laplace_fwd4_kernel(const T* __restrict__ query, const T* __restrict__ key, T* __restrict__ out, int N) {
+  constexpr int M = 64 * MG, QP = C + 4, WPG = 4 / MG, RPW = kF4Rows / WPG;
+  __shared__ __align__(16) float qs[kF4Rows * QP];
+  __shared__ __align__(16) float ks[C * M];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int cg = wave % MG, rw = wave / MG, chunk = lane & 15, rsub = lane >> 4;
+  const int bh = blockIdx.y, r0 = blockIdx.x * kF4Rows;
+  const T* qsl = query + (size_t)bh * N * C;
+#pragma unroll
+  for (int i = 0; i < kF4Rows * C / 256; ++i) {
+    const int e = tid + 256 * i, r = e / C, c = e - r * C;
+    qs[r * QP + c] = to_acc(qsl[(size_t)min(r0 + r, N - 1) * C + c]);
+  }
+#pragma unroll
+  for (int i = 0; i < C * M / 256; ++i) ks[tid + 256 * i] = to_acc(key[(size_t)bh * C * M + tid + 256 * i]);
+  __syncthreads();
+  float kr[C][4];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const float4 v = *reinterpret_cast<const float4*>(ks + c * M + cg * 64 + 4 * chunk);
+    kr[c][0] = v.x;
+    kr[c][1] = v.y;
+    kr[c][2] = v.z;
+    kr[c][3] = v.w;
+  }
+  T* const o = out + ((size_t)bh * N + r0) * M + cg * 64 + 4 * chunk;
+#pragma unroll 4
+  for (int t = 0; t < RPW / 4; ++t) {
+    const int r = rw * RPW + 4 * t + rsub;
+    float qv[C];
+#pragma unroll
+    for (int c4 = 0; c4 < C / 4; ++c4) {
+      const float4 v = *reinterpret_cast<const float4*>(qs + r * QP + 4 * c4);
+      qv[4 * c4] = v.x;
+      qv[4 * c4 + 1] = v.y;
+      qv[4 * c4 + 2] = v.z;
+      qv[4 * c4 + 3] = v.w;
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += __builtin_fabsf(qv[c] - kr[c][j]);
+    if (r0 + r < N) {
+      if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(o + (size_t)r * M) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      } else {
+        *reinterpret_cast<uint2*>(o + (size_t)r * M) = make_uint2(pack2<T>(acc[0], acc[1]), pack2<T>(acc[2], acc[3]));
+      }
+    }
+  }
+}
+
+template <typename T, int C, int MG>
+int launch_f4(const void* q, const void* k, void* o, int64_t BH, int64_t N, hipStream_t st) {
+  auto kern = laplace_fwd4_kernel<T, C, MG>;
+  if (int s = check_fit(reinterpret_cast<const void*>(kern), 256, 0, "laplace forward (small d)")) return s;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((N + kF4Rows - 1) / kF4Rows), (unsigned)BH), dim3(256), 0, st,
+                     static_cast<const T*>(q), static_cast<const T*>(k), static_cast<T*>(o), (int)N);
+  return check_launch("laplace forward (small d)");
+}
+
+template <typename T>
+int launch_f4_t(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
+  if (C == 8) return M == 256 ? launch_f4<T, 8, 4>(q, k, o, BH, N, st) : launch_f4<T, 8, 2>(q, k, o, BH, N, st);
+  return M == 256 ? launch_f4<T, 16, 4>(q, k, o, BH, N, st) : launch_f4<T, 16, 2>(q, k, o, BH, N, st);
+}
+
 template <typename T, int WAVES>
 int launch_f3_w(const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C, hipStream_t st) {
   auto kern = laplace_fwd3_kernel<T, WAVES>;
@@ -629,6 +727,11 @@ bool f3_ok(int dtype, int64_t BH, int64_t N, int64_t M, int64_t C, const void* q
 
 int f3_launch(int dtype, const void* q, const void* k, void* o, int64_t BH, int64_t N, int64_t M, int64_t C,
               hipStream_t st) {
+  if (C == 8 || C == 16) {  // output-bound: the line-coalesced small-d kernel
+    if (dtype == LFAMD_F32) return launch_f4_t<float>(q, k, o, BH, N, M, C, st);
+    if (dtype == LFAMD_F16) return launch_f4_t<f16s>(q, k, o, BH, N, M, C, st);
+    return launch_f4_t<bf16s>(q, k, o, BH, N, M, C, st);
+  }
   if (dtype == LFAMD_F32) return launch_f3<float>(q, k, o, BH, N, M, C, st);
   if (dtype == LFAMD_F16) return launch_f3<f16s>(q, k, o, BH, N, M, C, st);
   return launch_f3<bf16s>(q, k, o, BH, N, M, C, st);

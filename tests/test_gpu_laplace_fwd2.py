@@ -54,7 +54,9 @@ def test_fwd2_plans(gpu, shape, dt):
 
 
 # The wide-landmark forward (M in {128, 256}): whole and partial 192-row
-# workgroups, one-row slices, C = 8 to 64, the config-4 shape on two slices.
+# workgroups, one-row slices, C = 8 to 64, the config-4 shape on two slices; for
+# C in {8, 16} the line-coalesced small-d kernel (whole and partial 256-row
+# workgroups, both landmark counts, the small-d benchmark shape on two slices).
 WIDE = [
     (1, 2, 700, 128, 64),
     (2, 1, 192, 256, 64),
@@ -63,6 +65,9 @@ WIDE = [
     (1, 2, 4096, 256, 64),
     (2, 3, 500, 128, 16),
     (1, 4, 1000, 256, 8),
+    (1, 2, 4096, 256, 8),
+    (3, 1, 700, 128, 8),
+    (1, 2, 513, 256, 16),
 ]
 
 
