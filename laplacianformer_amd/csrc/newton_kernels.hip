@@ -51,7 +51,11 @@ template <int NP, int WPR = 1> struct NsLayout {
 // for four steps (lanes of one lk group on distinct 16-byte bank groups), a
 // row-major B operand and a transposed A operand one 4-byte read per step on
 // 64 distinct banks (the step-order k = k0 + lk puts 4 lanes on one bank).
-template <int NP, int WPR, bool TRANS_X, bool TRANS_Y>
+//
+// KL < 4: the inner dimension n has n - (NP - 16) = KL < 4 live k in the last
+// block (n = 16 m + KL); there the MFMA steps s >= KL, whose four k are all
+// zero padding, are left out (every skipped term is 0 * 0).
+template <int NP, int WPR, bool TRANS_X, bool TRANS_Y, int KL = 4>
 __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, const float* __restrict__ Ys,
                                               int wave, int lane, v4f (&acc)[NP / 16 / WPR]) {
   using L = NsLayout<NP, WPR>;
@@ -62,8 +66,13 @@ __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, cons
   const int i = 16 * strip + li;
 #pragma unroll
   for (int t = 0; t < L::TW; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-  for (int k0 = 0; k0 < NP; k0 += 16) {
+  constexpr int KEND = KL < 4 ? NP - 16 : NP;
+  // The wide layouts (4 waves per strip, few matrices per CU) are latency-bound:
+  // with at most 4 k blocks every operand read goes out before the first MFMA.
+  // Elsewhere one block at a time keeps the register count (and occupancy) low.
+  constexpr int kUnroll = WPR == 4 && L::NT <= 4 ? L::NT : 1;
+#pragma unroll kUnroll
+  for (int k0 = 0; k0 < KEND; k0 += 16) {  // (a trimmed last block follows the loop)
     const int kb = k0 + 4 * lk;  // this lane's 4 consecutive k
     float a[4];
     if constexpr (TRANS_X) {
@@ -91,11 +100,29 @@ __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, cons
       for (int t = 0; t < L::TW; ++t)
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
   }
+  if constexpr (KL < 4) {
+    const int kb = KEND + 4 * lk;
+    float a[KL];
+#pragma unroll
+    for (int s = 0; s < KL; ++s) a[s] = TRANS_X ? Xs[(kb + s) * L::LS + i] : Xs[i * L::LS + kb + s];
+    float b[L::TW][KL];
+#pragma unroll
+    for (int t = 0; t < L::TW; ++t) {
+      const int j = 16 * (t0 + t) + li;
+#pragma unroll
+      for (int s = 0; s < KL; ++s) b[t][s] = TRANS_Y ? Ys[j * L::LS + kb + s] : Ys[(kb + s) * L::LS + j];
+    }
+#pragma unroll
+    for (int s = 0; s < KL; ++s)
+#pragma unroll
+      for (int t = 0; t < L::TW; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
+  }
 }
 
 // As mfma_rowstrip with X = P held in registers: pa[b][s] = P[16*strip + lane%16][16b + 4*(lane/16) + s],
 // the row-major A operand of k block b, step s; Y row-major in LDS.
-template <int NP, int WPR>
+template <int NP, int WPR, int KL = 4>
 __device__ __forceinline__ void mfma_rowstrip_areg(const float (&pa)[NP / 16][4], const float* __restrict__ Ys,
                                                    int wave, int lane, v4f (&acc)[NP / 16 / WPR]) {
   using L = NsLayout<NP, WPR>;
@@ -113,9 +140,10 @@ __device__ __forceinline__ void mfma_rowstrip_areg(const float (&pa)[NP / 16][4]
       for (int s = 0; s < 4; ++s) b[t][s] = Ys[(k + s) * L::LS + 16 * (t0 + t) + li];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
+      if (kb + 1 < L::NT || s < KL)  // folded at compile time (kb unrolled)
 #pragma unroll
-      for (int t = 0; t < L::TW; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[kb][s], b[t][s], acc[t], 0, 0, 0);
+        for (int t = 0; t < L::TW; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[kb][s], b[t][s], acc[t], 0, 0, 0);
   }
 }
 
@@ -160,6 +188,22 @@ __device__ __forceinline__ void update_strip(float* __restrict__ Vs, int wave, i
     }
 }
 
+// Sum of x over the four 16-lane rows of the wave, in every lane, as
+// (row 0 + row 1) + (row 2 + row 3). v_permlane16_swap on two copies of x
+// leaves rows (0, 0, 2, 2) in one and (1, 1, 3, 3) in the other, whose sum is
+// each row pair's total; v_permlane32_swap does the same for the halves. The
+// swaps are written as asm on two distinct registers: the builtin, given the
+// same value twice, was folded to one result. s_nop 1 covers the VALU write
+// of an operand just before the swap.
+__device__ __forceinline__ float sum_rows4(float x) {
+  float a = x, b = x;
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  const float y = a + b;
+  float c = y, d = y;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+  return c + d;
+}
+
 // P = f32(mat) + 0.01 I on the live n x n block; zero padding elsewhere when `pad`.
 template <typename T, int NP, int WPR>
 __device__ __forceinline__ void load_P(float* __restrict__ Ps, const T* __restrict__ M, int n, bool pad) {
@@ -180,8 +224,15 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
   const int tid = threadIdx.x;
   float row = -1e30f;
   if (tid < n) {
+    // The whole padded row as 16-byte reads, all issued before the sum: columns
+    // past n are zero (the slot is zero-filled whenever n < NP), so summing all
+    // NP in ascending j adds exact zeros after the reference's n terms.
+    float4 v[NP / 4];
+#pragma unroll
+    for (int q = 0; q < NP / 4; ++q) v[q] = *reinterpret_cast<const float4*>(&Ps[tid * L::LS + 4 * q]);
     float s = 0.f;
-    for (int j = 0; j < n; ++j) s += Ps[tid * L::LS + j];
+#pragma unroll
+    for (int q = 0; q < NP / 4; ++q) s = (((s + v[q].x) + v[q].y) + v[q].z) + v[q].w;
     row = s;
   }
   for (int off = 32; off > 0; off >>= 1) row = fmaxf(row, __shfl_xor(row, off));
@@ -196,7 +247,7 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
 // registers as this wave's A operand after the set-up, so the LDS holds V and
 // T = PV only. Otherwise V <- 2V - (VP)V (its order for n = 128): LDS holds V
 // and P, P is overwritten by W = VP and reloaded each iteration.
-template <typename T, int NP, bool PV_FIRST, int WPR = 1>
+template <typename T, int NP, bool PV_FIRST, int WPR = 1, int KL = 4>
 __global__ void __launch_bounds__(NP * 4 * WPR)
 newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
   using L = NsLayout<NP, WPR>;
@@ -227,17 +278,77 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
         pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
       }
     }
+    // n = NP - 15 (KL = 1): the last strip holds one live row, r1 = NP - 16. Its
+    // waves compute that row on the VALU (lane (li, lk): column 16 (t0 + t) + li
+    // of each of its tiles, partial sums over its own k = 16 kb + 4 lk + s,
+    // added over lk by two exchanges) and leave the matrix core to the other
+    // strips; rows and columns past it stay zero padding. pa holds, for li = 0,
+    // row r1 of P: every lane takes its k set of that row.
+    constexpr int r1 = NP - 16;
+    const bool rowv = KL == 1 && wave / WPR == L::NT - 1;
+    if (rowv) {
+      const int kq = 4 * (lane >> 4);
+#pragma unroll
+      for (int kb = 0; kb < L::NT; ++kb) {
+        const float4 v = *reinterpret_cast<const float4*>(&Ps[r1 * L::LS + 16 * kb + kq]);
+        pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
+      }
+    }
     __syncthreads();  // P fully read (registers) and V0 written before slot P becomes T
     float* Ts = Ps;
+    const int t0v = (wave % WPR) * L::TW, li = lane & 15, lk = lane >> 4;
     for (int it = 0; it < iters; ++it) {
-      mfma_rowstrip_areg<NP, WPR>(pa, Vs, wave, lane, acc);           // T = P V
-      store_strip_t<NP, WPR>(Ts, wave, lane, acc);                     // slot T holds T^T
+      if (rowv) {
+#pragma unroll
+        for (int t = 0; t < L::TW; ++t) {  // T[r1][j] = sum_k P[r1][k] V[k][j]
+          const int j = 16 * (t0v + t) + li;
+          float sum = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < L::NT; ++kb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (kb + 1 < L::NT || q < KL) sum += pa[kb][q] * Vs[(16 * kb + 4 * lk + q) * L::LS + j];
+          sum = sum_rows4(sum);
+          if (lk == 0) Ts[j * L::LS + r1] = sum;
+        }
+      } else {
+        mfma_rowstrip_areg<NP, WPR, KL>(pa, Vs, wave, lane, acc);       // T = P V
+        store_strip_t<NP, WPR>(Ts, wave, lane, acc);                     // slot T holds T^T
+      }
       __syncthreads();
-      mfma_rowstrip<NP, WPR, false, true>(Vs, Ts, wave, lane, acc);   // U = V T (own V rows only)
+      float u[L::TW];
+      if (rowv) {
+#pragma unroll
+        for (int t = 0; t < L::TW; ++t) {  // U[r1][j] = sum_k V[r1][k] T[k][j], T[k][j] = Ts[j][k]
+          const int j = 16 * (t0v + t) + li;
+          float sum = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < L::NT; ++kb) {
+            const float4 vv = *reinterpret_cast<const float4*>(&Vs[r1 * L::LS + 16 * kb + 4 * lk]);
+            const float4 tt = *reinterpret_cast<const float4*>(&Ts[j * L::LS + 16 * kb + 4 * lk]);
+            const float va[4] = {vv.x, vv.y, vv.z, vv.w}, ta[4] = {tt.x, tt.y, tt.z, tt.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (kb + 1 < L::NT || q < KL) sum += va[q] * ta[q];
+          }
+          u[t] = sum_rows4(sum);
+        }
+      } else {
+        mfma_rowstrip<NP, WPR, false, true, KL>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
+      }
       // With WPR > 1 the waves of a strip read all of its V rows and each then
       // updates part of them: every read first.
       if constexpr (WPR > 1) __syncthreads();
-      update_strip<NP, WPR>(Vs, wave, lane, acc);                      // V = 2V - U
+      if (rowv) {
+        if (lk == 0)
+#pragma unroll
+          for (int t = 0; t < L::TW; ++t) {
+            float* p = &Vs[r1 * L::LS + 16 * (t0v + t) + li];
+            *p = 2.0f * (*p) - u[t];
+          }
+      } else {
+        update_strip<NP, WPR>(Vs, wave, lane, acc);                    // V = 2V - U
+      }
       __syncthreads();
     }
   } else {
@@ -260,7 +371,7 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
   }
 }
 
-template <typename T, int NP, int WPR = 1>
+template <typename T, int NP, int WPR = 1, int KL = 4>
 __global__ void __launch_bounds__(NP * 4 * WPR)
 newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __restrict__ gmat, int n) {
   using L = NsLayout<NP, WPR>;
@@ -294,11 +405,11 @@ newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __re
   }
   __syncthreads();
   v4f acc[L::TW];
-  mfma_rowstrip<NP, WPR, true, true>(Vs, Gs, wave, lane, acc);  // S = V^T G (B read from G^T)
+  mfma_rowstrip<NP, WPR, true, true, KL>(Vs, Gs, wave, lane, acc);  // S = V^T G (B read from G^T)
   __syncthreads();
   store_strip<NP, WPR>(Gs, wave, lane, acc);
   __syncthreads();
-  mfma_rowstrip<NP, WPR, false, true>(Gs, Vs, wave, lane, acc);  // R = S V^T
+  mfma_rowstrip<NP, WPR, false, true, KL>(Gs, Vs, wave, lane, acc);  // R = S V^T
   if (n == NP) {
     // Through LDS (slot V, free once every wave's products are done): whole
     // rows leave as 4-element groups.
@@ -812,9 +923,22 @@ template <int NP> constexpr int pick_wpr() {
   return (nt % 4 == 0 && nt * 4 <= 16) ? 4 : (nt % 2 == 0 && nt * 2 <= 16) ? 2 : 1;
 }
 
+// fp32 matrices with n = 16 m + 1 (e.g. 49 = 7 x 7 landmarks) take the
+// instantiations whose last k block runs one MFMA step of four.
+template <typename T, int NP> constexpr bool has_kl1() { return std::is_same<T, float>::value && NP >= 32 && NP < 128; }
+
 template <typename T, int NP, int WPR>
 int fwd_np_w(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
   // The reference's association order per bucket: V(PV) below 128, (VP)V at 128.
+  if constexpr (has_kl1<T, NP>()) {
+    if (n == NP - 15) {
+      auto k = newton_fwd_kernel<T, NP, true, WPR, 1>;
+      int s = set_lds(k, fwd_lds<NP>());
+      if (s) return s;
+      hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(), st, m, o, n, iters);
+      return check_launch("newton forward");
+    }
+  }
   if (NP < 128) {
     auto k = newton_fwd_kernel<T, NP, true, WPR>;
     int s = set_lds(k, fwd_lds<NP>());
@@ -832,6 +956,8 @@ int fwd_np_w(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
 template <typename T, int NP, int WPR>
 int bwd_np_w(const T* g, const T* v, T* o, int64_t bh, int n, hipStream_t st) {
   auto k = newton_bwd_kernel<T, NP, WPR>;
+  if constexpr (has_kl1<T, NP>())
+    if (n == NP - 15) k = newton_bwd_kernel<T, NP, WPR, 1>;
   const size_t lds = 2 * (size_t)NsLayout<NP>::ELEMS * 4;
   int s = set_lds(k, lds);
   if (s) return s;
