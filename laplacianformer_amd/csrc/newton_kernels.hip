@@ -204,16 +204,27 @@ __device__ __forceinline__ float sum_rows4(float x) {
   return c + d;
 }
 
-// P = f32(mat) + 0.01 I on the live n x n block; zero padding elsewhere when `pad`.
+// P = f32(mat) + 0.01 I on the live n x n block (the slot's padding is left as is).
 template <typename T, int NP, int WPR>
-__device__ __forceinline__ void load_P(float* __restrict__ Ps, const T* __restrict__ M, int n, bool pad) {
+__device__ __forceinline__ void load_P(float* __restrict__ Ps, const T* __restrict__ M, int n) {
   using L = NsLayout<NP, WPR>;
-  if (pad)
-    for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Ps[e] = 0.f;
-  if (pad) __syncthreads();
   for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
     const int i = e / n, j = e - i * n;
     Ps[i * L::LS + j] = to_acc(M[e]) + (i == j ? 0.01f : 0.f);
+  }
+}
+
+// P = f32(mat) + 0.01 I on the live n x n block and zero on the rest of the
+// NP x NP slot, in one pass (each slot element written once, no zero fill
+// and barrier ahead of it).
+template <typename T, int NP, int WPR>
+__device__ __forceinline__ void load_P_padded(float* __restrict__ Ps, const T* __restrict__ M, int n) {
+  using L = NsLayout<NP, WPR>;
+  for (int e = threadIdx.x; e < NP * NP; e += L::THREADS) {
+    const int i = e / NP, j = e - i * NP;
+    float v = 0.f;
+    if (i < n && j < n) v = to_acc(M[i * n + j]) + (i == j ? 0.01f : 0.f);
+    Ps[i * L::LS + j] = v;
   }
 }
 
@@ -255,14 +266,16 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
   __shared__ float red[16];
   float* Ps = nsm;                 // P; then T = PV (PV_FIRST) or W = VP
   float* Vs = nsm + L::ELEMS;      // V
-  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // With KL = 1 the last strip's waves (one live row, on the VALU) are the
+  // workgroup's first hardware waves: a SIMD issues its oldest waves first, and
+  // that row is the longest chain of each product.
+  const int hw = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wave = KL == 1 ? (hw + (L::NT - 1) * WPR) % L::NW : hw;
   const T* Mg = mat + (size_t)blockIdx.x * n * n;
   T* Og = out + (size_t)blockIdx.x * n * n;
-  const bool pad = n < NP;
 
-  if (pad)
-    for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = 0.f;
-  load_P<T, NP, WPR>(Ps, Mg, n, pad);
+  // V = alpha P below covers the whole V slot (zero padding included).
+  load_P_padded<T, NP, WPR>(Ps, Mg, n);
   __syncthreads();
   const float alpha = compute_alpha<NP, WPR>(Ps, n, red);
   for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = Ps[e] * alpha;
@@ -361,7 +374,7 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
       mfma_rowstrip<NP, WPR, false, false>(Ps, Vs, wave, lane, acc);  // U = W V
       __syncthreads();                                                 // V reads done
       update_strip<NP, WPR>(Vs, wave, lane, acc);
-      if (it + 1 < iters) load_P<T, NP, WPR>(Ps, Mg, n, false);        // padding of slot P is still zero
+      if (it + 1 < iters) load_P<T, NP, WPR>(Ps, Mg, n);               // padding of slot P is still zero
       __syncthreads();
     }
   }
@@ -381,12 +394,16 @@ newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __re
   const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const size_t off = (size_t)blockIdx.x * n * n;
   if (n < NP) {
-    for (int e = threadIdx.x; e < 2 * L::ELEMS; e += L::THREADS) nsm[e] = 0.f;
-    __syncthreads();
-    for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
-      const int i = e / n, j = e - i * n;
-      Vs[i * L::LS + j] = to_acc(inv[off + e]);
-      Gs[j * L::LS + i] = to_acc(gout[off + e]);
+    // Live block and zero padding of both NP x NP slots in one pass.
+    for (int e = threadIdx.x; e < NP * NP; e += L::THREADS) {
+      const int i = e / NP, j = e - i * NP;
+      float v = 0.f, g = 0.f;
+      if (i < n && j < n) {
+        v = to_acc(inv[off + (size_t)i * n + j]);
+        g = to_acc(gout[off + (size_t)i * n + j]);
+      }
+      Vs[i * L::LS + j] = v;
+      Gs[j * L::LS + i] = g;
     }
   } else {
     // Whole 4-element groups of a row (NP is a multiple of 16).
