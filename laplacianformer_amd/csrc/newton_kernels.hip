@@ -120,9 +120,9 @@ __device__ __forceinline__ void mfma_rowstrip(const float* __restrict__ Xs, cons
   }
 }
 
-// As mfma_rowstrip with X = P held in registers: pa[b][s] = P[16*strip + lane%16][16b + 4*(lane/16) + s],
-// the row-major A operand of k block b, step s; Y row-major in LDS.
-template <int NP, int WPR, int KL = 4>
+// As mfma_rowstrip with X held in registers: pa[b][s] = X[16*strip + lane%16][16b + 4*(lane/16) + s],
+// the row-major A operand of k block b, step s; Y in LDS, row-major or (TRANS_Y) transposed.
+template <int NP, int WPR, int KL = 4, bool TRANS_Y = false>
 __device__ __forceinline__ void mfma_rowstrip_areg(const float (&pa)[NP / 16][4], const float* __restrict__ Ys,
                                                    int wave, int lane, v4f (&acc)[NP / 16 / WPR]) {
   using L = NsLayout<NP, WPR>;
@@ -135,9 +135,22 @@ __device__ __forceinline__ void mfma_rowstrip_areg(const float (&pa)[NP / 16][4]
     const int k = 16 * kb + 4 * lk;
     float b[L::TW][4];
 #pragma unroll
-    for (int t = 0; t < L::TW; ++t)
+    for (int t = 0; t < L::TW; ++t) {
+      const int j = 16 * (t0 + t) + li;
+      if constexpr (TRANS_Y) {
+        if (kb + 1 < L::NT || KL == 4) {
+          const float4 v = *reinterpret_cast<const float4*>(&Ys[j * L::LS + k]);
+          b[t][0] = v.x; b[t][1] = v.y; b[t][2] = v.z; b[t][3] = v.w;
+        } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) b[t][s] = Ys[(k + s) * L::LS + 16 * (t0 + t) + li];
+          for (int s = 0; s < KL; ++s) b[t][s] = Ys[j * L::LS + k + s];
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          if (kb + 1 < L::NT || s < KL) b[t][s] = Ys[(k + s) * L::LS + j];
+      }
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       if (kb + 1 < L::NT || s < KL)  // folded at compile time (kb unrolled)
@@ -254,6 +267,11 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
   return 1.8f / (m * m);
 }
 
+// The forward variant whose U = V T reads V from registers (see the loop): the
+// one-live-row path with four waves per strip (its VGPR count still lets two
+// workgroups share a CU, as the wide layout assumes).
+template <int NP, int WPR, int KL> constexpr bool fwd_va() { return KL == 1 && WPR == 4; }
+
 // PV_FIRST: V <- 2V - V(PV) (the reference's order for n <= 112), P held in
 // registers as this wave's A operand after the set-up, so the LDS holds V and
 // T = PV only. Otherwise V <- 2V - (VP)V (its order for n = 128): LDS holds V
@@ -310,6 +328,20 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
     __syncthreads();  // P fully read (registers) and V0 written before slot P becomes T
     float* Ts = Ps;
     const int t0v = (wave % WPR) * L::TW, li = lane & 15, lk = lane >> 4;
+    // VA (one live row, four waves per strip): U = V T takes its A operand (the
+    // strip's V rows; row r1 on the row waves) from registers loaded while T is
+    // computed, so no wave reads V from LDS after T is complete and the update
+    // needs no barrier ahead of it.
+    constexpr bool VA = fwd_va<NP, WPR, KL>();
+    float va[L::NT][4];
+    auto load_va = [&]() {
+      const int i = rowv ? r1 : 16 * (wave / WPR) + li;
+#pragma unroll
+      for (int kb = 0; kb < L::NT; ++kb) {
+        const float4 v = *reinterpret_cast<const float4*>(&Vs[i * L::LS + 16 * kb + 4 * lk]);
+        va[kb][0] = v.x; va[kb][1] = v.y; va[kb][2] = v.z; va[kb][3] = v.w;
+      }
+    };
     for (int it = 0; it < iters; ++it) {
       if (rowv) {
 #pragma unroll
@@ -324,8 +356,10 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
           sum = sum_rows4(sum);
           if (lk == 0) Ts[j * L::LS + r1] = sum;
         }
+        if constexpr (VA) load_va();
       } else {
         mfma_rowstrip_areg<NP, WPR, KL>(pa, Vs, wave, lane, acc);       // T = P V
+        if constexpr (VA) load_va();  // behind T's operand reads, ahead of its barrier
         store_strip_t<NP, WPR>(Ts, wave, lane, acc);                     // slot T holds T^T
       }
       __syncthreads();
@@ -337,21 +371,30 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
           float sum = 0.f;
 #pragma unroll
           for (int kb = 0; kb < L::NT; ++kb) {
-            const float4 vv = *reinterpret_cast<const float4*>(&Vs[r1 * L::LS + 16 * kb + 4 * lk]);
+            float vr[4];
+            if constexpr (VA) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) vr[q] = va[kb][q];
+            } else {
+              const float4 vv = *reinterpret_cast<const float4*>(&Vs[r1 * L::LS + 16 * kb + 4 * lk]);
+              vr[0] = vv.x; vr[1] = vv.y; vr[2] = vv.z; vr[3] = vv.w;
+            }
             const float4 tt = *reinterpret_cast<const float4*>(&Ts[j * L::LS + 16 * kb + 4 * lk]);
-            const float va[4] = {vv.x, vv.y, vv.z, vv.w}, ta[4] = {tt.x, tt.y, tt.z, tt.w};
+            const float ta[4] = {tt.x, tt.y, tt.z, tt.w};
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              if (kb + 1 < L::NT || q < KL) sum += va[q] * ta[q];
+              if (kb + 1 < L::NT || q < KL) sum += vr[q] * ta[q];
           }
           u[t] = sum_rows4(sum);
         }
+      } else if constexpr (VA) {
+        mfma_rowstrip_areg<NP, WPR, KL, true>(va, Ts, wave, lane, acc);    // U = V T
       } else {
         mfma_rowstrip<NP, WPR, false, true, KL>(Vs, Ts, wave, lane, acc);  // U = V T (own V rows only)
       }
       // With WPR > 1 the waves of a strip read all of its V rows and each then
-      // updates part of them: every read first.
-      if constexpr (WPR > 1) __syncthreads();
+      // updates part of them: every read first (done before T was complete with VA).
+      if constexpr (WPR > 1 && !VA) __syncthreads();
       if (rowv) {
         if (lk == 0)
 #pragma unroll
