@@ -248,15 +248,18 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
   const int tid = threadIdx.x;
   float row = -1e30f;
   if (tid < n) {
-    // The whole padded row as 16-byte reads, all issued before the sum: columns
-    // past n are zero (the slot is zero-filled whenever n < NP), so summing all
-    // NP in ascending j adds exact zeros after the reference's n terms.
-    float4 v[NP / 4];
-#pragma unroll
-    for (int q = 0; q < NP / 4; ++q) v[q] = *reinterpret_cast<const float4*>(&Ps[tid * L::LS + 4 * q]);
+    // The whole padded row as 16-byte reads, four at a time ahead of their sums:
+    // columns past n are zero (the slot is zero-filled whenever n < NP), so
+    // summing all NP in ascending j adds exact zeros after the reference's n terms.
     float s = 0.f;
 #pragma unroll
-    for (int q = 0; q < NP / 4; ++q) s = (((s + v[q].x) + v[q].y) + v[q].z) + v[q].w;
+    for (int q0 = 0; q0 < NP / 4; q0 += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const float4*>(&Ps[tid * L::LS + 4 * (q0 + q)]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s = (((s + v[q].x) + v[q].y) + v[q].z) + v[q].w;
+    }
     row = s;
   }
   for (int off = 32; off > 0; off >>= 1) row = fmaxf(row, __shfl_xor(row, off));
@@ -292,39 +295,61 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
   const T* Mg = mat + (size_t)blockIdx.x * n * n;
   T* Og = out + (size_t)blockIdx.x * n * n;
 
-  // V = alpha P below covers the whole V slot (zero padding included).
-  load_P_padded<T, NP, WPR>(Ps, Mg, n);
+  // P = f32(mat) + 0.01 I on the live block, zero on the rest of the NP x NP
+  // slot, in one pass; with few elements per thread (PER) each thread keeps its
+  // own and writes V = alpha P from them below.
+  constexpr int PER = NP * NP / L::THREADS;
+  static_assert(PER * L::THREADS == NP * NP, "whole slot rows per pass");
+  constexpr bool KEEP = PER <= 8;
+  float pv[KEEP ? PER : 1];
+  if constexpr (KEEP) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * L::THREADS, i = e / NP, j = e - i * NP;
+      float v = 0.f;
+      if (i < n && j < n) v = to_acc(Mg[i * n + j]) + (i == j ? 0.01f : 0.f);
+      Ps[i * L::LS + j] = v;
+      pv[q] = v;
+    }
+  } else {
+    load_P_padded<T, NP, WPR>(Ps, Mg, n);
+  }
   __syncthreads();
+
+  // n = NP - 15 (KL = 1): the last strip holds one live row, r1 = NP - 16. Its
+  // waves compute that row on the VALU (lane (li, lk): column 16 (t0 + t) + li
+  // of each of its tiles, partial sums over its own k = 16 kb + 4 lk + s,
+  // added over lk by two exchanges) and leave the matrix core to the other
+  // strips; rows and columns past it stay zero padding. pa holds, for li = 0,
+  // row r1 of P: every lane takes its k set of that row.
+  constexpr int r1 = NP - 16;
+  const bool rowv = KL == 1 && wave / WPR == L::NT - 1;
+  float pa[PV_FIRST ? L::NT : 1][4];
+  auto load_pa = [&]() {  // A operand of T = P V
+    const int i = rowv ? r1 : 16 * (wave / WPR) + (lane & 15), kq = 4 * (lane >> 4);
+#pragma unroll
+    for (int kb = 0; kb < L::NT; ++kb) {
+      const float4 v = *reinterpret_cast<const float4*>(&Ps[i * L::LS + 16 * kb + kq]);
+      pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
+    }
+  };
+  // Small slots: read ahead of alpha's reduction (larger ones would hold more
+  // registers across it than their occupancy allows).
+  if constexpr (PV_FIRST && KEEP) load_pa();
   const float alpha = compute_alpha<NP, WPR>(Ps, n, red);
-  for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = Ps[e] * alpha;
+  if constexpr (KEEP) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int e = threadIdx.x + q * L::THREADS, i = e / NP, j = e - i * NP;
+      Vs[i * L::LS + j] = pv[q] * alpha;
+    }
+  } else {
+    for (int e = threadIdx.x; e < L::ELEMS; e += L::THREADS) Vs[e] = Ps[e] * alpha;
+  }
+  if constexpr (PV_FIRST && !KEEP) load_pa();
 
   v4f acc[L::TW];
   if constexpr (PV_FIRST) {
-    float pa[L::NT][4];
-    {
-      const int i = 16 * (wave / WPR) + (lane & 15), kq = 4 * (lane >> 4);
-#pragma unroll
-      for (int kb = 0; kb < L::NT; ++kb) {
-        const float4 v = *reinterpret_cast<const float4*>(&Ps[i * L::LS + 16 * kb + kq]);
-        pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
-      }
-    }
-    // n = NP - 15 (KL = 1): the last strip holds one live row, r1 = NP - 16. Its
-    // waves compute that row on the VALU (lane (li, lk): column 16 (t0 + t) + li
-    // of each of its tiles, partial sums over its own k = 16 kb + 4 lk + s,
-    // added over lk by two exchanges) and leave the matrix core to the other
-    // strips; rows and columns past it stay zero padding. pa holds, for li = 0,
-    // row r1 of P: every lane takes its k set of that row.
-    constexpr int r1 = NP - 16;
-    const bool rowv = KL == 1 && wave / WPR == L::NT - 1;
-    if (rowv) {
-      const int kq = 4 * (lane >> 4);
-#pragma unroll
-      for (int kb = 0; kb < L::NT; ++kb) {
-        const float4 v = *reinterpret_cast<const float4*>(&Ps[r1 * L::LS + 16 * kb + kq]);
-        pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
-      }
-    }
     __syncthreads();  // P fully read (registers) and V0 written before slot P becomes T
     float* Ts = Ps;
     const int t0v = (wave % WPR) * L::TW, li = lane & 15, lk = lane >> 4;
