@@ -446,10 +446,9 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
       __syncthreads();
     }
   }
-  for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
-    const int i = e / n, j = e - i * n;
-    Og[e] = from_acc<T>(Vs[i * L::LS + j]);
-  }
+  // Row i by wave i mod NW, columns by lane: no division by the runtime n.
+  for (int i = hw; i < n; i += L::NW)
+    for (int j = lane; j < n; j += 64) Og[i * n + j] = from_acc<T>(Vs[i * L::LS + j]);
 }
 
 template <typename T, int NP, int WPR = 1, int KL = 4>
