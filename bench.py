@@ -237,6 +237,9 @@ def bench_layer(args, dev):
     v.requires_grad_()
 
     def step():
+        # Gradients set to None before each step (optimizer.zero_grad(set_to_none=True),
+        # PyTorch's default), so that autograd writes them rather than adding to the last.
+        q.grad = k.grad = v.grad = None
         out = lf.laplacian_attention(q, k, v, grid=(28, 28), pool=4, iters=10)
         out.backward(g)
 

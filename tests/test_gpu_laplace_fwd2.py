@@ -30,6 +30,8 @@ SHAPES = [
     (32, 1, 3073, 49, 64, "16 waves, 6 sets + 0/1-row tails"),
     (8, 5, 1200, 49, 16, "16 waves, 3 sets + 8-row tail, C = 16"),
     (1, 256, 420, 49, 64, "one workgroup per slice, 7 sets (last partial)"),
+    (2, 3, 1000, 49, 64, "one partial set per workgroup"),
+    (1, 16, 2176, 49, 64, "2 sets + 8-row tail, C = 64"),
 ]
 
 
@@ -125,3 +127,27 @@ def test_fwd2_plan_cache_rotation(gpu):
             L.LaplaceSubtraction_forward(qd, kd, out)
             torch.cuda.synchronize()
             assert_bitwise(out, ref, "f16", f"forward bits {shape} round {rnd}")
+
+
+# The dataflow kernel (16-bit, C = 64, at most 400 rows per workgroup) writes
+# each row set's outputs as one span: an output that is not 16-byte aligned
+# takes the element-wise copy, a key that is not 16-byte aligned the
+# row-staged kernel. Every case must match the serial oracle bit for bit.
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("offset", [(1, 0), (0, 1), (3, 5)], ids=lambda o: f"out{o[0]}_key{o[1]}")
+def test_fwd5_unaligned(gpu, dt, offset):
+    import laplacianformer_amd as lf
+
+    B, H, N, M, C = 32, 1, 3136, 49, 64
+    oo, ko = offset
+    print(f"fwd5 unaligned {dt} out+{oo} key+{ko}", flush=True)
+    q = gen((B, H, N, C), 777, dt)
+    k = gen((B, H, C, M), 778, dt)
+    kbuf = torch.zeros(B * H * C * M + ko, dtype=k.dtype, device=gpu)
+    kd = kbuf[ko:].view(B, H, C, M)
+    kd.copy_(k.to(gpu))
+    obuf = torch.zeros(B * H * N * M + oo, dtype=q.dtype, device=gpu)
+    out = obuf[oo:].view(B, H, N, M)
+    lf.ext().LaplaceSubtraction_forward(q.to(gpu), kd, out)
+    torch.cuda.synchronize()
+    assert_bitwise(out, oracle.laplace_forward(q, k, dt), dt, f"forward bits (out +{oo}, key +{ko})")
