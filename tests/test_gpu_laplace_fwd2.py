@@ -129,18 +129,18 @@ def test_fwd2_plan_cache_rotation(gpu):
             assert_bitwise(out, ref, "f16", f"forward bits {shape} round {rnd}")
 
 
-# The dataflow kernel (16-bit, C = 64, at most 400 rows per workgroup) writes
-# each row set's outputs as one span: an output that is not 16-byte aligned
-# takes the element-wise copy, a key that is not 16-byte aligned the
-# row-staged kernel. Every case must match the serial oracle bit for bit.
+# The row-staged kernel copies each workgroup's span of outputs out of LDS in
+# 16-byte vectors when the span is 16-byte aligned, in 4-byte words when it is
+# 4-byte aligned, element by element otherwise, and reads the key element-wise;
+# outputs and keys at odd element offsets must match the serial oracle bit for bit.
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("offset", [(1, 0), (0, 1), (3, 5)], ids=lambda o: f"out{o[0]}_key{o[1]}")
-def test_fwd5_unaligned(gpu, dt, offset):
+def test_fwd2_unaligned(gpu, dt, offset):
     import laplacianformer_amd as lf
 
     B, H, N, M, C = 32, 1, 3136, 49, 64
     oo, ko = offset
-    print(f"fwd5 unaligned {dt} out+{oo} key+{ko}", flush=True)
+    print(f"fwd2 unaligned {dt} out+{oo} key+{ko}", flush=True)
     q = gen((B, H, N, C), 777, dt)
     k = gen((B, H, C, M), 778, dt)
     kbuf = torch.zeros(B * H * C * M + ko, dtype=k.dtype, device=gpu)
