@@ -201,8 +201,8 @@ template <> struct APieces<bf16s> { static constexpr int n = 1; };
 // of the pieces whose weight is at least 2^-16 of the leading one
 // (a1 b1, a1 b2, a2 b1, a1 b3, a2 b2, a3 b1) are accumulated in fp32 by
 // v_mfma_f32_16x16x32_bf16; the terms left out are below 2^-22 |a| |b|.
-// Each wave works alone on 16-row groups g, g + 4 * gridDim.x, ... of its slice
-// (one group's loads ahead). Lane (i, h) = (lane % 16, lane / 16) holds the A
+// A workgroup is kMixWaves waves; each works alone on 16-row groups g,
+// g + kMixWaves * gridDim.x, ... of its slice (one group's loads ahead). Lane (i, h) = (lane % 16, lane / 16) holds the A
 // operand of row i, k = 16 h + 8 kb + e (kb < 2, e < 8), i.e. elements
 // [16 h, 16 h + 16) of the row:
 //  * DIRECT (P = 64): loaded as 16-byte vectors straight from the row;
@@ -211,15 +211,16 @@ template <> struct APieces<bf16s> { static constexpr int n = 1; };
 //    LDS rows as fp32 with pitch P and read back per lane.
 // The workgroup splits B once into LDS in operand order (piece, column tile,
 // kb, lane). Outputs go straight from the accumulators to C.
+constexpr int kMixWaves = 12;  // one workgroup per CU, three waves per SIMD
 template <typename TA, typename TC, bool DIRECT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * kMixWaves)
 mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __restrict__ C, int N, int P,
                      int Q, int64_t sq, int64_t sp, int64_t bStride) {
   constexpr int EV = 16 / (int)sizeof(TA);  // elements per 16-byte vector
   constexpr int LV = 16 / EV;               // vectors per lane and group
   constexpr int NA = APieces<TA>::n;
   __shared__ __align__(16) uint4 Bp[3 * 4 * 2 * 64];                     // [piece][c][kb][lane]
-  __shared__ __align__(16) float Ws[DIRECT ? 1 : 4][kMixGroup * kMixPMax];  // per wave: its rows (fp32)
+  __shared__ __align__(16) float Ws[DIRECT ? 1 : kMixWaves][kMixGroup * kMixPMax];  // per wave: its rows (fp32)
   const int s = blockIdx.y;
   const int groups = (N + kMixGroup - 1) / kMixGroup;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -241,13 +242,13 @@ mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* 
       for (int v = 0; v < LV; ++v) xv[v] = src[min(lane + 64 * v, nv - 1)];
     }
   };
-  int g = blockIdx.x * 4 + wave;
-  const int gstep = gridDim.x * 4;
+  int g = blockIdx.x * kMixWaves + wave;
+  const int gstep = gridDim.x * kMixWaves;
   load(min(g, groups - 1));  // in flight while B is split
 
-  // B's pieces: thread t takes (c, kb, lane) = (t / 128, (t / 64) % 2, t % 64)
-  // and t + 256: B[k][16 c + i] for k = 16 h + 8 kb + e, zero outside Q x P.
-  {
+  // B's pieces: thread t < 256 takes (c, kb, lane) = (t / 128, (t / 64) % 2,
+  // t % 64) and t + 256: B[k][16 c + i] for k = 16 h + 8 kb + e, zero outside Q x P.
+  if (threadIdx.x < 256) {  // (the first four waves)
     const float* Bm = B + (size_t)s * bStride;
     float bv[2][8];
 #pragma unroll
@@ -350,29 +351,37 @@ mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* 
   }
 }
 
-// Workgroups per slice: at most one 16-row group per wave, and about two
-// workgroups per CU over the whole grid (measured at config 5 with the bf16
-// kernel: 10.7 / 11.7 us for the two layouts, against 11.7 / 14.8 us at four
-// per CU and 11.4 / 18.0 us at eight). A 16-byte aligned A with P = 64, or
-// with 16-byte aligned slices, takes the bf16 kernel; anything else the fp32
-// LDS-staged kernel.
+// Workgroups per slice. The bf16 kernel: one kMixWaves-wave workgroup per CU
+// over the grid, at most one 16-row group per wave (measured at config 5,
+// 128 slices of 784 rows, per call: 9.0 / 9.8 us for the two layouts with 12
+// waves and two workgroups per slice, against 9.5 / 10.1 with 8 waves, 10.2 /
+// 11.4 with 16, and 10.9 / 11.9 us with four 4-wave workgroups per slice: B is
+// split once per CU, and three waves per SIMD overlap one another's loads,
+// splits and MFMAs). The fp32 kernel (4 waves): about two workgroups per CU.
+// A 16-byte aligned A with P = 64, or with 16-byte aligned slices, takes the
+// bf16 kernel; anything else the fp32 LDS-staged kernel.
 template <typename TA, typename TC>
 int launch_mix(const void* A, const float* B, void* C, int64_t slices, int64_t N, int P, int Q, int64_t sq,
                int64_t sp, int64_t bStride, hipStream_t st) {
   const int64_t groups = (N + kMixGroup - 1) / kMixGroup;
-  const int64_t per =
-      std::max<int64_t>(1, std::min<int64_t>((groups + 3) / 4, (2 * (int64_t)num_cus() + slices - 1) / slices));
-  dim3 grid((unsigned)per, (unsigned)slices);
+  const int64_t cus = num_cus();
   const bool aligned = (reinterpret_cast<uintptr_t>(A) & 15) == 0;
-  if (aligned && P == kMixPMax) {
-    hipLaunchKernelGGL((mix_rows_bf16_kernel<TA, TC, true>), grid, dim3(256), 0, st, static_cast<const TA*>(A), B,
-                       static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
-  } else if (aligned && (N * P * (int64_t)sizeof(TA)) % 16 == 0) {
-    hipLaunchKernelGGL((mix_rows_bf16_kernel<TA, TC, false>), grid, dim3(256), 0, st, static_cast<const TA*>(A), B,
-                       static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
+  const bool direct = aligned && P == kMixPMax;
+  if (direct || (aligned && (N * P * (int64_t)sizeof(TA)) % 16 == 0)) {
+    const int64_t per = std::max<int64_t>(
+        1, std::min<int64_t>((groups + kMixWaves - 1) / kMixWaves, (cus + slices - 1) / slices));
+    const dim3 grid((unsigned)per, (unsigned)slices), block(64 * kMixWaves);
+    if (direct)
+      hipLaunchKernelGGL((mix_rows_bf16_kernel<TA, TC, true>), grid, block, 0, st, static_cast<const TA*>(A), B,
+                         static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
+    else
+      hipLaunchKernelGGL((mix_rows_bf16_kernel<TA, TC, false>), grid, block, 0, st, static_cast<const TA*>(A), B,
+                         static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
   } else {
-    hipLaunchKernelGGL((mix_rows_kernel<TA, TC>), grid, dim3(256), 0, st, static_cast<const TA*>(A), B,
-                       static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
+    const int64_t per =
+        std::max<int64_t>(1, std::min<int64_t>((groups + 3) / 4, (2 * cus + slices - 1) / slices));
+    hipLaunchKernelGGL((mix_rows_kernel<TA, TC>), dim3((unsigned)per, (unsigned)slices), dim3(256), 0, st,
+                       static_cast<const TA*>(A), B, static_cast<TC*>(C), (int)N, P, Q, sq, sp, bStride);
   }
   return check_launch("mix rows");
 }
