@@ -474,8 +474,9 @@ __device__ __forceinline__ void split8(const float (&x)[8], uint4 (&out)[NP]) {
 // bf16 pieces, B in APieces<TB> pieces; the pieces' products of weight at least
 // 2^-16 of the leading one, accumulated in fp32; what is left out is below
 // 2^-22 |a| |b|). For 16-byte aligned slices (N * P * 4 and N * Q *
-// sizeof(TB) multiples of 16). Each wave works alone on 32-row blocks kb,
-// kb + 4 * per, ... of its slice (the next block's 16-byte loads in flight):
+// sizeof(TB) multiples of 16). A workgroup is kTallWaves waves (one workgroup
+// per CU); each works alone on 32-row blocks kb, kb + kTallWaves * per, ... of
+// its slice (the next block's 16-byte loads in flight):
 // the block's A rows, one contiguous run, go to the wave's LDS as they are
 // (pitch P) and its B rows as fp32 with pitch 80 where Q is a multiple of the
 // vector width (else pitch Q), and the wave accumulates the whole 64 x 64
@@ -483,14 +484,17 @@ __device__ __forceinline__ void split8(const float (&x)[8], uint4 (&out)[NP]) {
 // (i, h) = (lane % 16, lane / 16) holds rows h + 4 e, e < 8, of column i of a
 // tile, so that the four lane groups read distinct banks for P = 49 and pitch
 // 80). Rows past the end of a last partial block are zero in LDS; columns past
-// P or Q only reach outputs that are never read. At the end the four waves'
-// sums are added in wave order and the workgroup's partial goes to the
-// workspace, as for tall_t_kernel.
-constexpr int kTallKB = 32;   // rows per block: one k-step of the bf16 MFMA
-constexpr int kTallBP = 80;   // padded B pitch (floats)
+// P or Q only reach outputs that are never read. At the end the waves' sums
+// are added in wave order and the workgroup's partial goes to the workspace,
+// as for tall_t_kernel. (Config 5, 128 slices of 784 rows, per call: 11.2 us
+// with 8 waves and two workgroups per slice, against 11.7 us with four 4-wave
+// workgroups per slice.)
+constexpr int kTallKB = 32;    // rows per block: one k-step of the bf16 MFMA
+constexpr int kTallBP = 80;    // padded B pitch (floats)
+constexpr int kTallWaves = 8;  // waves per workgroup (two per SIMD)
 
 template <typename TB>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(64 * kTallWaves)
 tall_t_bf16_kernel(const float* __restrict__ A, const TB* __restrict__ B, float* __restrict__ part, int N, int P,
                    int Q) {
   constexpr int EB = 16 / (int)sizeof(TB);   // B elements per 16-byte vector
@@ -498,7 +502,7 @@ tall_t_bf16_kernel(const float* __restrict__ A, const TB* __restrict__ B, float*
   constexpr int CHA = kTallKB * kMixPMax;    // floats of one staged A block
   constexpr int CHB = kTallKB * kTallBP;     // floats of one staged B block
   constexpr int LVA = CHA / 4 / 64, LVB = CHA / EB / 64;
-  __shared__ __align__(16) float Ws[4][CHA + CHB];  // per wave: A rows | B rows; then its 64 x 64 sums
+  __shared__ __align__(16) float Ws[kTallWaves][CHA + CHB];  // per wave: A rows | B rows; then its 64 x 64 sums
   const int s = blockIdx.y, per = gridDim.x;
   const int kblocks = (N + kTallKB - 1) / kTallKB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -527,8 +531,8 @@ tall_t_bf16_kernel(const float* __restrict__ A, const TB* __restrict__ B, float*
   for (int tp = 0; tp < 4; ++tp)
 #pragma unroll
     for (int tq = 0; tq < 4; ++tq) acc[tp][tq] = v4f{0.f, 0.f, 0.f, 0.f};
-  int kb = blockIdx.x * 4 + wave;
-  const int kstep = per * 4;
+  int kb = blockIdx.x * kTallWaves + wave;
+  const int kstep = per * kTallWaves;
   load(min(kb, kblocks - 1));
   for (; kb < kblocks; kb += kstep) {
     const int rows = min(kTallKB, N - kTallKB * kb);
@@ -587,8 +591,8 @@ tall_t_bf16_kernel(const float* __restrict__ A, const TB* __restrict__ B, float*
     }
     wave_lds_sync();
   }
-  // The wave's sums into its own LDS area ([p][q], 64 x 64), then the four
-  // areas added in wave order.
+  // The wave's sums into its own LDS area ([p][q], 64 x 64), then the areas
+  // added in wave order.
 #pragma unroll
   for (int tp = 0; tp < 4; ++tp)
 #pragma unroll
@@ -598,9 +602,12 @@ tall_t_bf16_kernel(const float* __restrict__ A, const TB* __restrict__ B, float*
   __syncthreads();
   float* out = part + ((size_t)s * per + blockIdx.x) * 64 * 64;
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int e = threadIdx.x + 256 * u;
-    out[e] = ((Ws[0][e] + Ws[1][e]) + Ws[2][e]) + Ws[3][e];
+  for (int u = 0; u < 64 * 64 / (64 * kTallWaves); ++u) {
+    const int e = threadIdx.x + 64 * kTallWaves * u;
+    float sum = Ws[0][e];
+#pragma unroll
+    for (int w = 1; w < kTallWaves; ++w) sum += Ws[w][e];
+    out[e] = sum;
   }
 }
 
@@ -628,21 +635,27 @@ __global__ void __launch_bounds__(256) tall_t_zero_kernel(float* __restrict__ C,
     C[i] = 0.0f;
 }
 
-// Workgroups per slice: about two per CU over the grid.
+// Workgroups per slice: about one per CU over the grid for the bf16 kernel
+// (kTallWaves waves each), two for the fp32 kernel (4 waves each).
 int tall_t_per(int64_t slices, int64_t N) {
   const int64_t tiles = (N + kMixRows - 1) / kMixRows;
   return (int)std::max<int64_t>(1, std::min<int64_t>(tiles, (2 * (int64_t)num_cus() + slices - 1) / slices));
+}
+int tall_t_bf16_per(int64_t slices, int64_t N) {
+  const int64_t blocks = (N + kTallKB - 1) / kTallKB;
+  return (int)std::max<int64_t>(
+      1, std::min<int64_t>((blocks + kTallWaves - 1) / kTallWaves, ((int64_t)num_cus() + slices - 1) / slices));
 }
 
 template <typename TB>
 int launch_tall_t(const float* A, const void* B, float* C, float* ws, int64_t slices, int64_t N, int P, int Q,
                   hipStream_t st) {
-  const int per = tall_t_per(slices, N);
   const bool rowsAligned = (reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0 &&
                            (N * P * 4) % 16 == 0 && (N * Q * (int64_t)sizeof(TB)) % 16 == 0;
+  const int per = rowsAligned ? tall_t_bf16_per(slices, N) : tall_t_per(slices, N);
   if (rowsAligned)
-    hipLaunchKernelGGL(tall_t_bf16_kernel<TB>, dim3((unsigned)per, (unsigned)slices), dim3(256), 0, st, A,
-                       static_cast<const TB*>(B), ws, (int)N, P, Q);
+    hipLaunchKernelGGL(tall_t_bf16_kernel<TB>, dim3((unsigned)per, (unsigned)slices), dim3(64 * kTallWaves), 0, st,
+                       A, static_cast<const TB*>(B), ws, (int)N, P, Q);
   else
     hipLaunchKernelGGL(tall_t_kernel<TB>, dim3((unsigned)per, (unsigned)slices), dim3(256), 0, st, A,
                        static_cast<const TB*>(B), ws, (int)N, P, Q);
@@ -659,7 +672,7 @@ using namespace lfamd;
 
 extern "C" size_t lfamd_tall_t_workspace_size(int64_t slices, int64_t rows) {
   if (slices <= 0 || rows <= 0) return 0;
-  return (size_t)slices * tall_t_per(slices, rows) * 64 * 64 * sizeof(float);
+  return (size_t)slices * std::max(tall_t_per(slices, rows), tall_t_bf16_per(slices, rows)) * 64 * 64 * sizeof(float);
 }
 
 extern "C" int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t slices, int64_t rows,
