@@ -72,6 +72,11 @@ int f2_launch(int dtype, bool kernelEpi, const void* q, const void* k, void* o, 
 int f2_launch_multi(int dtype, int nsrc, const void* const* q, const int64_t* n, const void* k, float* const* o,
                     int64_t BH, int64_t C, float scale, hipStream_t st);
 
+// The bf16 tall product's per-workgroup partials (mix_kernels.hip): [slices][per][64][64]
+// fp32, entry [p][q] = sum over a workgroup's rows of a[n][p] * b[n][q]; *perOut = per.
+int tall_t_partials(int b_dtype, const float* A, const void* B, float* ws, size_t wsBytes, int64_t slices,
+                    int64_t N, int P, int Q, hipStream_t st, int* perOut);
+
 inline bool valid_dtype(int dt) {
   return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;
 }

@@ -666,6 +666,36 @@ int launch_tall_t(const float* A, const void* B, float* C, float* ws, int64_t sl
   return check_launch("tall product reduction");
 }
 
+// The bf16 tall product's per-workgroup partials only ([slices][per][64][64]
+// fp32, entry [p][q]; the caller sums them): b_dtype F32 / F16 / BF16, inner and
+// cols <= 64, 16-byte aligned slices (else LFAMD_ERR_UNSUPPORTED).
+int tall_t_partials(int b_dtype, const float* A, const void* B, float* ws, size_t wsBytes, int64_t slices,
+                    int64_t N, int P, int Q, hipStream_t st, int* perOut) {
+  const size_t elems = b_dtype == LFAMD_F32 ? 4 : 2;
+  const bool rowsAligned = (reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0 &&
+                           (N * P * 4) % 16 == 0 && (N * Q * (int64_t)elems) % 16 == 0;
+  if (!rowsAligned || P > kMixPMax || Q > kMixPMax || N < 1 || slices < 1)
+    return fail(LFAMD_ERR_UNSUPPORTED, "tall product partials: unaligned or unsupported sizes");
+  const int per = tall_t_bf16_per(slices, N);
+  if (wsBytes < (size_t)slices * per * 64 * 64 * sizeof(float))
+    return fail(LFAMD_ERR_ARG, "tall product partials: workspace too small");
+  *perOut = per;
+  const dim3 grid((unsigned)per, (unsigned)slices), block(64 * kTallWaves);
+  switch (b_dtype) {
+    case LFAMD_F32:
+      hipLaunchKernelGGL(tall_t_bf16_kernel<float>, grid, block, 0, st, A, static_cast<const float*>(B), ws, (int)N, P, Q);
+      break;
+    case LFAMD_F16:
+      hipLaunchKernelGGL(tall_t_bf16_kernel<f16s>, grid, block, 0, st, A, static_cast<const f16s*>(B), ws, (int)N, P, Q);
+      break;
+    case LFAMD_BF16:
+      hipLaunchKernelGGL(tall_t_bf16_kernel<bf16s>, grid, block, 0, st, A, static_cast<const bf16s*>(B), ws, (int)N, P, Q);
+      break;
+    default: return fail(LFAMD_ERR_DTYPE, "tall product partials: unsupported dtype %d", b_dtype);
+  }
+  return check_launch("tall product partials");
+}
+
 }  // namespace lfamd
 
 using namespace lfamd;

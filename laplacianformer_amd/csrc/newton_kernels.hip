@@ -279,9 +279,8 @@ template <int NP, int WPR, int KL> constexpr bool fwd_va() { return KL == 1 && W
 // registers as this wave's A operand after the set-up, so the LDS holds V and
 // T = PV only. Otherwise V <- 2V - (VP)V (its order for n = 128): LDS holds V
 // and P, P is overwritten by W = VP and reloaded each iteration.
-template <typename T, int NP, bool PV_FIRST, int WPR = 1, int KL = 4>
-__global__ void __launch_bounds__(NP * 4 * WPR)
-newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
+template <typename T, int NP, bool PV_FIRST, int WPR, int KL>
+__device__ __forceinline__ void newton_fwd_body(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
   using L = NsLayout<NP, WPR>;
   extern __shared__ __align__(16) float nsm[];
   __shared__ float red[16];
@@ -449,6 +448,126 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
   // Row i by wave i mod NW, columns by lane: no division by the runtime n.
   for (int i = hw; i < n; i += L::NW)
     for (int j = lane; j < n; j += 64) Og[i * n + j] = from_acc<T>(Vs[i * L::LS + j]);
+}
+
+template <typename T, int NP, bool PV_FIRST, int WPR = 1, int KL = 4>
+__global__ void __launch_bounds__(NP * 4 * WPR)
+newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
+  newton_fwd_body<T, NP, PV_FIRST, WPR, KL>(mat, out, n, iters);
+}
+
+// ---------------------------------------------------------------------------
+// The attention layer's landmark products around NewtonInverse, fused into it
+// (no reference counterpart: the reference ships the operators only). With
+// Kmm the layer's m x m landmark kernel, 48 < m <= 64 (the 64 bucket), d <= 64,
+// fp32, one workgroup per slice:
+//   forward:  X = NewtonInverse(Kmm); kv = sum of the tall product's
+//             per-workgroup partials of K_km^T V (in workgroup order);
+//             W = X kv                                   (X, kv, W written)
+//   backward: dw = sum of the partials of K_qm^T G; then
+//             dX = dw kv^T,  dkv = X^T dw,  dKmm = -(X^T dX) X^T
+//             (dkv, dKmm written)
+// so that the partial sums, the m x m products and the inverse's gradient
+// input never make a round trip through HBM or a launch of their own.
+// Partials: [slice][per][64][64] fp32, entry [p][q] (landmark p, channel q);
+// entries outside m x d are not read as data (set to zero here).
+
+// Sum of the slice's `per` partials (in order) into an LDS tile [64][LS]:
+// rows < m and columns < d, zero elsewhere.
+template <int NP, int WPR>
+__device__ __forceinline__ void sum_partials(float* __restrict__ Ds, const float* __restrict__ part, int per, int m,
+                                             int d) {
+  using L = NsLayout<NP, WPR>;
+  static_assert(NP == 64, "64-column tiles");
+  const float* src = part + (size_t)blockIdx.x * per * 64 * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += L::THREADS) {
+    const int i = e >> 6, j = e & 63;
+    float sum = 0.0f;
+    if (i < m && j < d)
+      for (int x = 0; x < per; ++x) sum += src[(size_t)x * 64 * 64 + e];
+    Ds[i * L::LS + j] = sum;
+  }
+}
+
+// Rows < m, columns < d of this wave's tiles, row-major with d columns.
+template <int NP, int WPR>
+__device__ __forceinline__ void store_tiles(float* __restrict__ dst, int wave, int lane, const v4f (&acc)[NP / 16 / WPR],
+                                            int m, int d) {
+  using L = NsLayout<NP, WPR>;
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
+#pragma unroll
+  for (int t = 0; t < L::TW; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * strip + 4 * (lane >> 4) + r, j = 16 * (t0 + t) + (lane & 15);
+      if (i < m && j < d) dst[(size_t)i * d + j] = acc[t][r];
+    }
+}
+
+template <int NP, int WPR, int KL>
+__global__ void __launch_bounds__(NP * 4 * WPR)
+newton_fwd_mul_kernel(const float* __restrict__ mat, float* __restrict__ out, int n, int iters,
+                      const float* __restrict__ part, int per, int d, float* __restrict__ kvOut,
+                      float* __restrict__ wOut) {
+  using L = NsLayout<NP, WPR>;
+  newton_fwd_body<float, NP, true, WPR, KL>(mat, out, n, iters);
+  // The body ends after a barrier that follows every read of slot T (P V), so
+  // the slot takes kv; V stays in slot V.
+  extern __shared__ __align__(16) float nsm[];
+  float* KVs = nsm;
+  const float* Vs = nsm + L::ELEMS;
+  const int wave = KL == 1 ? (uniform(threadIdx.x >> 6) + (L::NT - 1) * WPR) % L::NW : uniform(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  sum_partials<NP, WPR>(KVs, part, per, n, d);
+  __syncthreads();
+  float* kvs = kvOut + (size_t)blockIdx.x * n * d;
+  for (int e = threadIdx.x; e < n * 64; e += L::THREADS) {
+    const int i = e >> 6, j = e & 63;
+    if (j < d) kvs[i * d + j] = KVs[i * L::LS + j];
+  }
+  v4f acc[L::TW];
+  mfma_rowstrip<NP, WPR, false, false, KL>(Vs, KVs, wave, lane, acc);  // W = X kv (k < n)
+  store_tiles<NP, WPR>(wOut + (size_t)blockIdx.x * n * d, wave, lane, acc, n, d);
+}
+
+template <int NP, int WPR, int KL>
+__global__ void __launch_bounds__(NP * 4 * WPR)
+newton_bwd_mul_kernel(const float* __restrict__ part, int per, const float* __restrict__ kv,
+                      const float* __restrict__ inv, float* __restrict__ dkv, float* __restrict__ gmat, int n, int d) {
+  using L = NsLayout<NP, WPR>;
+  extern __shared__ __align__(16) float nsm[];
+  float* Vs = nsm;                   // X
+  float* Gs = nsm + L::ELEMS;        // dX^T, then S = X^T dX
+  float* DWs = nsm + 2 * L::ELEMS;   // dw
+  float* KVs = nsm + 3 * L::ELEMS;   // kv
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const size_t off = (size_t)blockIdx.x * n * n, offd = (size_t)blockIdx.x * n * d;
+  for (int e = threadIdx.x; e < NP * NP; e += L::THREADS) {
+    const int i = e / NP, j = e - i * NP;
+    Vs[i * L::LS + j] = i < n && j < n ? inv[off + (size_t)i * n + j] : 0.0f;
+    KVs[i * L::LS + j] = i < n && j < d ? kv[offd + (size_t)i * d + j] : 0.0f;
+  }
+  sum_partials<NP, WPR>(DWs, part, per, n, d);
+  __syncthreads();
+  v4f acc[L::TW];
+  mfma_rowstrip<NP, WPR, false, true, 4>(DWs, KVs, wave, lane, acc);   // dX = dw kv^T (k < d)
+  store_strip_t<NP, WPR>(Gs, wave, lane, acc);                          // slot G holds dX^T
+  mfma_rowstrip<NP, WPR, true, false, KL>(Vs, DWs, wave, lane, acc);   // dkv = X^T dw (k < n)
+  store_tiles<NP, WPR>(dkv + offd, wave, lane, acc, n, d);
+  __syncthreads();
+  mfma_rowstrip<NP, WPR, true, true, KL>(Vs, Gs, wave, lane, acc);     // S = X^T dX (B read from dX^T)
+  __syncthreads();
+  store_strip<NP, WPR>(Gs, wave, lane, acc);
+  __syncthreads();
+  mfma_rowstrip<NP, WPR, false, true, KL>(Gs, Vs, wave, lane, acc);    // R = S X^T
+  const int strip = wave / WPR, t0 = (wave % WPR) * L::TW;
+#pragma unroll
+  for (int t = 0; t < L::TW; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * strip + 4 * (lane >> 4) + r, j = 16 * (t0 + t) + (lane & 15);
+      if (i < n && j < n) gmat[off + (size_t)i * n + j] = -acc[t][r];
+    }
 }
 
 template <typename T, int NP, int WPR = 1, int KL = 4>
@@ -1133,7 +1252,76 @@ int check_workspace(int dtype, int64_t bh, int64_t n, const void* ws, size_t byt
 
 using namespace lfamd;
 
+// The attention layer's fused landmark kernels (48 < m <= 64: the 64 bucket).
+constexpr size_t kMulBwdLds = 4 * (size_t)NsLayout<64>::ELEMS * 4;
+
+template <int WPR, int KL>
+int launch_fwd_mul(const float* kmm, float* inv, int64_t bh, int m, int iters, const float* part, int per, int d,
+                   float* kv, float* w, hipStream_t st) {
+  auto k = newton_fwd_mul_kernel<64, WPR, KL>;
+  if (int s = check_fit(reinterpret_cast<const void*>(k), 64 * 4 * WPR, fwd_lds<64>(), "attention landmarks forward")) return s;
+  if (int s = set_lds(k, fwd_lds<64>())) return s;
+  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(64 * 4 * WPR), fwd_lds<64>(), st, kmm, inv, m, iters, part, per, d,
+                     kv, w);
+  return check_launch("attention landmarks forward");
+}
+
+template <int KL>
+int launch_bwd_mul(const float* part, int per, const float* kv, const float* inv, float* dkv, float* dkmm, int64_t bh,
+                   int m, int d, hipStream_t st) {
+  auto k = newton_bwd_mul_kernel<64, 4, KL>;
+  if (int s = check_fit(reinterpret_cast<const void*>(k), 64 * 16, kMulBwdLds, "attention landmarks backward")) return s;
+  if (int s = set_lds(k, kMulBwdLds)) return s;
+  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(64 * 16), kMulBwdLds, st, part, per, kv, inv, dkv, dkmm, m, d);
+  return check_launch("attention landmarks backward");
+}
+
+int check_landmarks(int dt, int64_t slices, int64_t rows, int m, int d, const char* who) {
+  if (dt != LFAMD_F32 && dt != LFAMD_F16 && dt != LFAMD_BF16) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dt);
+  if (slices < 0 || slices > 65535 || rows < 1 || rows > (int64_t)1 << 30 || m < 1 || d < 1)
+    return fail(LFAMD_ERR_ARG, "%s: bad sizes (slices=%lld rows=%lld m=%d d=%d)", who, (long long)slices,
+                (long long)rows, m, d);
+  if (m <= 48 || m > 64 || d > 64)
+    return fail(LFAMD_ERR_UNSUPPORTED, "%s: landmark count %d or width %d outside (48, 64] / 64", who, m, d);
+  return LFAMD_OK;
+}
+
 extern "C" {
+
+int lfamd_attention_landmarks_forward(const float* kmm, const float* kkm, int v_dtype, const void* v, float* inv,
+                                      float* kv, float* w, int64_t slices, int64_t rows, int m, int d, int iters,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = check_landmarks(v_dtype, slices, rows, m, d, "attention landmarks forward")) return s;
+  if (slices == 0) return ok();
+  if (!kmm || !kkm || !v || !inv || !kv || !w || !workspace)
+    return fail(LFAMD_ERR_ARG, "attention landmarks forward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int per = 0;
+  float* part = static_cast<float*>(workspace);
+  if (int s = tall_t_partials(v_dtype, kkm, v, part, workspace_bytes, slices, rows, m, d, st, &per)) return s;
+  if (iters < 0) iters = 0;
+  const bool wide = use_wide<64>(slices);
+  if (m == 49)
+    return wide ? launch_fwd_mul<4, 1>(kmm, inv, slices, m, iters, part, per, d, kv, w, st)
+                : launch_fwd_mul<2, 1>(kmm, inv, slices, m, iters, part, per, d, kv, w, st);
+  return wide ? launch_fwd_mul<4, 4>(kmm, inv, slices, m, iters, part, per, d, kv, w, st)
+              : launch_fwd_mul<2, 4>(kmm, inv, slices, m, iters, part, per, d, kv, w, st);
+}
+
+int lfamd_attention_landmarks_backward(const float* kqm, int g_dtype, const void* g, const float* kv,
+                                       const float* inv, float* dkv, float* dkmm, int64_t slices, int64_t rows, int m,
+                                       int d, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = check_landmarks(g_dtype, slices, rows, m, d, "attention landmarks backward")) return s;
+  if (slices == 0) return ok();
+  if (!kqm || !g || !kv || !inv || !dkv || !dkmm || !workspace)
+    return fail(LFAMD_ERR_ARG, "attention landmarks backward: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int per = 0;
+  float* part = static_cast<float*>(workspace);
+  if (int s = tall_t_partials(g_dtype, kqm, g, part, workspace_bytes, slices, rows, m, d, st, &per)) return s;
+  if (m == 49) return launch_bwd_mul<1>(part, per, kv, inv, dkv, dkmm, slices, m, d, st);
+  return launch_bwd_mul<4>(part, per, kv, inv, dkv, dkmm, slices, m, d, st);
+}
 
 int lfamd_newton_is_supported(int64_t n) { return n >= 1 && n <= kMaxN ? 1 : 0; }
 

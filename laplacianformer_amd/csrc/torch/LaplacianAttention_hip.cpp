@@ -96,6 +96,49 @@ at::Tensor tall_t(const at::Tensor& a, const at::Tensor& b) {
   return c;
 }
 
+// inv = NewtonInverse(k_mm), kv = K_km^T V and w = inv kv in two launches (the
+// tall product's partials, then the inverse with the partials' sum and the m x m
+// product fused in) where the fused path takes the shape; false otherwise.
+bool landmarks_forward(const at::Tensor& k_mm, const at::Tensor& k_km, const at::Tensor& v, int64_t iters,
+                       at::Tensor& inv, at::Tensor& kv, at::Tensor& w) {
+  const int64_t B = v.size(0), H = v.size(1), N = v.size(2), d = v.size(3), M = k_mm.size(2);
+  at::hip::HIPGuardMasqueradingAsCUDA guard(v.device());
+  const size_t wsb = lfamd_tall_t_workspace_size(B * H, N);
+  kv = at::empty({B, H, M, d}, v.options().dtype(at::kFloat));
+  w = at::empty_like(kv);
+  at::Tensor ws = at::empty({(int64_t)wsb}, v.options().dtype(at::kByte));
+  const int st = lfamd_attention_landmarks_forward(
+      k_mm.data_ptr<float>(), k_km.data_ptr<float>(), detail::abi_dtype(v, "laplacian attention"), v.data_ptr(),
+      inv.data_ptr<float>(), kv.data_ptr<float>(), w.data_ptr<float>(), B * H, N, (int)M, (int)d, (int)iters,
+      ws.data_ptr(), wsb, detail::stream_of(v));
+  if (st == LFAMD_ERR_UNSUPPORTED) return false;
+  detail::check_status(st);
+  return true;
+}
+
+// Its backward for the gradient g of the output: d_kv and the gradient d_kmm of
+// K_mm from the tall product K_qm^T g (partials), kv and inv, in two launches
+// where the fused path takes the shape; false otherwise.
+bool landmarks_backward(const at::Tensor& k_qm, const at::Tensor& g, const at::Tensor& kv, const at::Tensor& inv,
+                        at::Tensor& d_kv, at::Tensor& d_kmm) {
+  const int64_t B = g.size(0), H = g.size(1), N = g.size(2), d = g.size(3), M = inv.size(2);
+  if (!kv.is_contiguous() || !inv.is_contiguous() || kv.scalar_type() != at::kFloat ||
+      inv.scalar_type() != at::kFloat)
+    return false;
+  at::hip::HIPGuardMasqueradingAsCUDA guard(g.device());
+  const size_t wsb = lfamd_tall_t_workspace_size(B * H, N);
+  d_kv = at::empty_like(kv);
+  d_kmm = at::empty_like(inv);
+  at::Tensor ws = at::empty({(int64_t)wsb}, g.options().dtype(at::kByte));
+  const int st = lfamd_attention_landmarks_backward(
+      k_qm.data_ptr<float>(), detail::abi_dtype(g, "laplacian attention backward"), g.data_ptr(),
+      kv.data_ptr<float>(), inv.data_ptr<float>(), d_kv.data_ptr<float>(), d_kmm.data_ptr<float>(), B * H, N,
+      (int)M, (int)d, ws.data_ptr(), wsb, detail::stream_of(g));
+  if (st == LFAMD_ERR_UNSUPPORTED) return false;
+  detail::check_status(st);
+  return true;
+}
+
 void check_layer(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t gh, int64_t gw,
                  int64_t pool) {
   // Every launch below takes raw device pointers: inputs on the CPU or on two
@@ -136,10 +179,12 @@ std::vector<at::Tensor> LaplacianAttention_forward(at::Tensor q, at::Tensor k, a
                                            (int)d, detail::stream_of(k)));
   const std::vector<at::Tensor> kk = kernel_fwd3(km, q, k, km_cm, s);
   const at::Tensor &k_mm = kk[0], &k_qm = kk[1], &k_km = kk[2];
-  at::Tensor inv = at::empty_like(k_mm);
-  NewtonInverse_forward(k_mm, inv, iters);
-  at::Tensor kv = tall_t(k_km, v);                               // K_km^T V  [B,H,M,d]
-  at::Tensor w = at::matmul(inv, kv);                            // [B,H,M,d]
+  at::Tensor inv = at::empty_like(k_mm), kv, w;
+  if (!landmarks_forward(k_mm, k_km, v, iters, inv, kv, w)) {
+    NewtonInverse_forward(k_mm, inv, iters);
+    kv = tall_t(k_km, v);                                        // K_km^T V  [B,H,M,d]
+    w = at::matmul(inv, kv);                                     // [B,H,M,d]
+  }
   at::Tensor out = mix_rows(k_qm, w.transpose(-1, -2), in);      // K_qm W, rounded once
   return {out, km, km_cm, k_qm, k_mm, k_km, inv, kv, w};
 }
@@ -160,13 +205,16 @@ std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at
   const double s = 1.0 / std::sqrt((double)dd);
   g = g.contiguous();
   at::Tensor d_kqm = mix_rows(g, w, at::kFloat);                        // G W^T       [B,H,N,M]
-  at::Tensor d_w = tall_t(k_qm, g);                                      // K_qm^T G    [B,H,M,d]
-  at::Tensor d_inv = at::matmul(d_w, kv.transpose(-1, -2));              // [B,H,M,M]
-  at::Tensor d_kv = at::matmul(inv.transpose(-1, -2), d_w);              // [B,H,M,d]
+  at::Tensor d_kv, d_kmm;
+  if (!landmarks_backward(k_qm, g, kv, inv, d_kv, d_kmm)) {
+    at::Tensor d_w = tall_t(k_qm, g);                                    // K_qm^T G    [B,H,M,d]
+    at::Tensor d_inv = at::matmul(d_w, kv.transpose(-1, -2));            // [B,H,M,M]
+    d_kv = at::matmul(inv.transpose(-1, -2), d_w);                       // [B,H,M,d]
+    d_kmm = at::empty_like(k_mm);
+    NewtonInverse_backward(d_inv.contiguous(), inv, d_kmm);
+  }
   at::Tensor d_kkm = mix_rows(v, d_kv, at::kFloat);                      // V dkv^T     [B,H,N,M]
   at::Tensor d_v = mix_rows(k_km, d_kv.transpose(-1, -2), v.scalar_type());  // K_km dkv [B,H,N,d]
-  at::Tensor d_kmm = at::empty_like(k_mm);
-  NewtonInverse_backward(d_inv.contiguous(), inv, d_kmm);
   at::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
   const int dt = detail::abi_dtype(k, "laplacian attention backward");
   // The three distances' gradients (K_qm, K_km, K_mm share the key km_cm): one

@@ -110,6 +110,21 @@ def test_attention_config5_grid_types(gpu, dtype, d):
     _run(gpu, 2, 2, (28, 28), d, dtype, seed=80 + d, slices=[slice(0, 1), slice(1, 2)])
 
 
+@pytest.mark.parametrize("grid,dtype", [((28, 32), "f16"), ((32, 32), "f32")], ids=["m56-f16", "m64-f32"])
+def test_attention_landmark_buckets(gpu, grid, dtype):
+    """Landmark counts 56 and 64 (a partial and a full 64 bucket): the fused landmark
+    kernels on their general instantiation (every k block whole)."""
+    print(f"attention grid {grid} {dtype}", flush=True)
+    _run(gpu, 2, 2, grid, 64, dtype, seed=90 + grid[1], slices=[slice(0, 1), slice(1, 2)])
+
+
+def test_attention_many_slices(gpu):
+    """512 (batch, head) slices: the fused landmark forward with two waves per strip (more
+    than two matrices per CU); every token a landmark (pool 1, M = 49)."""
+    print("attention 512 slices", flush=True)
+    _run(gpu, 128, 4, (7, 7), 16, "f32", seed=95, pool=1, slices=[slice(0, 1), slice(127, 128)])
+
+
 def test_attention_gradcheck(gpu):
     """fp64 end to end on the GPU: torch.autograd.gradcheck of the layer (Newton run to
     convergence, where -V^T G V^T is the exact derivative)."""
