@@ -240,22 +240,25 @@ size_t lfamd_tall_t_workspace_size(int64_t slices, int64_t rows);
 int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t slices, int64_t rows,
                  int inner, int cols, void* workspace, size_t workspace_bytes, void* stream);
 
-/* The attention layer's landmark products fused around NewtonInverse, for m landmarks with
- * 48 < m <= 64 and width d <= 64 (else LFAMD_ERR_UNSUPPORTED), fp32 [slices][...] contiguous, one
- * workgroup per slice. Forward: inv = NewtonInverse(kmm, iters) (kmm [m][m], as
- * lfamd_newton_forward), kv = kkm^T v (kkm [rows][m], v [rows][d] of element type v_dtype: F32,
- * F16 or BF16; kv [m][d]) and w = inv kv ([m][d]). Backward, for the gradient of w: dw = kqm^T g
- * (kqm [rows][m], g [rows][d] of element type g_dtype), dinv = dw kv^T, dkv = inv^T dw ([m][d])
- * and dkmm = -(inv^T dinv) inv^T ([m][m], as lfamd_newton_backward). The tall products need
- * 16-byte aligned slices (LFAMD_ERR_UNSUPPORTED otherwise) and lfamd_tall_t_workspace_size(slices,
- * rows) bytes of workspace. No reference counterpart: they replace, for the layer, the tall
- * products' reductions, the three m x m products and the two NewtonInverse launches. */
+/* The attention layer's landmark products around NewtonInverse, for m landmarks with 48 < m <= 64
+ * and width d <= 64 (else LFAMD_ERR_UNSUPPORTED), fp32 [slices][...] contiguous unless stated, one
+ * workgroup per slice in the fused kernels. Forward: inv = NewtonInverse(kmm, iters) (kmm [m][m],
+ * as lfamd_newton_forward), kv = kkm^T v (kkm [rows][m], v [rows][d] of element type v_dtype: F32,
+ * F16 or BF16; kv [m][d]) and w = inv kv ([m][d]). Backward, for the layer's output gradient g
+ * ([rows][d], element type dtype, as v): dw = kqm^T g, dinv = dw kv^T, dkv = inv^T dw ([m][d]),
+ * dkmm = -(inv^T dinv) inv^T ([m][m], as lfamd_newton_backward), then dkqm = g w^T and
+ * dkkm = v dkv^T ([rows][m], one launch) and dv = kkm dkv ([rows][d], element type dtype). The
+ * tall products need 16-byte aligned slices (LFAMD_ERR_UNSUPPORTED otherwise) and
+ * lfamd_tall_t_workspace_size(slices, rows) bytes of workspace. No reference counterpart: they
+ * replace, for the layer, the tall products' reductions, the three m x m products and the two
+ * NewtonInverse launches, and pair two of the row products in one launch. */
 int lfamd_attention_landmarks_forward(const float* kmm, const float* kkm, int v_dtype, const void* v, float* inv,
                                       float* kv, float* w, int64_t slices, int64_t rows, int m, int d, int iters,
                                       void* workspace, size_t workspace_bytes, void* stream);
-int lfamd_attention_landmarks_backward(const float* kqm, int g_dtype, const void* g, const float* kv,
-                                       const float* inv, float* dkv, float* dkmm, int64_t slices, int64_t rows, int m,
-                                       int d, void* workspace, size_t workspace_bytes, void* stream);
+int lfamd_attention_landmarks_backward(const float* kqm, int dtype, const void* g, const void* v, const float* kkm,
+                                       const float* w, const float* kv, const float* inv, float* dkqm, float* dkkm,
+                                       void* dv, float* dkv, float* dkmm, int64_t slices, int64_t rows, int m, int d,
+                                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* km[b][h][m][c] = (sum over the pool x pool patch m of k[b][h][n][c]) / pool^2, summed in fp32 and
  * rounded once to `dtype` (F32, F16 or BF16), for k [B][H][gh*gw][d] on a gh x gw token grid

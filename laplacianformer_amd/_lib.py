@@ -48,7 +48,8 @@ CAPI_PROTOTYPES = [
     ("lfamd_tall_t_workspace_size", _SZ, [_I64, _I64]),
     ("lfamd_tall_t", _I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _P, _SZ, _P]),
     ("lfamd_attention_landmarks_forward", _I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _P, _SZ, _P]),
-    ("lfamd_attention_landmarks_backward", _I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _P, _SZ, _P]),
+    ("lfamd_attention_landmarks_backward", _I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I,
+                                                _I, _P, _SZ, _P]),
     ("lfamd_landmark_pool", _I, [_I, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _P]),
     ("lfamd_landmark_pool_backward", _I, [_I, _P, _P, _P, _P, _P, _I64, _I64, _I, _I, _I, _I, _P]),
     ("lfamd_runtime_version", _I, []),

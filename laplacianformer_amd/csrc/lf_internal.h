@@ -77,6 +77,12 @@ int f2_launch_multi(int dtype, int nsrc, const void* const* q, const int64_t* n,
 int tall_t_partials(int b_dtype, const float* A, const void* B, float* ws, size_t wsBytes, int64_t slices,
                     int64_t N, int P, int Q, hipStream_t st, int* perOut);
 
+// Two row products of one shape, c[i][s][n][q] = sum_p a[i][s][n][p] * b[i][s](q, p)
+// (fp32 C), in one launch (mix_kernels.hip); LFAMD_ERR_UNSUPPORTED where the
+// bf16 row kernel does not take them.
+int mix_rows_pair(int a_dtype, const void* const* A, const float* const* B, float* const* C, int64_t slices,
+                  int64_t N, int P, int Q, int64_t sq, int64_t sp, int64_t bStride, hipStream_t st);
+
 inline bool valid_dtype(int dt) {
   return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;
 }

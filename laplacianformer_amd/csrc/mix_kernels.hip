@@ -213,15 +213,14 @@ template <> struct APieces<bf16s> { static constexpr int n = 1; };
 // kb, lane). Outputs go straight from the accumulators to C.
 constexpr int kMixWaves = 12;  // one workgroup per CU, three waves per SIMD
 template <typename TA, typename TC, bool DIRECT>
-__global__ void __launch_bounds__(64 * kMixWaves)
-mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __restrict__ C, int N, int P,
-                     int Q, int64_t sq, int64_t sp, int64_t bStride) {
+__device__ __forceinline__ void mix_rows_bf16_body(const TA* __restrict__ A, const float* __restrict__ B,
+                                                   TC* __restrict__ C, int N, int P, int Q, int64_t sq, int64_t sp,
+                                                   int64_t bStride, int s, int xb, int per) {
   constexpr int EV = 16 / (int)sizeof(TA);  // elements per 16-byte vector
   constexpr int LV = 16 / EV;               // vectors per lane and group
   constexpr int NA = APieces<TA>::n;
   __shared__ __align__(16) uint4 Bp[3 * 4 * 2 * 64];                     // [piece][c][kb][lane]
   __shared__ __align__(16) float Ws[DIRECT ? 1 : kMixWaves][kMixGroup * kMixPMax];  // per wave: its rows (fp32)
-  const int s = blockIdx.y;
   const int groups = (N + kMixGroup - 1) / kMixGroup;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -242,8 +241,8 @@ mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* 
       for (int v = 0; v < LV; ++v) xv[v] = src[min(lane + 64 * v, nv - 1)];
     }
   };
-  int g = blockIdx.x * kMixWaves + wave;
-  const int gstep = gridDim.x * kMixWaves;
+  int g = xb * kMixWaves + wave;
+  const int gstep = per * kMixWaves;
   load(min(g, groups - 1));  // in flight while B is split
 
   // B's pieces: thread t < 256 takes (c, kb, lane) = (t / 128, (t / 64) % 2,
@@ -349,6 +348,29 @@ mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* 
         if (row < rows && col < Q) Cg[(size_t)row * Q + col] = from_acc<TC>(acc[c][r]);
       }
   }
+}
+
+// Grid (workgroups per slice, slices).
+template <typename TA, typename TC, bool DIRECT>
+__global__ void __launch_bounds__(64 * kMixWaves)
+mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __restrict__ C, int N, int P,
+                     int Q, int64_t sq, int64_t sp, int64_t bStride) {
+  mix_rows_bf16_body<TA, TC, DIRECT>(A, B, C, N, P, Q, sq, sp, bStride, blockIdx.y, blockIdx.x, gridDim.x);
+}
+
+// Two products of one shape in one launch (two operand sets; grid (workgroups
+// per slice, 2 * slices), the second set's workgroups after the first's).
+struct MixPair {
+  const void* A[2];
+  const float* B[2];
+  void* C[2];
+};
+template <typename TA, typename TC, bool DIRECT>
+__global__ void __launch_bounds__(64 * kMixWaves)
+mix_rows_bf16_pair_kernel(MixPair pr, int slices, int N, int P, int Q, int64_t sq, int64_t sp, int64_t bStride) {
+  const int src = (int)blockIdx.y >= slices ? 1 : 0;
+  mix_rows_bf16_body<TA, TC, DIRECT>(static_cast<const TA*>(pr.A[src]), pr.B[src], static_cast<TC*>(pr.C[src]), N,
+                                     P, Q, sq, sp, bStride, (int)blockIdx.y - src * slices, blockIdx.x, gridDim.x);
 }
 
 // Workgroups per slice. The bf16 kernel: one kMixWaves-wave workgroup per CU
@@ -664,6 +686,42 @@ int launch_tall_t(const float* A, const void* B, float* C, float* ws, int64_t sl
   hipLaunchKernelGGL(tall_t_reduce_kernel, dim3((unsigned)((P * Q + 255) / 256), (unsigned)slices), dim3(256), 0,
                      st, ws, C, per, P, Q);
   return check_launch("tall product reduction");
+}
+
+// Two row products of one shape (A of element type a_dtype [slices][N][P], B
+// fp32 through strides, C fp32 [slices][N][Q]) in one launch of the bf16
+// kernel: about one workgroup per CU for both. LFAMD_ERR_UNSUPPORTED where the
+// bf16 kernel does not take the operands (the caller then makes two calls).
+int mix_rows_pair(int a_dtype, const void* const* A, const float* const* B, float* const* C, int64_t slices,
+                  int64_t N, int P, int Q, int64_t sq, int64_t sp, int64_t bStride, hipStream_t st) {
+  const int64_t es = a_dtype == LFAMD_F32 ? 4 : 2;
+  bool direct = P == kMixPMax, rows16 = (N * P * es) % 16 == 0;
+  for (int i = 0; i < 2; ++i)
+    if ((reinterpret_cast<uintptr_t>(A[i]) & 15) != 0) direct = rows16 = false;
+  if (!(direct || rows16) || slices < 1 || N < 1 || 2 * slices > 65535 || P > kMixPMax || Q > kMixPMax)
+    return fail(LFAMD_ERR_UNSUPPORTED, "row product pair: operands the bf16 kernel does not take");
+  const MixPair pr{{A[0], A[1]}, {B[0], B[1]}, {C[0], C[1]}};
+  const int64_t groups = (N + kMixGroup - 1) / kMixGroup;
+  const int64_t per = std::max<int64_t>(
+      1, std::min<int64_t>((groups + kMixWaves - 1) / kMixWaves, ((int64_t)num_cus() + 2 * slices - 1) / (2 * slices)));
+  const dim3 grid((unsigned)per, (unsigned)(2 * slices)), block(64 * kMixWaves);
+#define LFAMD_PAIR(TA)                                                                                          \
+  do {                                                                                                          \
+    if (direct)                                                                                                 \
+      hipLaunchKernelGGL((mix_rows_bf16_pair_kernel<TA, float, true>), grid, block, 0, st, pr, (int)slices,     \
+                         (int)N, P, Q, sq, sp, bStride);                                                        \
+    else                                                                                                        \
+      hipLaunchKernelGGL((mix_rows_bf16_pair_kernel<TA, float, false>), grid, block, 0, st, pr, (int)slices,    \
+                         (int)N, P, Q, sq, sp, bStride);                                                        \
+  } while (0)
+  switch (a_dtype) {
+    case LFAMD_F32: LFAMD_PAIR(float); break;
+    case LFAMD_F16: LFAMD_PAIR(f16s); break;
+    case LFAMD_BF16: LFAMD_PAIR(bf16s); break;
+    default: return fail(LFAMD_ERR_DTYPE, "row product pair: unsupported dtype %d", a_dtype);
+  }
+#undef LFAMD_PAIR
+  return check_launch("row product pair");
 }
 
 // The bf16 tall product's per-workgroup partials only ([slices][per][64][64]

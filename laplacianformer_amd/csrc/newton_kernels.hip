@@ -1308,19 +1308,33 @@ int lfamd_attention_landmarks_forward(const float* kmm, const float* kkm, int v_
               : launch_fwd_mul<2, 4>(kmm, inv, slices, m, iters, part, per, d, kv, w, st);
 }
 
-int lfamd_attention_landmarks_backward(const float* kqm, int g_dtype, const void* g, const float* kv,
-                                       const float* inv, float* dkv, float* dkmm, int64_t slices, int64_t rows, int m,
-                                       int d, void* workspace, size_t workspace_bytes, void* stream) {
-  if (int s = check_landmarks(g_dtype, slices, rows, m, d, "attention landmarks backward")) return s;
+int lfamd_attention_landmarks_backward(const float* kqm, int dtype, const void* g, const void* v, const float* kkm,
+                                       const float* w, const float* kv, const float* inv, float* dkqm, float* dkkm,
+                                       void* dv, float* dkv, float* dkmm, int64_t slices, int64_t rows, int m, int d,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (int s = check_landmarks(dtype, slices, rows, m, d, "attention landmarks backward")) return s;
   if (slices == 0) return ok();
-  if (!kqm || !g || !kv || !inv || !dkv || !dkmm || !workspace)
+  if (!kqm || !g || !v || !kkm || !w || !kv || !inv || !dkqm || !dkkm || !dv || !dkv || !dkmm || !workspace)
     return fail(LFAMD_ERR_ARG, "attention landmarks backward: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   int per = 0;
   float* part = static_cast<float*>(workspace);
-  if (int s = tall_t_partials(g_dtype, kqm, g, part, workspace_bytes, slices, rows, m, d, st, &per)) return s;
-  if (m == 49) return launch_bwd_mul<1>(part, per, kv, inv, dkv, dkmm, slices, m, d, st);
-  return launch_bwd_mul<4>(part, per, kv, inv, dkv, dkmm, slices, m, d, st);
+  if (int s = tall_t_partials(dtype, kqm, g, part, workspace_bytes, slices, rows, m, d, st, &per)) return s;
+  if (int s = (m == 49 ? launch_bwd_mul<1>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)
+                       : launch_bwd_mul<4>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)))
+    return s;
+  // dK_qm = g w^T and dK_km = v dkv^T (one shape: one launch), then dv = K_km dkv.
+  const int64_t md = (int64_t)m * d;
+  const void* as[2] = {g, v};
+  const float* bs[2] = {w, dkv};
+  float* cs[2] = {dkqm, dkkm};
+  int s = mix_rows_pair(dtype, as, bs, cs, slices, rows, d, m, d, 1, md, st);
+  if (s == LFAMD_ERR_UNSUPPORTED) {
+    if ((s = lfamd_mix_rows(dtype, g, w, LFAMD_F32, dkqm, slices, rows, d, m, d, 1, md, st))) return s;
+    s = lfamd_mix_rows(dtype, v, dkv, LFAMD_F32, dkkm, slices, rows, d, m, d, 1, md, st);
+  }
+  if (s) return s;
+  return lfamd_mix_rows(LFAMD_F32, kkm, dkv, dtype, dv, slices, rows, m, d, 1, d, md, st);
 }
 
 int lfamd_newton_is_supported(int64_t n) { return n >= 1 && n <= kMaxN ? 1 : 0; }

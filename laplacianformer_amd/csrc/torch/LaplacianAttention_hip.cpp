@@ -116,24 +116,30 @@ bool landmarks_forward(const at::Tensor& k_mm, const at::Tensor& k_km, const at:
   return true;
 }
 
-// Its backward for the gradient g of the output: d_kv and the gradient d_kmm of
-// K_mm from the tall product K_qm^T g (partials), kv and inv, in two launches
-// where the fused path takes the shape; false otherwise.
-bool landmarks_backward(const at::Tensor& k_qm, const at::Tensor& g, const at::Tensor& kv, const at::Tensor& inv,
-                        at::Tensor& d_kv, at::Tensor& d_kmm) {
+// Its backward with the row products around it, for the output gradient g:
+// d_kmm (the gradient of K_mm, through dw = K_qm^T g, kv and inv), d_kqm = g w^T,
+// d_kkm = v dkv^T and d_v = K_km dkv, where the fused path takes the shape;
+// false otherwise.
+bool landmarks_backward(const at::Tensor& g, const at::Tensor& v, const at::Tensor& k_qm, const at::Tensor& k_km,
+                        const at::Tensor& w, const at::Tensor& kv, const at::Tensor& inv, at::Tensor& d_kqm,
+                        at::Tensor& d_kkm, at::Tensor& d_v, at::Tensor& d_kmm) {
   const int64_t B = g.size(0), H = g.size(1), N = g.size(2), d = g.size(3), M = inv.size(2);
-  if (!kv.is_contiguous() || !inv.is_contiguous() || kv.scalar_type() != at::kFloat ||
-      inv.scalar_type() != at::kFloat)
-    return false;
+  for (const at::Tensor* t : {&w, &kv, &inv, &k_qm, &k_km})
+    if (!t->is_contiguous() || t->scalar_type() != at::kFloat) return false;
+  if (!v.is_contiguous() || !g.is_contiguous() || v.scalar_type() != g.scalar_type()) return false;
   at::hip::HIPGuardMasqueradingAsCUDA guard(g.device());
   const size_t wsb = lfamd_tall_t_workspace_size(B * H, N);
-  d_kv = at::empty_like(kv);
+  d_kqm = at::empty_like(k_qm);
+  d_kkm = at::empty_like(k_km);
+  d_v = at::empty_like(v);
   d_kmm = at::empty_like(inv);
+  at::Tensor d_kv = at::empty_like(kv);
   at::Tensor ws = at::empty({(int64_t)wsb}, g.options().dtype(at::kByte));
   const int st = lfamd_attention_landmarks_backward(
-      k_qm.data_ptr<float>(), detail::abi_dtype(g, "laplacian attention backward"), g.data_ptr(),
-      kv.data_ptr<float>(), inv.data_ptr<float>(), d_kv.data_ptr<float>(), d_kmm.data_ptr<float>(), B * H, N,
-      (int)M, (int)d, ws.data_ptr(), wsb, detail::stream_of(g));
+      k_qm.data_ptr<float>(), detail::abi_dtype(g, "laplacian attention backward"), g.data_ptr(), v.data_ptr(),
+      k_km.data_ptr<float>(), w.data_ptr<float>(), kv.data_ptr<float>(), inv.data_ptr<float>(),
+      d_kqm.data_ptr<float>(), d_kkm.data_ptr<float>(), d_v.data_ptr(), d_kv.data_ptr<float>(),
+      d_kmm.data_ptr<float>(), B * H, N, (int)M, (int)d, ws.data_ptr(), wsb, detail::stream_of(g));
   if (st == LFAMD_ERR_UNSUPPORTED) return false;
   detail::check_status(st);
   return true;
@@ -204,17 +210,17 @@ std::vector<at::Tensor> LaplacianAttention_backward(at::Tensor g, std::vector<at
   const int64_t B = k.size(0), H = k.size(1), dd = k.size(3);
   const double s = 1.0 / std::sqrt((double)dd);
   g = g.contiguous();
-  at::Tensor d_kqm = mix_rows(g, w, at::kFloat);                        // G W^T       [B,H,N,M]
-  at::Tensor d_kv, d_kmm;
-  if (!landmarks_backward(k_qm, g, kv, inv, d_kv, d_kmm)) {
+  at::Tensor d_kqm, d_kkm, d_v, d_kmm;
+  if (!landmarks_backward(g, v, k_qm, k_km, w, kv, inv, d_kqm, d_kkm, d_v, d_kmm)) {
+    d_kqm = mix_rows(g, w, at::kFloat);                                  // G W^T       [B,H,N,M]
     at::Tensor d_w = tall_t(k_qm, g);                                    // K_qm^T G    [B,H,M,d]
     at::Tensor d_inv = at::matmul(d_w, kv.transpose(-1, -2));            // [B,H,M,M]
-    d_kv = at::matmul(inv.transpose(-1, -2), d_w);                       // [B,H,M,d]
+    at::Tensor d_kv = at::matmul(inv.transpose(-1, -2), d_w);            // [B,H,M,d]
     d_kmm = at::empty_like(k_mm);
     NewtonInverse_backward(d_inv.contiguous(), inv, d_kmm);
+    d_kkm = mix_rows(v, d_kv, at::kFloat);                               // V dkv^T     [B,H,N,M]
+    d_v = mix_rows(k_km, d_kv.transpose(-1, -2), v.scalar_type());       // K_km dkv    [B,H,N,d]
   }
-  at::Tensor d_kkm = mix_rows(v, d_kv, at::kFloat);                      // V dkv^T     [B,H,N,M]
-  at::Tensor d_v = mix_rows(k_km, d_kv.transpose(-1, -2), v.scalar_type());  // K_km dkv [B,H,N,d]
   at::hip::HIPGuardMasqueradingAsCUDA guard(k.device());
   const int dt = detail::abi_dtype(k, "laplacian attention backward");
   // The three distances' gradients (K_qm, K_km, K_mm share the key km_cm): one

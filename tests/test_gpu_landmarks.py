@@ -66,37 +66,58 @@ def test_landmarks_forward(gpu, slices, rows, m, d, vdt):
     _close(w, i64 @ k64, i64.abs() @ k64.abs(), "w = inv kv")
 
 
-@pytest.mark.parametrize("slices,rows,m,d,gdt", [
+@pytest.mark.parametrize("slices,rows,m,d,dt", [
     (3, 784, 49, 64, "f16"),
     (5, 200, 64, 64, "f32"),
     (4, 96, 56, 16, "bf16"),
     (600, 32, 49, 32, "f16"),
 ])
-def test_landmarks_backward(gpu, slices, rows, m, d, gdt):
+def test_landmarks_backward(gpu, slices, rows, m, d, dt):
     import laplacianformer_amd as lf
 
-    print(f"landmarks backward {slices}x{rows} m={m} d={d} {gdt}", flush=True)
+    print(f"landmarks backward {slices}x{rows} m={m} d={d} {dt}", flush=True)
     lib = lf.capi()
-    kmm, kqm, g = _inputs(slices, rows, m, d, gdt, 21 + m + d, gpu)
+    kmm, kqm, g = _inputs(slices, rows, m, d, dt, 21 + m + d, gpu)
+    _, kkm, v = _inputs(slices, rows, m, d, dt, 31 + m + d, gpu)
     inv = torch.empty_like(kmm)
     lf.check(lib.lfamd_newton_forward(0, kmm.data_ptr(), inv.data_ptr(), slices, m, 10, None, 0, None))
-    kv = torch.randn((slices, m, d), generator=torch.Generator().manual_seed(5)).to(gpu)
+    gen = torch.Generator().manual_seed(5)
+    kv = torch.randn((slices, m, d), generator=gen).to(gpu)
+    w = torch.randn((slices, m, d), generator=gen).to(gpu)
     wsb = lib.lfamd_tall_t_workspace_size(slices, rows)
     ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    dkqm = torch.empty((slices, rows, m), device=gpu)
+    dkkm = torch.empty_like(dkqm)
+    dv = torch.empty_like(v)
     dkv = torch.empty_like(kv)
     dkmm = torch.empty_like(kmm)
-    gt = lf.dtype_code(g.dtype)
-    lf.check(lib.lfamd_attention_landmarks_backward(kqm.data_ptr(), gt, g.data_ptr(), kv.data_ptr(), inv.data_ptr(),
-                                                    dkv.data_ptr(), dkmm.data_ptr(), slices, rows, m, d,
-                                                    ws.data_ptr(), wsb, None))
+    code = lf.dtype_code(g.dtype)
+    lf.check(lib.lfamd_attention_landmarks_backward(
+        kqm.data_ptr(), code, g.data_ptr(), v.data_ptr(), kkm.data_ptr(), w.data_ptr(), kv.data_ptr(), inv.data_ptr(),
+        dkqm.data_ptr(), dkkm.data_ptr(), dv.data_ptr(), dkv.data_ptr(), dkmm.data_ptr(), slices, rows, m, d,
+        ws.data_ptr(), wsb, None))
+    # The unfused operations: the tall product (dw) and the row products one call each.
     dw = torch.empty_like(kv)
-    lf.check(lib.lfamd_tall_t(gt, kqm.data_ptr(), g.data_ptr(), dw.data_ptr(), slices, rows, m, d, ws.data_ptr(), wsb,
+    lf.check(lib.lfamd_tall_t(code, kqm.data_ptr(), g.data_ptr(), dw.data_ptr(), slices, rows, m, d, ws.data_ptr(), wsb,
                               None))
+    md = m * d
+    r_kqm, r_kkm, r_dv = torch.empty_like(dkqm), torch.empty_like(dkkm), torch.empty_like(dv)
+    lf.check(lib.lfamd_mix_rows(code, g.data_ptr(), w.data_ptr(), 0, r_kqm.data_ptr(), slices, rows, d, m, d, 1, md,
+                                None))
+    lf.check(lib.lfamd_mix_rows(code, v.data_ptr(), dkv.data_ptr(), 0, r_kkm.data_ptr(), slices, rows, d, m, d, 1, md,
+                                None))
+    lf.check(lib.lfamd_mix_rows(0, kkm.data_ptr(), dkv.data_ptr(), code, r_dv.data_ptr(), slices, rows, m, d, 1, d, md,
+                                None))
     torch.cuda.synchronize()
+    # The paired launch runs the same per-row arithmetic as one call per product.
+    assert torch.equal(dkqm, r_kqm), "g w^T differs from lfamd_mix_rows"
+    assert torch.equal(dkkm, r_kkm), "v dkv^T differs from lfamd_mix_rows"
+    assert torch.equal(dv, r_dv), "k_km dkv differs from lfamd_mix_rows"
     i64, k64, w64 = inv.double(), kv.double(), dw.double()
-    _close(dkv, i64.transpose(1, 2) @ w64, i64.abs().transpose(1, 2) @ w64.abs(), "dkv = inv^T dw")
+    wabs = kqm.double().abs().transpose(1, 2) @ g.double().abs()
+    _close(dkv, i64.transpose(1, 2) @ w64, i64.abs().transpose(1, 2) @ wabs, "dkv = inv^T dw")
     dinv = w64 @ k64.transpose(1, 2)
-    dinv_abs = w64.abs() @ k64.abs().transpose(1, 2)
+    dinv_abs = wabs @ k64.abs().transpose(1, 2)
     ref = -(i64.transpose(1, 2) @ dinv) @ i64.transpose(1, 2)
     scale = (i64.abs().transpose(1, 2) @ dinv_abs) @ i64.abs().transpose(1, 2)
     _close(dkmm, ref, scale, "dkmm = -(inv^T dinv) inv^T")
@@ -119,7 +140,7 @@ def test_landmarks_unsupported(gpu):
         rc = lib.lfamd_attention_landmarks_forward(kmm.data_ptr(), kkm.data_ptr(), 0, vptr, p, p, p, slices, rows, m,
                                                    dd, 10, ws.data_ptr(), wsb, None)
         assert rc == UNSUPPORTED, (m, dd, rc)
-        rc = lib.lfamd_attention_landmarks_backward(kkm.data_ptr(), 0, vptr, p, p, p, p, slices, rows, m, dd,
-                                                    ws.data_ptr(), wsb, None)
+        rc = lib.lfamd_attention_landmarks_backward(kkm.data_ptr(), 0, vptr, vptr, kkm.data_ptr(), p, p, p, p, p, p, p,
+                                                    p, slices, rows, m, dd, ws.data_ptr(), wsb, None)
         assert rc == UNSUPPORTED, (m, dd, rc)
     torch.cuda.synchronize()
