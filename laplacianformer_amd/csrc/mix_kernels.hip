@@ -358,19 +358,29 @@ mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* 
   mix_rows_bf16_body<TA, TC, DIRECT>(A, B, C, N, P, Q, sq, sp, bStride, blockIdx.y, blockIdx.x, gridDim.x);
 }
 
-// Two products of one shape in one launch (two operand sets; grid (workgroups
-// per slice, 2 * slices), the second set's workgroups after the first's).
-struct MixPair {
-  const void* A[2];
-  const float* B[2];
-  void* C[2];
+// Three row products in one launch (grid (workgroups per slice, 3 * slices),
+// each product's workgroups after the previous one's): products 0 and 1 of one
+// shape, A of element type TA [N][P0] and fp32 C [N][Q0]; product 2 with fp32 A
+// [N][P1] and C of element type TA [N][Q1] (the attention layer's g w^T,
+// v dkv^T and K_km dkv).
+struct MixTrio {
+  const void* A[3];
+  const float* B[3];
+  void* C[3];
+  int P[2], Q[2];
+  int64_t sq[2], sp[2], bStride[2];
 };
-template <typename TA, typename TC, bool DIRECT>
+template <typename TA, bool DIRECT01>
 __global__ void __launch_bounds__(64 * kMixWaves)
-mix_rows_bf16_pair_kernel(MixPair pr, int slices, int N, int P, int Q, int64_t sq, int64_t sp, int64_t bStride) {
-  const int src = (int)blockIdx.y >= slices ? 1 : 0;
-  mix_rows_bf16_body<TA, TC, DIRECT>(static_cast<const TA*>(pr.A[src]), pr.B[src], static_cast<TC*>(pr.C[src]), N,
-                                     P, Q, sq, sp, bStride, (int)blockIdx.y - src * slices, blockIdx.x, gridDim.x);
+mix_rows_bf16_trio_kernel(MixTrio t, int slices, int N) {
+  const int src = (int)blockIdx.y / slices, s = (int)blockIdx.y - src * slices;
+  if (src < 2)
+    mix_rows_bf16_body<TA, float, DIRECT01>(static_cast<const TA*>(t.A[src]), t.B[src], static_cast<float*>(t.C[src]),
+                                            N, t.P[0], t.Q[0], t.sq[0], t.sp[0], t.bStride[0], s, blockIdx.x,
+                                            gridDim.x);
+  else
+    mix_rows_bf16_body<float, TA, false>(static_cast<const float*>(t.A[2]), t.B[2], static_cast<TA*>(t.C[2]), N,
+                                         t.P[1], t.Q[1], t.sq[1], t.sp[1], t.bStride[1], s, blockIdx.x, gridDim.x);
 }
 
 // Workgroups per slice. The bf16 kernel: one kMixWaves-wave workgroup per CU
@@ -688,40 +698,43 @@ int launch_tall_t(const float* A, const void* B, float* C, float* ws, int64_t sl
   return check_launch("tall product reduction");
 }
 
-// Two row products of one shape (A of element type a_dtype [slices][N][P], B
-// fp32 through strides, C fp32 [slices][N][Q]) in one launch of the bf16
-// kernel: about one workgroup per CU for both. LFAMD_ERR_UNSUPPORTED where the
-// bf16 kernel does not take the operands (the caller then makes two calls).
-int mix_rows_pair(int a_dtype, const void* const* A, const float* const* B, float* const* C, int64_t slices,
-                  int64_t N, int P, int Q, int64_t sq, int64_t sp, int64_t bStride, hipStream_t st) {
-  const int64_t es = a_dtype == LFAMD_F32 ? 4 : 2;
-  bool direct = P == kMixPMax, rows16 = (N * P * es) % 16 == 0;
+// The three row products of MixTrio in one launch of the bf16 kernel (about one
+// workgroup per CU per product). LFAMD_ERR_UNSUPPORTED where the bf16 kernel
+// does not take an operand (the caller then makes one call per product).
+int mix_rows_trio(int dtype, const void* const* A, const float* const* B, void* const* C, int64_t slices, int64_t N,
+                  const int* P, const int* Q, const int64_t* sq, const int64_t* sp, const int64_t* bStride,
+                  hipStream_t st) {
+  const int64_t es = dtype == LFAMD_F32 ? 4 : 2;
+  bool direct = P[0] == kMixPMax, rows16 = (N * P[0] * es) % 16 == 0;
   for (int i = 0; i < 2; ++i)
     if ((reinterpret_cast<uintptr_t>(A[i]) & 15) != 0) direct = rows16 = false;
-  if (!(direct || rows16) || slices < 1 || N < 1 || 2 * slices > 65535 || P > kMixPMax || Q > kMixPMax)
-    return fail(LFAMD_ERR_UNSUPPORTED, "row product pair: operands the bf16 kernel does not take");
-  const MixPair pr{{A[0], A[1]}, {B[0], B[1]}, {C[0], C[1]}};
+  const bool two16 = (reinterpret_cast<uintptr_t>(A[2]) & 15) == 0 && (N * P[1] * 4) % 16 == 0;
+  if (!(direct || rows16) || !two16 || slices < 1 || N < 1 || 3 * slices > 65535)
+    return fail(LFAMD_ERR_UNSUPPORTED, "row product trio: operands the bf16 kernel does not take");
+  for (int i = 0; i < 2; ++i)
+    if (P[i] > kMixPMax || Q[i] > kMixPMax || P[i] < 1 || Q[i] < 1)
+      return fail(LFAMD_ERR_UNSUPPORTED, "row product trio: widths above %d", kMixPMax);
+  const MixTrio t{{A[0], A[1], A[2]}, {B[0], B[1], B[2]}, {C[0], C[1], C[2]}, {P[0], P[1]}, {Q[0], Q[1]},
+                  {sq[0], sq[1]}, {sp[0], sp[1]}, {bStride[0], bStride[1]}};
   const int64_t groups = (N + kMixGroup - 1) / kMixGroup;
   const int64_t per = std::max<int64_t>(
-      1, std::min<int64_t>((groups + kMixWaves - 1) / kMixWaves, ((int64_t)num_cus() + 2 * slices - 1) / (2 * slices)));
-  const dim3 grid((unsigned)per, (unsigned)(2 * slices)), block(64 * kMixWaves);
-#define LFAMD_PAIR(TA)                                                                                          \
-  do {                                                                                                          \
-    if (direct)                                                                                                 \
-      hipLaunchKernelGGL((mix_rows_bf16_pair_kernel<TA, float, true>), grid, block, 0, st, pr, (int)slices,     \
-                         (int)N, P, Q, sq, sp, bStride);                                                        \
-    else                                                                                                        \
-      hipLaunchKernelGGL((mix_rows_bf16_pair_kernel<TA, float, false>), grid, block, 0, st, pr, (int)slices,    \
-                         (int)N, P, Q, sq, sp, bStride);                                                        \
+      1, std::min<int64_t>((groups + kMixWaves - 1) / kMixWaves, ((int64_t)num_cus() + 3 * slices - 1) / (3 * slices)));
+  const dim3 grid((unsigned)per, (unsigned)(3 * slices)), block(64 * kMixWaves);
+#define LFAMD_TRIO(TA)                                                                                             \
+  do {                                                                                                             \
+    if (direct)                                                                                                    \
+      hipLaunchKernelGGL((mix_rows_bf16_trio_kernel<TA, true>), grid, block, 0, st, t, (int)slices, (int)N);      \
+    else                                                                                                           \
+      hipLaunchKernelGGL((mix_rows_bf16_trio_kernel<TA, false>), grid, block, 0, st, t, (int)slices, (int)N);     \
   } while (0)
-  switch (a_dtype) {
-    case LFAMD_F32: LFAMD_PAIR(float); break;
-    case LFAMD_F16: LFAMD_PAIR(f16s); break;
-    case LFAMD_BF16: LFAMD_PAIR(bf16s); break;
-    default: return fail(LFAMD_ERR_DTYPE, "row product pair: unsupported dtype %d", a_dtype);
+  switch (dtype) {
+    case LFAMD_F32: LFAMD_TRIO(float); break;
+    case LFAMD_F16: LFAMD_TRIO(f16s); break;
+    case LFAMD_BF16: LFAMD_TRIO(bf16s); break;
+    default: return fail(LFAMD_ERR_DTYPE, "row product trio: unsupported dtype %d", dtype);
   }
-#undef LFAMD_PAIR
-  return check_launch("row product pair");
+#undef LFAMD_TRIO
+  return check_launch("row product trio");
 }
 
 // The bf16 tall product's per-workgroup partials only ([slices][per][64][64]

@@ -1323,17 +1323,17 @@ int lfamd_attention_landmarks_backward(const float* kqm, int dtype, const void* 
   if (int s = (m == 49 ? launch_bwd_mul<1>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)
                        : launch_bwd_mul<4>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)))
     return s;
-  // dK_qm = g w^T and dK_km = v dkv^T (one shape: one launch), then dv = K_km dkv.
+  // dK_qm = g w^T, dK_km = v dkv^T and dv = K_km dkv in one launch.
   const int64_t md = (int64_t)m * d;
-  const void* as[2] = {g, v};
-  const float* bs[2] = {w, dkv};
-  float* cs[2] = {dkqm, dkkm};
-  int s = mix_rows_pair(dtype, as, bs, cs, slices, rows, d, m, d, 1, md, st);
-  if (s == LFAMD_ERR_UNSUPPORTED) {
-    if ((s = lfamd_mix_rows(dtype, g, w, LFAMD_F32, dkqm, slices, rows, d, m, d, 1, md, st))) return s;
-    s = lfamd_mix_rows(dtype, v, dkv, LFAMD_F32, dkkm, slices, rows, d, m, d, 1, md, st);
-  }
-  if (s) return s;
+  const void* as[3] = {g, v, kkm};
+  const float* bs[3] = {w, dkv, dkv};
+  void* cs[3] = {dkqm, dkkm, dv};
+  const int P[2] = {d, m}, Q[2] = {m, d};
+  const int64_t sq[2] = {d, 1}, sp[2] = {1, d}, bstr[2] = {md, md};
+  int s = mix_rows_trio(dtype, as, bs, cs, slices, rows, P, Q, sq, sp, bstr, st);
+  if (s != LFAMD_ERR_UNSUPPORTED) return s;
+  if ((s = lfamd_mix_rows(dtype, g, w, LFAMD_F32, dkqm, slices, rows, d, m, d, 1, md, st))) return s;
+  if ((s = lfamd_mix_rows(dtype, v, dkv, LFAMD_F32, dkkm, slices, rows, d, m, d, 1, md, st))) return s;
   return lfamd_mix_rows(LFAMD_F32, kkm, dkv, dtype, dv, slices, rows, m, d, 1, d, md, st);
 }
 

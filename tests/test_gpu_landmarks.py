@@ -109,7 +109,7 @@ def test_landmarks_backward(gpu, slices, rows, m, d, dt):
     lf.check(lib.lfamd_mix_rows(0, kkm.data_ptr(), dkv.data_ptr(), code, r_dv.data_ptr(), slices, rows, m, d, 1, d, md,
                                 None))
     torch.cuda.synchronize()
-    # The paired launch runs the same per-row arithmetic as one call per product.
+    # The one launch of the three products runs the same per-row arithmetic as one call each.
     assert torch.equal(dkqm, r_kqm), "g w^T differs from lfamd_mix_rows"
     assert torch.equal(dkkm, r_kkm), "v dkv^T differs from lfamd_mix_rows"
     assert torch.equal(dv, r_dv), "k_km dkv differs from lfamd_mix_rows"
