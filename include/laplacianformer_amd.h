@@ -246,12 +246,12 @@ int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t s
  * as lfamd_newton_forward), kv = kkm^T v (kkm [rows][m], v [rows][d] of element type v_dtype: F32,
  * F16 or BF16; kv [m][d]) and w = inv kv ([m][d]). Backward, for the layer's output gradient g
  * ([rows][d], element type dtype, as v): dw = kqm^T g, dinv = dw kv^T, dkv = inv^T dw ([m][d]),
- * dkmm = -(inv^T dinv) inv^T ([m][m], as lfamd_newton_backward), then dkqm = g w^T and
- * dkkm = v dkv^T ([rows][m], one launch) and dv = kkm dkv ([rows][d], element type dtype). The
+ * dkmm = -(inv^T dinv) inv^T ([m][m], as lfamd_newton_backward), then, in one launch,
+ * dkqm = g w^T, dkkm = v dkv^T ([rows][m]) and dv = kkm dkv ([rows][d], element type dtype). The
  * tall products need 16-byte aligned slices (LFAMD_ERR_UNSUPPORTED otherwise) and
  * lfamd_tall_t_workspace_size(slices, rows) bytes of workspace. No reference counterpart: they
  * replace, for the layer, the tall products' reductions, the three m x m products and the two
- * NewtonInverse launches, and pair two of the row products in one launch. */
+ * NewtonInverse launches, and run the three backward row products in one launch. */
 int lfamd_attention_landmarks_forward(const float* kmm, const float* kkm, int v_dtype, const void* v, float* inv,
                                       float* kv, float* w, int64_t slices, int64_t rows, int m, int d, int iters,
                                       void* workspace, size_t workspace_bytes, void* stream);
