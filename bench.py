@@ -515,7 +515,7 @@ K_FWD = "lfamd::(anonymous namespace)::laplace_fwd2_kernel<lfamd::f16s, 0, 16>"
 K_BWD = "lfamd::(anonymous namespace)::laplace_bwd2_kernel<lfamd::f16s, 49, true, true, false>"
 K_RED = "lfamd::(anonymous namespace)::laplace_dk_reduce_t_kernel<lfamd::f16s>"
 K_NF = "lfamd::newton_fwd_kernel<float, 64, true, 2, 4>"
-K_NB = "lfamd::newton_bwd_kernel<float, 64, 4, 4>"
+K_NB = "lfamd::newton_bwd_pipe_kernel<float, 64>"
 
 
 def _ms(st):

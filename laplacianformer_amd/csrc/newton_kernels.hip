@@ -638,6 +638,172 @@ newton_bwd_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __re
     }
 }
 
+// The chained product pair of one wave (strip w) on full NP x NP matrices in LDS
+// (V row-major, G^T row-major, row stride NP + 4): acc2 = R[16w.., :] = (V^T G V^T)
+// rows, lane (i, g) holding R[16w + 4g + r][16 t + i] in acc2[t][r]. Each k block's
+// operands are read while the previous block's MFMAs run (two register sets; the
+// scheduling fences keep the reads ahead), and consecutive MFMAs go to different
+// accumulators.
+template <int NP>
+__device__ __forceinline__ void chain_products(const float* __restrict__ Vs, const float* __restrict__ Gts, int w,
+                                               int lane, v4f (&acc2)[NP / 16]) {
+  using L = NsLayout<NP, 1>;
+  constexpr int NT = L::NT;
+  const int li = lane & 15, lg = lane >> 4;
+  v4f acc1[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc1[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  // S^T[:, 16w..16w+16) = G^T V[:, 16w..16w+16): k over the rows of G and V.
+  float4 a[2][NT];
+  float b[2][4];
+#pragma unroll
+  for (int kk = 0; kk <= NT; ++kk) {
+    if (kk < NT) {
+      const int kb = 16 * kk + 4 * lg, nb = kk & 1;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[nb][s] = Vs[(kb + s) * L::LS + 16 * w + li];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) a[nb][t] = *reinterpret_cast<const float4*>(&Gts[(16 * t + li) * L::LS + kb]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kk > 0) {
+      const int cb = (kk - 1) & 1;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc1[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[cb][t].x, b[cb][0], acc1[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc1[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[cb][t].y, b[cb][1], acc1[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc1[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[cb][t].z, b[cb][2], acc1[t], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc1[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[cb][t].w, b[cb][3], acc1[t], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // R = S V^T: block t's A operand is acc1[t] (k = 16t + 4g + r), B = V rows as 16-byte reads.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc2[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  float4 vb[2][NT];
+#pragma unroll
+  for (int kk = 0; kk <= NT; ++kk) {
+    if (kk < NT) {
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2)
+        vb[kk & 1][t2] = *reinterpret_cast<const float4*>(&Vs[(16 * t2 + li) * L::LS + 16 * kk + 4 * lg]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kk > 0) {
+      const int t = kk - 1, cb = t & 1;
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2) acc2[t2] = __builtin_amdgcn_mfma_f32_16x16x4f32(acc1[t][0], vb[cb][t2].x, acc2[t2], 0, 0, 0);
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2) acc2[t2] = __builtin_amdgcn_mfma_f32_16x16x4f32(acc1[t][1], vb[cb][t2].y, acc2[t2], 0, 0, 0);
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2) acc2[t2] = __builtin_amdgcn_mfma_f32_16x16x4f32(acc1[t][2], vb[cb][t2].z, acc2[t2], 0, 0, 0);
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2) acc2[t2] = __builtin_amdgcn_mfma_f32_16x16x4f32(acc1[t][3], vb[cb][t2].w, acc2[t2], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Four consecutive elements at p (16-byte aligned for float, 8-byte for the 16-bit types) as fp32.
+template <typename T>
+__device__ __forceinline__ float4 load4_acc(const T* __restrict__ p) {
+  if constexpr (std::is_same<T, float>::value) {
+    return *reinterpret_cast<const float4*>(p);
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    T e[4];
+    __builtin_memcpy(e, &u, sizeof(e));
+    return float4{to_acc(e[0]), to_acc(e[1]), to_acc(e[2]), to_acc(e[3])};
+  }
+}
+
+// Bounded wait on a workgroup counter in LDS: returns once *c >= target. Every
+// counter this kernel waits on is raised by waves of the same workgroup whose own
+// waits point only at earlier matrices, so every wait ends.
+__device__ __forceinline__ void lds_wait_ge(int* c, int target) {
+  while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+}
+
+__device__ __forceinline__ void lds_raise(int* c, int lane) {
+  if (lane == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Four matrices' slots of two NP x (NP + 4) fp32 buffers and 9 counters.
+template <int NP> constexpr size_t pipe_lds() { return 4 * 2 * (size_t)NsLayout<NP>::ELEMS * 4 + 12 * sizeof(int); }
+
+// NewtonInverse backward for full 64 x 64 matrices, dA = -(V^T G) V^T, several per
+// CU: one persistent workgroup per CU of four teams (4 waves each), team q taking
+// the workgroup's matrices r = q, q + 4, ... through LDS slot q.
+// * The two products chain in registers (chain_products): wave w of a team computes
+//   the column strip w of S^T = G^T V, which is the A operand of its rows of
+//   R = S V^T, so S never goes through LDS and the team meets only once per matrix,
+//   after staging V row-major and G transposed.
+// * Matrix r's loads are issued only after every wave has issued matrix r - 1's, so
+//   a CU's requests reach the memory system in matrix order (all of them in flight
+//   at once); each team's products start as soon as its own matrix is in LDS.
+// Counters (each raised once per wave and matrix): issued (loads issued, in matrix
+// order), ready[q] (waves of team q that wrote their share of the slot) and done[q]
+// (waves of team q that finished reading it).
+template <typename T, int NP>
+__global__ void __launch_bounds__(1024)
+newton_bwd_pipe_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T* __restrict__ gmat, int64_t bh,
+                       int per) {
+  using L = NsLayout<NP, 1>;
+  constexpr int NT = L::NT, TEAM_THREADS = NP * 4;
+  static_assert(NP == 64, "four teams of four waves");
+  extern __shared__ __align__(16) float nsm[];
+  int* ready = reinterpret_cast<int*>(nsm + 4 * 2 * L::ELEMS);
+  int* done = ready + 4;
+  int* issued = ready + 8;
+  const int team = uniform(threadIdx.x >> 8), w = uniform((threadIdx.x >> 6) & 3), lane = threadIdx.x & 63;
+  const int tt = threadIdx.x & (TEAM_THREADS - 1);
+  const int li = lane & 15, lg = lane >> 4;
+  if (threadIdx.x < 9) ready[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t m0 = (int64_t)blockIdx.x * per;
+  const int cnt = (int)(bh - m0 < per ? bh - m0 : per);
+  float* Vs = nsm + team * 2 * L::ELEMS;
+  float* Gts = Vs + L::ELEMS;
+  constexpr int GROUPS = NP * NP / 4, PER = GROUPS / TEAM_THREADS;
+  for (int r = team, k = 0; r < cnt; r += 4, ++k) {
+    // Issue order only (no data is read through this counter), so relaxed.
+    while (__hip_atomic_load(issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 4 * r) __builtin_amdgcn_s_sleep(1);
+    const size_t off = (size_t)(m0 + r) * NP * NP;
+    float4 vv[PER], gg[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int c = q * TEAM_THREADS + tt;
+      vv[q] = load4_acc(inv + off + (size_t)(c / (NP / 4)) * NP + 4 * (c % (NP / 4)));
+      gg[q] = load4_acc(gout + off + (size_t)(16 * (c / (16 * NP / 4)) + (c & 15)) * NP + 4 * ((c >> 4) % (NP / 4)));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // raised after the load instructions, not after their data
+    if (lane == 0) __hip_atomic_fetch_add(issued, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (k > 0) lds_wait_ge(&done[team], 4 * k);  // the team's previous matrix has left the slot
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int c = q * TEAM_THREADS + tt;
+      *reinterpret_cast<float4*>(&Vs[(c / (NP / 4)) * L::LS + 4 * (c % (NP / 4))]) = vv[q];
+      const int gi = 16 * (c / (16 * NP / 4)) + (c & 15), gj = 4 * ((c >> 4) % (NP / 4));
+      Gts[(gj + 0) * L::LS + gi] = gg[q].x;
+      Gts[(gj + 1) * L::LS + gi] = gg[q].y;
+      Gts[(gj + 2) * L::LS + gi] = gg[q].z;
+      Gts[(gj + 3) * L::LS + gi] = gg[q].w;
+    }
+    lds_raise(&ready[team], lane);
+    lds_wait_ge(&ready[team], 4 * (k + 1));
+    v4f acc2[NT];
+    chain_products<NP>(Vs, Gts, w, lane, acc2);
+    lds_raise(&done[team], lane);
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2)
+#pragma unroll
+      for (int r2 = 0; r2 < 4; ++r2)
+        gmat[off + (size_t)(16 * w + 4 * lg + r2) * NP + 16 * t2 + li] = from_acc<T>(-acc2[t2][r2]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // fp64: VALU products, 2-buffer (VP)V order, one workgroup of 256 threads per
 // matrix. Slot A holds P, then W = VP; P is reloaded each iteration.
@@ -1156,8 +1322,31 @@ int fwd_np_w(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
   return check_launch("newton forward");
 }
 
+// 64 x 64 fp32 matrices, 2 to 8 per CU: the persistent issue-ordered kernel (1024 x 64^2:
+// 14.25 against 14.6 us; 600 and 1000 matrices 4.6-6 % faster; at 16 per CU, 44.8 against
+// 44.1 us, the one-matrix-per-workgroup kernel stays).
+template <typename T, int NP>
+bool use_pipe(int64_t bh, int n) {
+  return std::is_same<T, float>::value && NP == 64 && n == NP && bh > (int64_t)num_cus() &&
+         bh <= 8 * (int64_t)num_cus();
+}
+
+template <typename T, int NP>
+int bwd_np_pipe(const T* g, const T* v, T* o, int64_t bh, hipStream_t st) {
+  auto k = newton_bwd_pipe_kernel<T, NP>;
+  int s = set_lds(k, pipe_lds<NP>());
+  if (s) return s;
+  const int64_t cus = num_cus();
+  const int per = (int)((bh + cus - 1) / cus);
+  const int64_t grid = (bh + per - 1) / per;
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(1024), pipe_lds<NP>(), st, g, v, o, bh, per);
+  return check_launch("newton backward");
+}
+
 template <typename T, int NP, int WPR>
 int bwd_np_w(const T* g, const T* v, T* o, int64_t bh, int n, hipStream_t st) {
+  if constexpr (std::is_same<T, float>::value && NP == 64)
+    if (use_pipe<T, NP>(bh, n)) return bwd_np_pipe<T, NP>(g, v, o, bh, st);
   auto k = newton_bwd_kernel<T, NP, WPR>;
   if constexpr (has_kl1<T, NP>())
     if (n == NP - 15) k = newton_bwd_kernel<T, NP, WPR, 1>;

@@ -99,6 +99,21 @@ def test_newton_config3(gpu):
     assert (r_gpu - r_ref).abs().max().item() <= 1e-4 * 8
 
 
+@pytest.mark.parametrize("bh", [257, 600, 1000, 2048])
+def test_newton_backward_persistent(gpu, bh):
+    """Full 64 x 64 fp32 matrices at 2 to 8 per CU take the persistent backward (one
+    workgroup per CU, its matrices through four LDS slots in turn); counts that leave
+    the last workgroup short, against the oracle."""
+    import laplacianformer_amd as lf
+
+    print(f"newton backward persistent bh={bh}", flush=True)
+    V = gen((bh, 1, 64, 64), 40 + bh, "f32", scale=0.3)
+    G = gen((bh, 1, 64, 64), 41 + bh, "f32")
+    out = torch.empty_like(V, device=gpu)
+    lf.ext().NewtonInverse_backward(G.to(gpu), V.to(gpu), out)
+    assert_newton_close(out, oracle.newton_backward(G, V, "f32"), "f32", f"bwd persistent bh={bh}", rtol=1e-5)
+
+
 def test_newton_closed_forms(gpu):
     """Diagonal A = c I: X_k = (1 - (-0.8)^(2^k)) / mu * I with mu = c + 0.01; and iter = 0 gives alpha P."""
     import laplacianformer_amd as lf
