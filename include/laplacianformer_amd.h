@@ -241,8 +241,9 @@ int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t s
                  int inner, int cols, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The attention layer's landmark products around NewtonInverse, for m landmarks with 48 < m <= 64
- * and width d <= 64 (else LFAMD_ERR_UNSUPPORTED), fp32 [slices][...] contiguous unless stated, one
- * workgroup per slice in the fused kernels. Forward: inv = NewtonInverse(kmm, iters) (kmm [m][m],
+ * and width d <= 64 (else LFAMD_ERR_UNSUPPORTED), fp32 [slices][...] contiguous unless stated.
+ * Forward (NewtonInverse and the tall product's partials in one launch, then one for kv and w):
+ * inv = NewtonInverse(kmm, iters) (kmm [m][m],
  * as lfamd_newton_forward), kv = kkm^T v (kkm [rows][m], v [rows][d] of element type v_dtype: F32,
  * F16 or BF16; kv [m][d]) and w = inv kv ([m][d]). Backward, for the layer's output gradient g
  * ([rows][d], element type dtype, as v): dw = kqm^T g, dinv = dw kv^T, dkv = inv^T dw ([m][d]),
@@ -251,7 +252,8 @@ int lfamd_tall_t(int b_dtype, const float* a, const void* b, float* c, int64_t s
  * tall products need 16-byte aligned slices (LFAMD_ERR_UNSUPPORTED otherwise) and
  * lfamd_tall_t_workspace_size(slices, rows) bytes of workspace. No reference counterpart: they
  * replace, for the layer, the tall products' reductions, the three m x m products and the two
- * NewtonInverse launches, and run the three backward row products in one launch. */
+ * NewtonInverse launches, run the forward's tall product beside NewtonInverse, and run the three
+ * backward row products in one launch. */
 int lfamd_attention_landmarks_forward(const float* kmm, const float* kkm, int v_dtype, const void* v, float* inv,
                                       float* kv, float* w, int64_t slices, int64_t rows, int m, int d, int iters,
                                       void* workspace, size_t workspace_bytes, void* stream);

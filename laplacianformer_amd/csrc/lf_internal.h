@@ -74,6 +74,9 @@ int f2_launch_multi(int dtype, int nsrc, const void* const* q, const int64_t* n,
 
 // The bf16 tall product's per-workgroup partials (mix_kernels.hip): [slices][per][64][64]
 // fp32, entry [p][q] = sum over a workgroup's rows of a[n][p] * b[n][q]; *perOut = per.
+// Checks a tall product's partial launch (tall_t_partials) and gives its workgroups per slice.
+int tall_t_check(int b_dtype, const float* A, const void* B, size_t wsBytes, int64_t slices, int64_t N, int P, int Q,
+                 int* perOut);
 int tall_t_partials(int b_dtype, const float* A, const void* B, float* ws, size_t wsBytes, int64_t slices,
                     int64_t N, int P, int Q, hipStream_t st, int* perOut);
 

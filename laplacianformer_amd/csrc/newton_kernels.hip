@@ -22,6 +22,7 @@
 
 #include "lf_common.h"
 #include "lf_internal.h"
+#include "mix_common.h"
 
 namespace lfamd {
 
@@ -273,7 +274,7 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
 // The forward variant whose U = V T reads V from registers (see the loop): the
 // one-live-row path with four waves per strip (its VGPR count still lets two
 // workgroups share a CU, as the wide layout assumes).
-template <int NP, int WPR, int KL> constexpr bool fwd_va() { return KL == 1 && WPR == 4; }
+template <int NP, int WPR, int KL> constexpr bool fwd_va() { return KL == 1 && WPR >= 2; }
 
 // PV_FIRST: V <- 2V - V(PV) (the reference's order for n <= 112), P held in
 // registers as this wave's A operand after the set-up, so the LDS holds V and
@@ -352,7 +353,7 @@ __device__ __forceinline__ void newton_fwd_body(const T* __restrict__ mat, T* __
     __syncthreads();  // P fully read (registers) and V0 written before slot P becomes T
     float* Ts = Ps;
     const int t0v = (wave % WPR) * L::TW, li = lane & 15, lk = lane >> 4;
-    // VA (one live row, four waves per strip): U = V T takes its A operand (the
+    // VA (one live row, two or four waves per strip): U = V T takes its A operand (the
     // strip's V rows; row r1 on the row waves) from registers loaded while T is
     // computed, so no wave reads V from LDS after T is complete and the update
     // needs no barrier ahead of it.
@@ -457,18 +458,18 @@ newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int ite
 }
 
 // ---------------------------------------------------------------------------
-// The attention layer's landmark products around NewtonInverse, fused into it
-// (no reference counterpart: the reference ships the operators only). With
-// Kmm the layer's m x m landmark kernel, 48 < m <= 64 (the 64 bucket), d <= 64,
-// fp32, one workgroup per slice:
-//   forward:  X = NewtonInverse(Kmm); kv = sum of the tall product's
-//             per-workgroup partials of K_km^T V (in workgroup order);
-//             W = X kv                                   (X, kv, W written)
+// The attention layer's landmark products around NewtonInverse (no reference
+// counterpart: the reference ships the operators only). With Kmm the layer's
+// m x m landmark kernel, 48 < m <= 64 (the 64 bucket), d <= 64, fp32:
+//   forward:  X = NewtonInverse(Kmm) beside the tall product's per-workgroup
+//             partials of K_km^T V in one launch (newton_fwd_tall_kernel);
+//             then kv = sum of the partials (in workgroup order), W = X kv
+//             (landmark_kv_w_kernel)                     (X, kv, W written)
 //   backward: dw = sum of the partials of K_qm^T G; then
 //             dX = dw kv^T,  dkv = X^T dw,  dKmm = -(X^T dX) X^T
-//             (dkv, dKmm written)
-// so that the partial sums, the m x m products and the inverse's gradient
-// input never make a round trip through HBM or a launch of their own.
+//             (newton_bwd_mul_kernel, one workgroup per slice; dkv, dKmm written)
+// so that the m x m products and the inverse's gradient input never make a
+// round trip through HBM or a launch of their own.
 // Partials: [slice][per][64][64] fp32, entry [p][q] (landmark p, channel q);
 // entries outside m x d are not read as data (set to zero here).
 
@@ -504,22 +505,71 @@ __device__ __forceinline__ void store_tiles(float* __restrict__ dst, int wave, i
     }
 }
 
+// The landmark forward in two launches. First, workgroups [0, bh) run
+// NewtonInverse on the bh landmark matrices (newton_fwd_body, writing the
+// inverse) and workgroups [bh, bh (1 + per)) the tall product's partials of
+// K_km^T V (tall_t_bf16_body, per workgroups per slice): the two sets share
+// nothing, so the memory-bound tall product runs on the CUs that the
+// latency-bound iterations leave free. Then landmark_kv_w_kernel sums the
+// partials into kv (in workgroup order) and forms W = inv kv. One block size
+// serves both roles: 512 threads, two waves per 16-row strip of NewtonInverse
+// (the tall body needs more registers than 1024-thread blocks allow).
+template <int NP, int KL, typename TB>
+__global__ void __launch_bounds__(NP * 8)
+newton_fwd_tall_kernel(const float* __restrict__ kmm, float* __restrict__ inv, int n, int iters, int bh,
+                       const float* __restrict__ A, const TB* __restrict__ B, float* __restrict__ part, int N, int P,
+                       int Q, int per) {
+  if ((int)blockIdx.x < bh) {
+    newton_fwd_body<float, NP, true, 2, KL>(kmm, inv, n, iters);
+  } else {
+    extern __shared__ __align__(16) float nsm[];
+    const int t = (int)blockIdx.x - bh;
+    tall_t_bf16_body<TB>(A, B, part, N, P, Q, nsm, t / per, t % per, per);
+  }
+}
+
 template <int NP, int WPR, int KL>
 __global__ void __launch_bounds__(NP * 4 * WPR)
-newton_fwd_mul_kernel(const float* __restrict__ mat, float* __restrict__ out, int n, int iters,
-                      const float* __restrict__ part, int per, int d, float* __restrict__ kvOut,
-                      float* __restrict__ wOut) {
+landmark_kv_w_kernel(const float* __restrict__ inv, const float* __restrict__ part, int per, int n, int d,
+                     float* __restrict__ kvOut, float* __restrict__ wOut) {
   using L = NsLayout<NP, WPR>;
-  newton_fwd_body<float, NP, true, WPR, KL>(mat, out, n, iters);
-  // The body ends after a barrier that follows every read of slot T (P V), so
-  // the slot takes kv; V stays in slot V.
   extern __shared__ __align__(16) float nsm[];
   float* KVs = nsm;
-  const float* Vs = nsm + L::ELEMS;
-  const int wave = KL == 1 ? (uniform(threadIdx.x >> 6) + (L::NT - 1) * WPR) % L::NW : uniform(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  sum_partials<NP, WPR>(KVs, part, per, n, d);
+  float* Vs = nsm + L::ELEMS;
+  static_assert(NP == 64 && L::THREADS == 1024, "four elements of each 64 x 64 slot per thread");
+  // Every load in flight before the first LDS write: the inverse (zero padded to 64 x 64) and the
+  // partials, summed in workgroup order as sum_partials does.
+  const float* Vg = inv + (size_t)blockIdx.x * n * n;
+  const float* src = part + (size_t)blockIdx.x * per * 64 * 64;
+  float vi[4], ks[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = threadIdx.x + 1024 * q, i = e >> 6, j = e & 63;
+    vi[q] = (i < n && j < n) ? Vg[i * n + j] : 0.f;
+  }
+  int x = 0;
+  for (; x + 2 <= per; x += 2) {
+    float a[4], b[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = threadIdx.x + 1024 * q;
+      a[q] = src[(size_t)x * 4096 + e];
+      b[q] = src[(size_t)(x + 1) * 4096 + e];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ks[q] = (ks[q] + a[q]) + b[q];
+  }
+  for (; x < per; ++x)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ks[q] += src[(size_t)x * 4096 + threadIdx.x + 1024 * q];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = threadIdx.x + 1024 * q, i = e >> 6, j = e & 63;
+    Vs[i * L::LS + j] = vi[q];
+    KVs[i * L::LS + j] = (i < n && j < d) ? ks[q] : 0.f;
+  }
   __syncthreads();
+  const int wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   float* kvs = kvOut + (size_t)blockIdx.x * n * d;
   for (int e = threadIdx.x; e < n * 64; e += L::THREADS) {
     const int i = e >> 6, j = e & 63;
@@ -1444,15 +1494,32 @@ using namespace lfamd;
 // The attention layer's fused landmark kernels (48 < m <= 64: the 64 bucket).
 constexpr size_t kMulBwdLds = 4 * (size_t)NsLayout<64>::ELEMS * 4;
 
-template <int WPR, int KL>
-int launch_fwd_mul(const float* kmm, float* inv, int64_t bh, int m, int iters, const float* part, int per, int d,
-                   float* kv, float* w, hipStream_t st) {
-  auto k = newton_fwd_mul_kernel<64, WPR, KL>;
-  if (int s = check_fit(reinterpret_cast<const void*>(k), 64 * 4 * WPR, fwd_lds<64>(), "attention landmarks forward")) return s;
+template <int KL>
+int launch_fwd_tall(int v_dtype, const float* kmm, float* inv, int64_t bh, int m, int iters, const float* kkm,
+                    const void* v, float* part, int64_t rows, int d, int per, hipStream_t st) {
+  const size_t lds = std::max<size_t>(fwd_lds<64>(), (size_t)tall_lds_floats() * 4);
+  const dim3 grid((unsigned)(bh * (1 + per))), block(64 * 8);
+  auto go = [&](auto k, const auto* B) -> int {
+    if (int s = check_fit(reinterpret_cast<const void*>(k), 64 * 8, lds, "attention landmarks forward")) return s;
+    if (int s = set_lds(k, lds)) return s;
+    hipLaunchKernelGGL(k, grid, block, lds, st, kmm, inv, m, iters, (int)bh, kkm, B, part, (int)rows, m, d, per);
+    return check_launch("attention landmarks forward");
+  };
+  switch (v_dtype) {
+    case LFAMD_F32: return go(newton_fwd_tall_kernel<64, KL, float>, static_cast<const float*>(v));
+    case LFAMD_F16: return go(newton_fwd_tall_kernel<64, KL, f16s>, static_cast<const f16s*>(v));
+    default: return go(newton_fwd_tall_kernel<64, KL, bf16s>, static_cast<const bf16s*>(v));
+  }
+}
+
+template <int KL>
+int launch_kv_w(const float* inv, const float* part, int per, int64_t bh, int m, int d, float* kv, float* w,
+                hipStream_t st) {
+  auto k = landmark_kv_w_kernel<64, 4, KL>;
+  if (int s = check_fit(reinterpret_cast<const void*>(k), 64 * 16, fwd_lds<64>(), "attention landmarks forward")) return s;
   if (int s = set_lds(k, fwd_lds<64>())) return s;
-  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(64 * 4 * WPR), fwd_lds<64>(), st, kmm, inv, m, iters, part, per, d,
-                     kv, w);
-  return check_launch("attention landmarks forward");
+  hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(64 * 16), fwd_lds<64>(), st, inv, part, per, m, d, kv, w);
+  return check_launch("attention landmarks forward (kv, W)");
 }
 
 template <int KL>
@@ -1487,14 +1554,13 @@ int lfamd_attention_landmarks_forward(const float* kmm, const float* kkm, int v_
   hipStream_t st = static_cast<hipStream_t>(stream);
   int per = 0;
   float* part = static_cast<float*>(workspace);
-  if (int s = tall_t_partials(v_dtype, kkm, v, part, workspace_bytes, slices, rows, m, d, st, &per)) return s;
   if (iters < 0) iters = 0;
-  const bool wide = use_wide<64>(slices);
-  if (m == 49)
-    return wide ? launch_fwd_mul<4, 1>(kmm, inv, slices, m, iters, part, per, d, kv, w, st)
-                : launch_fwd_mul<2, 1>(kmm, inv, slices, m, iters, part, per, d, kv, w, st);
-  return wide ? launch_fwd_mul<4, 4>(kmm, inv, slices, m, iters, part, per, d, kv, w, st)
-              : launch_fwd_mul<2, 4>(kmm, inv, slices, m, iters, part, per, d, kv, w, st);
+  if (int s = tall_t_check(v_dtype, kkm, v, workspace_bytes, slices, rows, m, d, &per)) return s;
+  if (int s = (m == 49 ? launch_fwd_tall<1>(v_dtype, kmm, inv, slices, m, iters, kkm, v, part, rows, d, per, st)
+                       : launch_fwd_tall<4>(v_dtype, kmm, inv, slices, m, iters, kkm, v, part, rows, d, per, st)))
+    return s;
+  return m == 49 ? launch_kv_w<1>(inv, part, per, slices, m, d, kv, w, st)
+                 : launch_kv_w<4>(inv, part, per, slices, m, d, kv, w, st);
 }
 
 int lfamd_attention_landmarks_backward(const float* kqm, int dtype, const void* g, const void* v, const float* kkm,
