@@ -84,10 +84,11 @@ int tall_t_partials(int b_dtype, const float* A, const void* B, float* ws, size_
 // launch (mix_kernels.hip): i = 0, 1 with A of element type dtype [N][P[0]],
 // fp32 C [N][Q[0]], B strides sq[0], sp[0], bStride[0]; i = 2 with fp32 A
 // [N][P[1]] and C of element type dtype [N][Q[1]] (strides [1]).
-// LFAMD_ERR_UNSUPPORTED where the bf16 row kernel does not take them.
+// LFAMD_ERR_UNSUPPORTED where the bf16 row kernel does not take them. Only
+// products first..2 run (first = 0: all three).
 int mix_rows_trio(int dtype, const void* const* A, const float* const* B, void* const* C, int64_t slices, int64_t N,
                   const int* P, const int* Q, const int64_t* sq, const int64_t* sp, const int64_t* bStride,
-                  hipStream_t st);
+                  hipStream_t st, int first = 0);
 
 inline bool valid_dtype(int dt) {
   return dt == LFAMD_F32 || dt == LFAMD_F16 || dt == LFAMD_BF16 || dt == LFAMD_F64;

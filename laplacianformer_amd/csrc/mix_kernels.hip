@@ -141,160 +141,6 @@ mix_rows_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* __res
 }
 
 
-// The row product on the bf16 matrix cores, exact to fp32 rounding: A and B are
-// split into bf16 pieces (A exactly; B = b1 + b2 + b3 exactly) and the products
-// of the pieces whose weight is at least 2^-16 of the leading one
-// (a1 b1, a1 b2, a2 b1, a1 b3, a2 b2, a3 b1) are accumulated in fp32 by
-// v_mfma_f32_16x16x32_bf16; the terms left out are below 2^-22 |a| |b|.
-// A workgroup is kMixWaves waves; each works alone on 16-row groups g,
-// g + kMixWaves * gridDim.x, ... of its slice (one group's loads ahead). Lane (i, h) = (lane % 16, lane / 16) holds the A
-// operand of row i, k = 16 h + 8 kb + e (kb < 2, e < 8), i.e. elements
-// [16 h, 16 h + 16) of the row:
-//  * DIRECT (P = 64): loaded as 16-byte vectors straight from the row;
-//  * otherwise (N * P * sizeof(TA) a multiple of 16): the group's rows * P
-//    elements are one contiguous run of 16-byte vectors, written to the wave's
-//    LDS rows as fp32 with pitch P and read back per lane.
-// The workgroup splits B once into LDS in operand order (piece, column tile,
-// kb, lane). Outputs go straight from the accumulators to C.
-constexpr int kMixWaves = 12;  // one workgroup per CU, three waves per SIMD
-template <typename TA, typename TC, bool DIRECT>
-__device__ __forceinline__ void mix_rows_bf16_body(const TA* __restrict__ A, const float* __restrict__ B,
-                                                   TC* __restrict__ C, int N, int P, int Q, int64_t sq, int64_t sp,
-                                                   int64_t bStride, int s, int xb, int per) {
-  constexpr int EV = 16 / (int)sizeof(TA);  // elements per 16-byte vector
-  constexpr int LV = 16 / EV;               // vectors per lane and group
-  constexpr int NA = APieces<TA>::n;
-  __shared__ __align__(16) uint4 Bp[3 * 4 * 2 * 64];                     // [piece][c][kb][lane]
-  __shared__ __align__(16) float Ws[DIRECT ? 1 : kMixWaves][kMixGroup * kMixPMax];  // per wave: its rows (fp32)
-  const int groups = (N + kMixGroup - 1) / kMixGroup;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  const TA* A0 = A + (size_t)s * N * P;
-  TC* C0 = C + (size_t)s * N * Q;
-
-  uint4 xv[LV];
-  auto load = [&](int g) {
-    const int r0 = kMixGroup * g, rows = min(kMixGroup, N - r0);
-    if constexpr (DIRECT) {
-      const uint4* src = reinterpret_cast<const uint4*>(A0 + (size_t)(r0 + min(li, rows - 1)) * kMixPMax + 16 * lg);
-#pragma unroll
-      for (int v = 0; v < LV; ++v) xv[v] = src[v];
-    } else {
-      const uint4* src = reinterpret_cast<const uint4*>(A0 + (size_t)r0 * P);
-      const int nv = (rows * P + EV - 1) / EV;
-#pragma unroll
-      for (int v = 0; v < LV; ++v) xv[v] = src[min(lane + 64 * v, nv - 1)];
-    }
-  };
-  int g = xb * kMixWaves + wave;
-  const int gstep = per * kMixWaves;
-  load(min(g, groups - 1));  // in flight while B is split
-
-  // B's pieces: thread t < 256 takes (c, kb, lane) = (t / 128, (t / 64) % 2,
-  // t % 64) and t + 256: B[k][16 c + i] for k = 16 h + 8 kb + e, zero outside Q x P.
-  if (threadIdx.x < 256) {  // (the first four waves)
-    const float* Bm = B + (size_t)s * bStride;
-    float bv[2][8];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int cmb = threadIdx.x + 256 * t, ln = cmb & 63, kb = (cmb >> 6) & 1, c = cmb >> 7;
-      const int q = 16 * c + (ln & 15), p0 = 16 * (ln >> 4) + 8 * kb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bv[t][e] = Bm[min(q, Q - 1) * sq + min(p0 + e, P - 1) * sp];
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(bv[t][e]));
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int cmb = threadIdx.x + 256 * t, ln = cmb & 63, kb = (cmb >> 6) & 1, c = cmb >> 7;
-      const int q = 16 * c + (ln & 15), p0 = 16 * (ln >> 4) + 8 * kb;
-      uint32_t h[3][4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float x0 = (q < Q && p0 + 2 * e < P) ? bv[t][2 * e] : 0.0f;
-        const float x1 = (q < Q && p0 + 2 * e + 1 < P) ? bv[t][2 * e + 1] : 0.0f;
-        split3_pair(x0, x1, h[0][e], h[1][e], h[2][e]);
-      }
-#pragma unroll
-      for (int pc = 0; pc < 3; ++pc) Bp[((pc * 4 + c) * 2 + kb) * 64 + ln] = make_uint4(h[pc][0], h[pc][1], h[pc][2], h[pc][3]);
-    }
-  }
-  __syncthreads();  // the only workgroup barrier
-  float* W = Ws[DIRECT ? 0 : wave];
-
-  for (; g < groups; g += gstep) {
-    const int r0 = kMixGroup * g, rows = min(kMixGroup, N - r0);
-    float a[16];  // the lane's A operand, k = 16 lg + j
-    if constexpr (DIRECT) {
-#pragma unroll
-      for (int v = 0; v < LV; ++v) unpack16<TA>(xv[v], &a[v * EV]);
-    } else {
-      const int nv = (rows * P + EV - 1) / EV;
-#pragma unroll
-      for (int v = 0; v < LV; ++v) {
-        float f[EV];
-        unpack16<TA>(xv[v], f);
-        float4* dst = reinterpret_cast<float4*>(W + min(lane + 64 * v, nv - 1) * EV);
-#pragma unroll
-        for (int e = 0; e < EV / 4; ++e) dst[e] = make_float4(f[4 * e], f[4 * e + 1], f[4 * e + 2], f[4 * e + 3]);
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < 16; ++j) a[j] = W[min(li * P + 16 * lg + j, kMixGroup * kMixPMax - 1)];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(a[j]));  // (keeps the reads unconditional)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) a[j] = 16 * lg + j < P ? a[j] : 0.0f;  // k >= P: the next row's value
-      wave_lds_sync();
-    }
-    load(min(g + gstep, groups - 1));  // the last group reloads itself (cached)
-    asm volatile("" ::: "memory");  // B's pieces are read from LDS per group, not held in registers
-    uint4 ap[3][2];  // [piece][kb]
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      uint32_t h[3][4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) split3_pair(a[8 * kb + 2 * e], a[8 * kb + 2 * e + 1], h[0][e], h[1][e], h[2][e]);
-#pragma unroll
-      for (int pc = 0; pc < 3; ++pc) ap[pc][kb] = make_uint4(h[pc][0], h[pc][1], h[pc][2], h[pc][3]);
-    }
-    v4f acc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 b1 = __builtin_bit_cast(bf16x8, Bp[((0 * 4 + c) * 2 + kb) * 64 + lane]);
-        const bf16x8 b2 = __builtin_bit_cast(bf16x8, Bp[((1 * 4 + c) * 2 + kb) * 64 + lane]);
-        const bf16x8 b3 = __builtin_bit_cast(bf16x8, Bp[((2 * 4 + c) * 2 + kb) * 64 + lane]);
-        const bf16x8 a1 = __builtin_bit_cast(bf16x8, ap[0][kb]);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[c], 0, 0, 0);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b2, acc[c], 0, 0, 0);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b3, acc[c], 0, 0, 0);
-        if constexpr (NA >= 2) {
-          const bf16x8 a2 = __builtin_bit_cast(bf16x8, ap[1][kb]);
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b1, acc[c], 0, 0, 0);
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b2, acc[c], 0, 0, 0);
-        }
-        if constexpr (NA >= 3) {
-          const bf16x8 a3 = __builtin_bit_cast(bf16x8, ap[2][kb]);
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b1, acc[c], 0, 0, 0);
-        }
-      }
-    }
-    TC* Cg = C0 + (size_t)r0 * Q;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 4 * lg + r, col = 16 * c + li;
-        if (row < rows && col < Q) Cg[(size_t)row * Q + col] = from_acc<TC>(acc[c][r]);
-      }
-  }
-}
-
 // Grid (workgroups per slice, slices).
 template <typename TA, typename TC, bool DIRECT>
 __global__ void __launch_bounds__(64 * kMixWaves)
@@ -304,7 +150,7 @@ mix_rows_bf16_kernel(const TA* __restrict__ A, const float* __restrict__ B, TC* 
 }
 
 // Three row products in one launch (grid (workgroups per slice, 3 * slices),
-// each product's workgroups after the previous one's): products 0 and 1 of one
+// each product's workgroups after the previous one's; or products first..2 only): products 0 and 1 of one
 // shape, A of element type TA [N][P0] and fp32 C [N][Q0]; product 2 with fp32 A
 // [N][P1] and C of element type TA [N][Q1] (the attention layer's g w^T,
 // v dkv^T and K_km dkv).
@@ -317,8 +163,8 @@ struct MixTrio {
 };
 template <typename TA, bool DIRECT01>
 __global__ void __launch_bounds__(64 * kMixWaves)
-mix_rows_bf16_trio_kernel(MixTrio t, int slices, int N) {
-  const int src = (int)blockIdx.y / slices, s = (int)blockIdx.y - src * slices;
+mix_rows_bf16_trio_kernel(MixTrio t, int slices, int N, int first) {
+  const int src = first + (int)blockIdx.y / slices, s = (int)blockIdx.y % slices;
   if (src < 2)
     mix_rows_bf16_body<TA, float, DIRECT01>(static_cast<const TA*>(t.A[src]), t.B[src], static_cast<float*>(t.C[src]),
                                             N, t.P[0], t.Q[0], t.sq[0], t.sp[0], t.bStride[0], s, blockIdx.x,
@@ -506,13 +352,13 @@ int launch_tall_t(const float* A, const void* B, float* C, float* ws, int64_t sl
 // does not take an operand (the caller then makes one call per product).
 int mix_rows_trio(int dtype, const void* const* A, const float* const* B, void* const* C, int64_t slices, int64_t N,
                   const int* P, const int* Q, const int64_t* sq, const int64_t* sp, const int64_t* bStride,
-                  hipStream_t st) {
+                  hipStream_t st, int first) {
   const int64_t es = dtype == LFAMD_F32 ? 4 : 2;
   bool direct = P[0] == kMixPMax, rows16 = (N * P[0] * es) % 16 == 0;
-  for (int i = 0; i < 2; ++i)
+  for (int i = first; i < 2; ++i)
     if ((reinterpret_cast<uintptr_t>(A[i]) & 15) != 0) direct = rows16 = false;
   const bool two16 = (reinterpret_cast<uintptr_t>(A[2]) & 15) == 0 && (N * P[1] * 4) % 16 == 0;
-  if (!(direct || rows16) || !two16 || slices < 1 || N < 1 || 3 * slices > 65535)
+  if (!(direct || rows16) || !two16 || slices < 1 || N < 1 || 3 * slices > 65535 || first < 0 || first > 2)
     return fail(LFAMD_ERR_UNSUPPORTED, "row product trio: operands the bf16 kernel does not take");
   for (int i = 0; i < 2; ++i)
     if (P[i] > kMixPMax || Q[i] > kMixPMax || P[i] < 1 || Q[i] < 1)
@@ -520,15 +366,16 @@ int mix_rows_trio(int dtype, const void* const* A, const float* const* B, void* 
   const MixTrio t{{A[0], A[1], A[2]}, {B[0], B[1], B[2]}, {C[0], C[1], C[2]}, {P[0], P[1]}, {Q[0], Q[1]},
                   {sq[0], sq[1]}, {sp[0], sp[1]}, {bStride[0], bStride[1]}};
   const int64_t groups = (N + kMixGroup - 1) / kMixGroup;
-  const int64_t per = std::max<int64_t>(
-      1, std::min<int64_t>((groups + kMixWaves - 1) / kMixWaves, ((int64_t)num_cus() + 3 * slices - 1) / (3 * slices)));
-  const dim3 grid((unsigned)per, (unsigned)(3 * slices)), block(64 * kMixWaves);
+  const int64_t nsrc = 3 - first;
+  const int64_t per = std::max<int64_t>(1, std::min<int64_t>((groups + kMixWaves - 1) / kMixWaves,
+                                                             ((int64_t)num_cus() + nsrc * slices - 1) / (nsrc * slices)));
+  const dim3 grid((unsigned)per, (unsigned)(nsrc * slices)), block(64 * kMixWaves);
 #define LFAMD_TRIO(TA)                                                                                             \
   do {                                                                                                             \
     if (direct)                                                                                                    \
-      hipLaunchKernelGGL((mix_rows_bf16_trio_kernel<TA, true>), grid, block, 0, st, t, (int)slices, (int)N);      \
+      hipLaunchKernelGGL((mix_rows_bf16_trio_kernel<TA, true>), grid, block, 0, st, t, (int)slices, (int)N, first); \
     else                                                                                                           \
-      hipLaunchKernelGGL((mix_rows_bf16_trio_kernel<TA, false>), grid, block, 0, st, t, (int)slices, (int)N);     \
+      hipLaunchKernelGGL((mix_rows_bf16_trio_kernel<TA, false>), grid, block, 0, st, t, (int)slices, (int)N, first); \
   } while (0)
   switch (dtype) {
     case LFAMD_F32: LFAMD_TRIO(float); break;

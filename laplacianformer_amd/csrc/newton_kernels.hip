@@ -581,9 +581,9 @@ landmark_kv_w_kernel(const float* __restrict__ inv, const float* __restrict__ pa
 }
 
 template <int NP, int WPR, int KL>
-__global__ void __launch_bounds__(NP * 4 * WPR)
-newton_bwd_mul_kernel(const float* __restrict__ part, int per, const float* __restrict__ kv,
-                      const float* __restrict__ inv, float* __restrict__ dkv, float* __restrict__ gmat, int n, int d) {
+__device__ __forceinline__ void newton_bwd_mul_body(const float* __restrict__ part, int per, const float* __restrict__ kv,
+                                                    const float* __restrict__ inv, float* __restrict__ dkv,
+                                                    float* __restrict__ gmat, int n, int d) {
   using L = NsLayout<NP, WPR>;
   extern __shared__ __align__(16) float nsm[];
   float* Vs = nsm;                   // X
@@ -618,6 +618,33 @@ newton_bwd_mul_kernel(const float* __restrict__ part, int per, const float* __re
       const int i = 16 * strip + 4 * (lane >> 4) + r, j = 16 * (t0 + t) + (lane & 15);
       if (i < n && j < n) gmat[off + (size_t)i * n + j] = -acc[t][r];
     }
+}
+
+template <int NP, int WPR, int KL>
+__global__ void __launch_bounds__(NP * 4 * WPR)
+newton_bwd_mul_kernel(const float* __restrict__ part, int per, const float* __restrict__ kv,
+                      const float* __restrict__ inv, float* __restrict__ dkv, float* __restrict__ gmat, int n, int d) {
+  newton_bwd_mul_body<NP, WPR, KL>(part, per, kv, inv, dkv, gmat, n, d);
+}
+
+// The landmark backward's first launch after the tall product: workgroups [0, bh)
+// run newton_bwd_mul_body (dkv and dKmm), the others the row product
+// dK_qm = g W^T (mix_rows_bf16_body, 16 waves, `per` workgroups per slice), which
+// needs neither: it runs on the CUs the one-workgroup-per-slice products leave
+// free. The other two row products, which read dkv, follow in one launch.
+template <int KL, typename TA, bool DIRECT>
+__global__ void __launch_bounds__(1024)
+newton_bwd_mix_kernel(const float* __restrict__ part, int per, const float* __restrict__ kv,
+                      const float* __restrict__ inv, float* __restrict__ dkv, float* __restrict__ dkmm, int n, int d,
+                      int bh, const TA* __restrict__ g, const float* __restrict__ w, float* __restrict__ dkqm, int N,
+                      int permix) {
+  if ((int)blockIdx.x < bh) {
+    newton_bwd_mul_body<64, 4, KL>(part, per, kv, inv, dkv, dkmm, n, d);
+  } else {
+    const int t = (int)blockIdx.x - bh;
+    mix_rows_bf16_body<TA, float, DIRECT, 16>(g, w, dkqm, N, d, n, d, 1, (int64_t)n * d, t / permix, t % permix,
+                                              permix);
+  }
 }
 
 template <typename T, int NP, int WPR = 1, int KL = 4>
@@ -1532,6 +1559,38 @@ int launch_bwd_mul(const float* part, int per, const float* kv, const float* inv
   return check_launch("attention landmarks backward");
 }
 
+// Launch 1 of the landmark backward after the tall product (newton_bwd_mix_kernel);
+// LFAMD_ERR_UNSUPPORTED (nothing launched) where the row kernel does not take g.
+template <int KL>
+int launch_bwd_mix(int dtype, const float* part, int per, const float* kv, const float* inv, float* dkv, float* dkmm,
+                   int64_t bh, int m, int d, const void* g, const float* w, float* dkqm, int64_t rows,
+                   hipStream_t st) {
+  const int64_t es = dtype == LFAMD_F32 ? 4 : 2;
+  const bool aligned = (reinterpret_cast<uintptr_t>(g) & 15) == 0;
+  const bool direct = aligned && d == kMixPMax, rows16 = aligned && (rows * d * es) % 16 == 0;
+  if (!(direct || rows16) || rows > INT32_MAX / 2)
+    return fail(LFAMD_ERR_UNSUPPORTED, "attention landmarks backward: g not 16-byte aligned by rows");
+  const int64_t groups = (rows + kMixGroup - 1) / kMixGroup, cus = num_cus();
+  const int permix = (int)std::max<int64_t>(1, std::min<int64_t>((groups + 15) / 16, (cus - bh + bh - 1) / bh));
+  const dim3 grid((unsigned)(bh * (1 + permix))), block(1024);
+  auto go = [&](auto k, const auto* G) -> int {
+    if (int s = check_fit(reinterpret_cast<const void*>(k), 1024, kMulBwdLds, "attention landmarks backward")) return s;
+    if (int s = set_lds(k, kMulBwdLds)) return s;
+    hipLaunchKernelGGL(k, grid, block, kMulBwdLds, st, part, per, kv, inv, dkv, dkmm, m, d, (int)bh, G, w, dkqm,
+                       (int)rows, permix);
+    return check_launch("attention landmarks backward");
+  };
+#define LFAMD_BWDMIX(TA)                                                                          \
+  return direct ? go(newton_bwd_mix_kernel<KL, TA, true>, static_cast<const TA*>(g))             \
+                : go(newton_bwd_mix_kernel<KL, TA, false>, static_cast<const TA*>(g))
+  switch (dtype) {
+    case LFAMD_F32: LFAMD_BWDMIX(float);
+    case LFAMD_F16: LFAMD_BWDMIX(f16s);
+    default: LFAMD_BWDMIX(bf16s);
+  }
+#undef LFAMD_BWDMIX
+}
+
 int check_landmarks(int dt, int64_t slices, int64_t rows, int m, int d, const char* who) {
   if (dt != LFAMD_F32 && dt != LFAMD_F16 && dt != LFAMD_BF16) return fail(LFAMD_ERR_DTYPE, "%s: unsupported dtype %d", who, dt);
   if (slices < 0 || slices > 65535 || rows < 1 || rows > (int64_t)1 << 30 || m < 1 || d < 1)
@@ -1575,17 +1634,28 @@ int lfamd_attention_landmarks_backward(const float* kqm, int dtype, const void* 
   int per = 0;
   float* part = static_cast<float*>(workspace);
   if (int s = tall_t_partials(dtype, kqm, g, part, workspace_bytes, slices, rows, m, d, st, &per)) return s;
-  if (int s = (m == 49 ? launch_bwd_mul<1>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)
-                       : launch_bwd_mul<4>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)))
-    return s;
-  // dK_qm = g w^T, dK_km = v dkv^T and dv = K_km dkv in one launch.
   const int64_t md = (int64_t)m * d;
   const void* as[3] = {g, v, kkm};
   const float* bs[3] = {w, dkv, dkv};
   void* cs[3] = {dkqm, dkkm, dv};
   const int P[2] = {d, m}, Q[2] = {m, d};
   const int64_t sq[2] = {d, 1}, sp[2] = {1, d}, bstr[2] = {md, md};
-  int s = mix_rows_trio(dtype, as, bs, cs, slices, rows, P, Q, sq, sp, bstr, st);
+  // dK_qm = g w^T beside the inverse's products, then dK_km = v dkv^T and dv = K_km dkv in one launch.
+  int s = m == 49 ? launch_bwd_mix<1>(dtype, part, per, kv, inv, dkv, dkmm, slices, m, d, g, w, dkqm, rows, st)
+                  : launch_bwd_mix<4>(dtype, part, per, kv, inv, dkv, dkmm, slices, m, d, g, w, dkqm, rows, st);
+  if (s == LFAMD_OK) {
+    s = mix_rows_trio(dtype, as, bs, cs, slices, rows, P, Q, sq, sp, bstr, st, 1);
+    if (s != LFAMD_ERR_UNSUPPORTED) return s;
+    if ((s = lfamd_mix_rows(dtype, v, dkv, LFAMD_F32, dkkm, slices, rows, d, m, d, 1, md, st))) return s;
+    return lfamd_mix_rows(LFAMD_F32, kkm, dkv, dtype, dv, slices, rows, m, d, 1, d, md, st);
+  }
+  if (s != LFAMD_ERR_UNSUPPORTED) return s;
+  // g the row kernel does not take as a whole: the inverse's products, then the row products
+  // one call each.
+  if ((s = (m == 49 ? launch_bwd_mul<1>(part, per, kv, inv, dkv, dkmm, slices, m, d, st)
+                    : launch_bwd_mul<4>(part, per, kv, inv, dkv, dkmm, slices, m, d, st))))
+    return s;
+  s = mix_rows_trio(dtype, as, bs, cs, slices, rows, P, Q, sq, sp, bstr, st);
   if (s != LFAMD_ERR_UNSUPPORTED) return s;
   if ((s = lfamd_mix_rows(dtype, g, w, LFAMD_F32, dkqm, slices, rows, d, m, d, 1, md, st))) return s;
   if ((s = lfamd_mix_rows(dtype, v, dkv, LFAMD_F32, dkkm, slices, rows, d, m, d, 1, md, st))) return s;
