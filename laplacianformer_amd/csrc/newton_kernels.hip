@@ -272,8 +272,7 @@ __device__ __forceinline__ float compute_alpha(const float* __restrict__ Ps, int
 }
 
 // The forward variant whose U = V T reads V from registers (see the loop): the
-// one-live-row path with four waves per strip (its VGPR count still lets two
-// workgroups share a CU, as the wide layout assumes).
+// one-live-row path with two or four waves per strip.
 template <int NP, int WPR, int KL> constexpr bool fwd_va() { return KL == 1 && WPR >= 2; }
 
 // PV_FIRST: V <- 2V - V(PV) (the reference's order for n <= 112), P held in
@@ -451,6 +450,206 @@ __device__ __forceinline__ void newton_fwd_body(const T* __restrict__ mat, T* __
     for (int j = lane; j < n; j += 64) Og[i * n + j] = from_acc<T>(Vs[i * L::LS + j]);
 }
 
+// One 16 x 16 tile of X Y (X's 16 rows in registers as in mfma_rowstrip_areg,
+// Y in LDS: rows k, or TRANS_Y: Y[k][j] read from Ys[j][k]) for column tile t,
+// with n = 16 m + 1 (KL = 1: one live k in the last block).
+template <bool TRANS_Y>
+__device__ __forceinline__ v4f mfma_tile_areg64(const float (&pa)[4][4], const float* __restrict__ Ys, int t, int lane) {
+  constexpr int LS = NsLayout<64>::LS;
+  const int li = lane & 15, lk = lane >> 4, j = 16 * t + li;
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  float b[4][4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const int k = 16 * kb + 4 * lk;
+    if constexpr (TRANS_Y) {
+      if (kb < 3) {
+        const float4 v = *reinterpret_cast<const float4*>(&Ys[j * LS + k]);
+        b[kb][0] = v.x; b[kb][1] = v.y; b[kb][2] = v.z; b[kb][3] = v.w;
+      } else {
+        b[kb][0] = Ys[j * LS + k];
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (kb < 3 || q == 0) b[kb][q] = Ys[(k + q) * LS + j];
+    }
+  }
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (kb < 3 || q == 0) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[kb][q], b[kb][q], acc, 0, 0, 0);
+  return acc;
+}
+
+// NewtonInverse for fp32 n = 49 (the 64 bucket with one live row in the last
+// strip) when P is symmetric, which the workgroup checks on the staged P (else
+// it runs newton_fwd_body). Every iterate V is then a polynomial in P, so V, T = PV
+// and U = VT are symmetric: the iteration (the reference's V <- 2V - V(PV) order)
+// computes the six 16 x 16 tiles (r, t), r <= t < 3, on the matrix cores, row 48 on
+// the VALU, and writes each tile and its mirror (the diagonal tiles and row 48
+// from their upper halves, so every iterate is exactly symmetric): half the
+// matrix-core tiles of the general path (twelve), which computes the column-48
+// tiles as well. NW waves: 6 tile waves (two per SIMD on SIMDs 0 and 1, one on 2
+// and 3), NW = 8: 2 row-48 waves of 32 columns, NW = 16: 4 of 16 (6 idle).
+template <int NW>
+__device__ __forceinline__ void newton_fwd_sym_body(const float* __restrict__ mat, float* __restrict__ out, int n,
+                                                    int iters) {
+  constexpr int NP = 64, WPR = NW / 4, R = NW == 8 ? 2 : 4, TWR = 4 / R;
+  using L = NsLayout<NP, WPR>;
+  static_assert(L::THREADS == 64 * NW && (NW == 8 || NW == 16), "8 or 16 waves");
+  extern __shared__ __align__(16) float nsm[];
+  __shared__ float red[16];
+  float* Ps = nsm;             // P; then T (stored transposed: Ts[j][k] = T[k][j])
+  float* Vs = nsm + L::ELEMS;  // V
+  const int hw = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63, li = lane & 15, lk = lane >> 4;
+  const float* Mg = mat + (size_t)blockIdx.x * n * n;
+  float* Og = out + (size_t)blockIdx.x * n * n;
+  constexpr int PER = NP * NP / L::THREADS;
+  float pv[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + q * L::THREADS, i = e / NP, j = e - i * NP;
+    float v = 0.f;
+    if (i < n && j < n) v = Mg[i * n + j] + (i == j ? 0.01f : 0.f);
+    Ps[i * L::LS + j] = v;
+    pv[q] = v;
+  }
+  __syncthreads();
+  int asym = 0;
+  for (int e = threadIdx.x; e < n * n; e += L::THREADS) {
+    const int i = e / n, j = e - i * n;
+    if (j > i && Ps[i * L::LS + j] != Ps[j * L::LS + i]) asym = 1;
+  }
+  if (__syncthreads_or(asym)) {  // not symmetric: the general iteration
+    newton_fwd_body<float, NP, true, WPR, 1>(mat, out, n, iters);
+    return;
+  }
+  constexpr int r1 = NP - 16;  // the last strip's live row (48)
+  // Tile waves hw < 6: (r, t) = (0,0) (0,1) (0,2) (1,1) (1,2) (2,2); row waves 6 .. 6 + R - 1.
+  const bool tilew = hw < 6, roww = hw >= 6 && hw < 6 + R;
+  const int tr = hw < 3 ? 0 : hw < 5 ? 1 : 2;
+  const int tc = hw < 3 ? hw : hw < 5 ? hw - 2 : 2;
+  const int c0 = (hw - 6) * TWR;  // row waves: first column tile
+  float pa[4][4];
+  {
+    const int i = roww ? r1 : 16 * tr + li;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 v = *reinterpret_cast<const float4*>(&Ps[i * L::LS + 16 * kb + 4 * lk]);
+      pa[kb][0] = v.x; pa[kb][1] = v.y; pa[kb][2] = v.z; pa[kb][3] = v.w;
+    }
+  }
+  const float alpha = compute_alpha<NP, WPR>(Ps, n, red);
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = threadIdx.x + q * L::THREADS, i = e / NP, j = e - i * NP;
+    Vs[i * L::LS + j] = pv[q] * alpha;
+  }
+  __syncthreads();  // P read, V0 written: slot P takes T
+  float* Ts = Ps;
+  float va[4][4];
+  auto load_va = [&]() {
+    const int i = roww ? r1 : 16 * tr + li;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 v = *reinterpret_cast<const float4*>(&Vs[i * L::LS + 16 * kb + 4 * lk]);
+      va[kb][0] = v.x; va[kb][1] = v.y; va[kb][2] = v.z; va[kb][3] = v.w;
+    }
+  };
+  // Tile (r, c) and its mirror, from the lanes' 16 x 16 values val[row 4 lk + q][col li]:
+  // off the diagonal, D[16r + a][16c + b] and D[16c + b][16r + a] (the transposed one as a
+  // 16-byte store); on it, both from the upper half (a <= b) only.
+  auto store_sym = [&](float* D, int r, int c, const float (&val)[4]) {
+    if (r != c) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) D[(16 * r + 4 * lk + q) * L::LS + 16 * c + li] = val[q];
+      *reinterpret_cast<float4*>(&D[(16 * c + li) * L::LS + 16 * r + 4 * lk]) = float4{val[0], val[1], val[2], val[3]};
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int a = 4 * lk + q, b = li;
+        if (a <= b) {
+          D[(16 * r + a) * L::LS + 16 * c + b] = val[q];
+          D[(16 * c + b) * L::LS + 16 * r + a] = val[q];
+        }
+      }
+    }
+  };
+  // Row 48 of X Y on the VALU (X's row in xr, Y row-major in LDS or TRANS_Y), for the
+  // row wave's columns 16 (c0 + u) + li, summed over k by the lane groups.
+  auto row48 = [&](const float (&xr)[4][4], const float* Ys, bool transY, float (&res)[TWR]) {
+#pragma unroll
+    for (int u = 0; u < TWR; ++u) {
+      const int j = 16 * (c0 + u) + li;
+      float sum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (kb < 3 || q == 0) {
+            const int k = 16 * kb + 4 * lk + q;
+            sum += xr[kb][q] * (transY ? Ys[j * L::LS + k] : Ys[k * L::LS + j]);
+          }
+      res[u] = sum_rows4(sum);
+    }
+  };
+  for (int it = 0; it < iters; ++it) {
+    if (tilew) {
+      const v4f acc = mfma_tile_areg64<false>(pa, Vs, tc, lane);  // T(r, c) = P(r, :) V(:, c)
+      load_va();
+      // Ts holds T transposed: T(r, c) goes to Ts block (c, r) transposed, i.e. the
+      // mirror of a symmetric T: Ts[16c + b][16r + a] = T[16r + a][16c + b].
+      const float val[4] = {acc[0], acc[1], acc[2], acc[3]};
+      store_sym(Ts, tr, tc, val);
+    } else if (roww) {
+      float res[TWR];
+      row48(pa, Vs, false, res);  // T[48][j]
+      load_va();
+      if (lk == 0)
+#pragma unroll
+        for (int u = 0; u < TWR; ++u) {
+          const int j = 16 * (c0 + u) + li;
+          if (j <= r1) {
+            Ts[j * L::LS + r1] = res[u];
+            Ts[r1 * L::LS + j] = res[u];
+          }
+        }
+    }
+    __syncthreads();
+    if (tilew) {
+      const v4f acc = mfma_tile_areg64<true>(va, Ts, tc, lane);  // U(r, c) = V(r, :) T(:, c)
+      float val[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) val[q] = 2.0f * Vs[(16 * tr + 4 * lk + q) * L::LS + 16 * tc + li] - acc[q];
+      store_sym(Vs, tr, tc, val);
+    } else if (roww) {
+      float res[TWR];
+      row48(va, Ts, true, res);  // U[48][j]
+      if (lk == 0)
+#pragma unroll
+        for (int u = 0; u < TWR; ++u) {
+          const int j = 16 * (c0 + u) + li;
+          if (j <= r1) {
+            const float v = 2.0f * Vs[r1 * L::LS + j] - res[u];
+            Vs[r1 * L::LS + j] = v;
+            Vs[j * L::LS + r1] = v;
+          }
+        }
+    }
+    __syncthreads();
+  }
+  for (int i = hw; i < n; i += L::NW)
+    for (int j = lane; j < n; j += 64) Og[i * n + j] = Vs[i * L::LS + j];
+}
+
+template <int NW>
+__global__ void __launch_bounds__(64 * NW)
+newton_fwd_sym_kernel(const float* __restrict__ mat, float* __restrict__ out, int n, int iters) {
+  newton_fwd_sym_body<NW>(mat, out, n, iters);
+}
+
 template <typename T, int NP, bool PV_FIRST, int WPR = 1, int KL = 4>
 __global__ void __launch_bounds__(NP * 4 * WPR)
 newton_fwd_kernel(const T* __restrict__ mat, T* __restrict__ out, int n, int iters) {
@@ -520,7 +719,10 @@ newton_fwd_tall_kernel(const float* __restrict__ kmm, float* __restrict__ inv, i
                        const float* __restrict__ A, const TB* __restrict__ B, float* __restrict__ part, int N, int P,
                        int Q, int per) {
   if ((int)blockIdx.x < bh) {
-    newton_fwd_body<float, NP, true, 2, KL>(kmm, inv, n, iters);
+    if constexpr (KL == 1 && NP == 64)
+      newton_fwd_sym_body<8>(kmm, inv, n, iters);
+    else
+      newton_fwd_body<float, NP, true, 2, KL>(kmm, inv, n, iters);
   } else {
     extern __shared__ __align__(16) float nsm[];
     const int t = (int)blockIdx.x - bh;
@@ -1375,6 +1577,16 @@ template <typename T, int NP> constexpr bool has_kl1() { return std::is_same<T, 
 
 template <typename T, int NP, int WPR>
 int fwd_np_w(const T* m, T* o, int64_t bh, int n, int iters, hipStream_t st) {
+  // fp32 n = 49: the symmetric iteration when P is symmetric (the kernel checks; else the general one).
+  if constexpr (std::is_same<T, float>::value && NP == 64) {
+    if (n == NP - 15) {
+      auto k = newton_fwd_sym_kernel<WPR * 4>;
+      int s = set_lds(k, fwd_lds<NP>());
+      if (s) return s;
+      hipLaunchKernelGGL(k, dim3((unsigned)bh), dim3(NP * 4 * WPR), fwd_lds<NP>(), st, m, o, n, iters);
+      return check_launch("newton forward");
+    }
+  }
   // The reference's association order per bucket: V(PV) below 128, (VP)V at 128.
   if constexpr (has_kl1<T, NP>()) {
     if (n == NP - 15) {
