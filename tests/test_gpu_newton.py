@@ -114,6 +114,33 @@ def test_newton_backward_persistent(gpu, bh):
     assert_newton_close(out, oracle.newton_backward(G, V, "f32"), "f32", f"bwd persistent bh={bh}", rtol=1e-5)
 
 
+@pytest.mark.parametrize("case", ["symmetric", "one_pair", "general"])
+@pytest.mark.parametrize("bh", [3, 600])
+def test_newton_forward_n49_symmetry(gpu, case, bh):
+    """fp32 n = 49 runs the symmetric iteration (upper tiles, mirrored) when P is exactly
+    symmetric and the general one otherwise, decided per matrix in the kernel. Both against
+    the oracle; the symmetric path's result is exactly symmetric, a matrix with a single
+    asymmetric pair and a general matrix take the general path. 600 matrices: two waves per
+    strip (the 8-wave variant of the symmetric body)."""
+    import laplacianformer_amd as lf
+
+    print(f"newton forward n=49 {case} bh={bh}", flush=True)
+    n = 49
+    A = gram(bh, n, 64, seed=300 + bh)
+    if case == "one_pair":
+        A[:, 3, 40] += 1e-3  # every matrix asymmetric in one element pair
+    elif case == "general":
+        A = A + 1e-4 * np.random.default_rng(7).standard_normal(A.shape)
+    At = torch.from_numpy(A).float().reshape(bh, 1, n, n)
+    out = torch.empty_like(At, device=gpu)
+    lf.ext().NewtonInverse_forward(At.to(gpu), out, 10)
+    ref = oracle.newton_forward(At, 10, "f32")
+    assert_newton_close(out, ref, "f32", f"n=49 {case}", rtol=1e-4)
+    o = out.cpu()
+    if case == "symmetric":
+        assert torch.equal(o, o.transpose(-1, -2)), "symmetric path result not exactly symmetric"
+
+
 def test_newton_closed_forms(gpu):
     """Diagonal A = c I: X_k = (1 - (-0.8)^(2^k)) / mu * I with mu = c + 0.01; and iter = 0 gives alpha P."""
     import laplacianformer_amd as lf
