@@ -1055,7 +1055,7 @@ newton_bwd_pipe_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T*
     for (int q = 0; q < PER; ++q) {
       const int c = q * TEAM_THREADS + tt;
       vv[q] = load4_acc(inv + off + (size_t)(c / (NP / 4)) * NP + 4 * (c % (NP / 4)));
-      gg[q] = load4_acc(gout + off + (size_t)(16 * (c / (16 * NP / 4)) + (c & 15)) * NP + 4 * ((c >> 4) % (NP / 4)));
+      gg[q] = load4_acc(gout + off + (size_t)(8 * (c >> 7) + ((c & 63) >> 3)) * NP + 32 * ((c >> 6) & 1) + 4 * (c & 7));
     }
     __builtin_amdgcn_sched_barrier(0);  // raised after the load instructions, not after their data
     if (lane == 0) __hip_atomic_fetch_add(issued, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1064,7 +1064,7 @@ newton_bwd_pipe_kernel(const T* __restrict__ gout, const T* __restrict__ inv, T*
     for (int q = 0; q < PER; ++q) {
       const int c = q * TEAM_THREADS + tt;
       *reinterpret_cast<float4*>(&Vs[(c / (NP / 4)) * L::LS + 4 * (c % (NP / 4))]) = vv[q];
-      const int gi = 16 * (c / (16 * NP / 4)) + (c & 15), gj = 4 * ((c >> 4) % (NP / 4));
+      const int gi = 8 * (c >> 7) + ((c & 63) >> 3), gj = 32 * ((c >> 6) & 1) + 4 * (c & 7);
       Gts[(gj + 0) * L::LS + gi] = gg[q].x;
       Gts[(gj + 1) * L::LS + gi] = gg[q].y;
       Gts[(gj + 2) * L::LS + gi] = gg[q].z;
