@@ -211,6 +211,13 @@ __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int sk
 // i's N[i] rows (gk[i], kv[i], query q[i], grad_query dq[i]); every workgroup
 // writes a partial, so grad_key sums all sources' rows. Read only by the SEG
 // instantiations.
+// With cat set, the slice's rows are instead taken as one list (source 0's,
+// then source 1's, then source 2's) cut into nx equal workgroup ranges, so that
+// every workgroup carries the same work whatever the sources' lengths; each
+// wave keeps to one source, and wv[x * 12 + w] gives wave w of workgroup x its
+// rows: source (bits 0-1), row count (2-8), first LDS row (9-18) and first row
+// within the source (19-31).
+constexpr int kB2CatSlots = 8;  // most workgroups per slice with cat
 struct B2Seg {
   int count;
   int nx[3], N[3];
@@ -218,6 +225,8 @@ struct B2Seg {
   const float* kv[3];
   const void* q[3];
   void* dq[3];
+  int cat;
+  uint32_t wv[kB2CatSlots * 12];
 };
 
 template <typename T, int M, bool DQ, bool DK, bool GK, bool SEG>
@@ -240,7 +249,23 @@ __device__ __forceinline__ void bwd2_body(const T* __restrict__ gout, const floa
   const float* kv = kvIn;
   const T* query = queryIn;
   T* dq = dqIn;
+  // With a concatenated plan: this wave's rows (first LDS row, first source row).
+  int catW0 = 0, catRows = 0, catStart = 0;
   if constexpr (SEG) {
+    if (sg.cat) {
+      const uint32_t e = sg.wv[xg * 12 + wave];
+      const int si = (int)(e & 3u);
+      catRows = (int)((e >> 2) & 127u);
+      catW0 = (int)((e >> 9) & 1023u);
+      catStart = (int)(e >> 19);
+      N = si == 0 ? sg.N[0] : si == 1 ? sg.N[1] : sg.N[2];
+      gk = si == 0 ? sg.gk[0] : si == 1 ? sg.gk[1] : sg.gk[2];
+      kv = si == 0 ? sg.kv[0] : si == 1 ? sg.kv[1] : sg.kv[2];
+      query = static_cast<const T*>(si == 0 ? sg.q[0] : si == 1 ? sg.q[1] : sg.q[2]);
+      dq = static_cast<T*>(si == 0 ? sg.dq[0] : si == 1 ? sg.dq[1] : sg.dq[2]);
+    }
+  }
+  if constexpr (SEG) if (!sg.cat) {
     // Source-major order of the linear workgroup id (dispatch order): all of
     // source 0's workgroups, then source 1's, then source 2's. (Slice-major
     // order left a third round of big workgroups on half the CUs; callers put
@@ -270,8 +295,11 @@ __device__ __forceinline__ void bwd2_body(const T* __restrict__ gout, const floa
   float* rowsA = reinterpret_cast<float*>(smem + S.rows_off());       // [rows + 1][PITCH]
   const unsigned rowsBase = ldsBase + S.rows_off();
 
-  const int P0 = (int)((int64_t)x * N / nx), P1 = (int)((int64_t)(x + 1) * N / nx);
-  const int n = P1 - P0;
+  const bool cat = SEG && sg.cat;
+  // P0 + (LDS row) is the source row: the workgroup's first row, or for a
+  // concatenated plan the wave's first source row less its first LDS row.
+  const int P0 = cat ? catStart - catW0 : (int)((int64_t)x * N / nx);
+  const int n = cat ? 0 : (int)((int64_t)(x + 1) * N / nx) - P0;
   const uint16_t* qsl = reinterpret_cast<const uint16_t*>(query) + (size_t)bh * N * C + cb * 64;
 
   // All loads first: the key block [64][M] of the channel block (the whole
@@ -280,7 +308,8 @@ __device__ __forceinline__ void bwd2_body(const T* __restrict__ gout, const floa
   constexpr int kKeyW = (64 * M + 2 + 2 * THREADS - 1) / (2 * THREADS);
   uint32_t kwd[kKeyW];
   const int kskew = load_words<THREADS>(reinterpret_cast<const uint16_t*>(key) + ((size_t)bh * C + cb * 64) * M, 64 * M, tid, kwd);
-  const int w0 = uniform(b2_wave_start<WAVES>(wave, n)), w1 = uniform(b2_wave_start<WAVES>(wave + 1, n));
+  const int w0 = uniform(cat ? catW0 : b2_wave_start<WAVES>(wave, n));
+  const int w1 = uniform(cat ? catW0 + catRows : b2_wave_start<WAVES>(wave + 1, n));
   const int rows = w1 - w0;  // at most b2_max_wave_rows(WAVES)
   const int h = lane >> 5, p = lane & 31;
   constexpr int RPI = 64 / M;                                         // rows per load instruction
@@ -604,9 +633,161 @@ int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, 
 
 namespace {
 // Workgroups per source of a segmented launch and the partials they write.
+// Modelled duration of one SIMD's row work (M = 49, 12 waves) whose oldest,
+// middle and youngest waves have r[0], r[1], r[2] rows: three busy waves
+// issue at rate 1 and share it 35 : 35 : 29 (the b2_wave_start split that makes
+// them end together), two at 0.864 (the measured 118 against 102 cycles per
+// row of 8- and 12-wave workgroups) and one alone at 0.5, shared evenly.
+double b2_simd_time(const int (&r)[3]) {
+  double rem[3] = {(double)r[0], (double)r[1], (double)r[2]}, t = 0.0;
+  const double w3[3] = {kB2P0 / 99.0, kB2P1 / 99.0, kB2P2 / 99.0};
+  for (;;) {
+    int act[3], na = 0;
+    for (int i = 0; i < 3; ++i)
+      if (rem[i] > 1e-9) act[na++] = i;
+    if (na == 0) return t;
+    double sh[3], dt = 1e300;
+    for (int a = 0; a < na; ++a) {
+      sh[a] = na == 3 ? w3[act[a]] : (na == 2 ? 0.864 : 0.5) / na;
+      dt = std::min(dt, rem[act[a]] / sh[a]);
+    }
+    for (int a = 0; a < na; ++a) rem[act[a]] -= sh[a] * dt;
+    t += dt;
+  }
+}
+
+// Waves of one workgroup of a concatenated plan: the pieces (source, first
+// row, length) of its row range, in order, become wave table entries (see
+// B2Seg). Each piece gets a run of waves, taken from the youngest places first
+// (a short piece on the waves that get the fewest rows) and split over them by
+// the b2_wave_start weights; the counts and the order of the pieces are
+// searched for the least modelled time of the slowest SIMD. False when some
+// wave would get more than b2_max_wave_rows(12) rows.
+bool b2_cat_waves(int k, const int (&src)[3], const int (&start)[3], const int (&len)[3], uint32_t* wv) {
+  static constexpr int kPref[12] = {8, 9, 10, 11, 4, 5, 6, 7, 0, 1, 2, 3};  // youngest places first
+  auto units = [](int w) { return w < 4 ? kB2P0 : w < 8 ? kB2P1 : kB2P2; };
+  double best = 1e300;
+  int c[3] = {0, 0, 0};
+  for (c[0] = 1; c[0] <= 12; ++c[0])
+    for (c[1] = k > 1 ? 1 : 0; c[1] <= (k > 1 ? 12 : 0); ++c[1]) {
+      c[2] = k > 2 ? 12 - c[0] - c[1] : 0;
+      if (c[0] + c[1] + c[2] != 12 || (k > 2 && c[2] < 1)) continue;
+      bool fits = true;
+      for (int j = 0; j < k; ++j) fits = fits && c[j] <= std::max(1, len[j]);
+      if (!fits) continue;
+      int perm[3] = {0, 1, 2};
+      do {
+        int rows[12] = {}, first[12] = {}, from[12] = {}, pos = 0;
+        for (int a = 0; a < k; ++a) {
+          const int j = perm[a];
+          int ws[12];
+          for (int i = 0; i < c[j]; ++i) ws[i] = kPref[pos + i];
+          pos += c[j];
+          std::sort(ws, ws + c[j]);
+          int tot = 0, cum = 0, prev = 0, off = start[j];
+          for (int i = 0; i < c[j]; ++i) tot += units(ws[i]);
+          for (int i = 0; i < c[j]; ++i) {
+            cum += units(ws[i]);
+            const int next = (int)((int64_t)cum * len[j] / tot);
+            rows[ws[i]] = next - prev;
+            from[ws[i]] = j;
+            first[ws[i]] = rows[ws[i]] > 0 ? off : start[j];
+            off += next - prev;
+            prev = next;
+          }
+        }
+        int mx = 0;
+        for (int w = 0; w < 12; ++w) mx = std::max(mx, rows[w]);
+        if (mx > b2_max_wave_rows(12)) continue;
+        double cost = 0.0;
+        for (int s = 0; s < 4; ++s) {
+          const int r3[3] = {rows[s], rows[s + 4], rows[s + 8]};
+          cost = std::max(cost, b2_simd_time(r3));
+        }
+        if (cost < best) {
+          best = cost;
+          int lds = 0;
+          for (int w = 0; w < 12; ++w) {
+            const int l = rows[w] > 0 ? lds : 0;
+            wv[w] = (uint32_t)src[from[w]] | (uint32_t)rows[w] << 2 | (uint32_t)l << 9 | (uint32_t)first[w] << 19;
+            lds += rows[w];
+          }
+        }
+      } while (std::next_permutation(perm, perm + k));
+    }
+  return best < 1e300;
+}
+
+// The concatenated plan (B2Seg::cat) for sources of n[i] rows: nx workgroups
+// per slice by plan_b2's rule for the total, at most kB2CatSlots of them; zero
+// when the sources would not gain from it or do not fit it (then each source
+// takes its own workgroups). The wave table is searched once per shape and host
+// thread (~0.8 ms) and kept for the last few shapes.
+int plan_b2_cat(int nsrc, const int64_t* n, int64_t BH, int64_t C, uint32_t* wv) {
+  if (nsrc < 2) return 0;
+  int64_t tot = 0;
+  for (int i = 0; i < nsrc; ++i) tot += n[i];
+  const int64_t slices = BH * (C / 64);
+  const int64_t nx64 = std::max<int64_t>((tot + kB2MaxRows - 1) / kB2MaxRows,
+                                         std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
+                                                                                (tot + 7) / 8)));
+  if (nx64 > kB2CatSlots || tot > (int64_t)kB2CatSlots * kB2MaxRows) return 0;
+  const int nx = (int)nx64;
+  struct Key {
+    int nsrc, nx;
+    int64_t n[3];
+  };
+  constexpr int kCache = 4;
+  static thread_local Key keys[kCache] = {};
+  static thread_local uint32_t tabs[kCache][kB2CatSlots * 12];
+  static thread_local int okay[kCache] = {};
+  static thread_local int used = 0, next = 0;
+  const Key key{nsrc, nx, {n[0], nsrc > 1 ? n[1] : 0, nsrc > 2 ? n[2] : 0}};
+  for (int i = 0; i < used; ++i)
+    if (keys[i].nsrc == key.nsrc && keys[i].nx == key.nx && keys[i].n[0] == key.n[0] && keys[i].n[1] == key.n[1] &&
+        keys[i].n[2] == key.n[2]) {
+      std::copy(tabs[i], tabs[i] + kB2CatSlots * 12, wv);
+      return okay[i] ? nx : 0;
+    }
+  const int slot = used < kCache ? used++ : next;
+  next = (slot + 1) % kCache;
+  keys[slot] = key;
+  bool ok = true;
+  for (int x = 0; x < nx && ok; ++x) {
+    const int64_t a = (int64_t)x * tot / nx, b = (int64_t)(x + 1) * tot / nx;
+    int k = 0, src[3] = {}, start[3] = {}, len[3] = {};
+    int64_t s0 = 0;
+    for (int i = 0; i < nsrc; ++i) {
+      const int64_t lo = std::max(a, s0), hi = std::min(b, s0 + n[i]);
+      if (hi > lo) {
+        src[k] = i;
+        start[k] = (int)(lo - s0);
+        len[k] = (int)(hi - lo);
+        ++k;
+      }
+      s0 += n[i];
+    }
+    ok = b2_cat_waves(k, src, start, len, tabs[slot] + x * 12);
+  }
+  okay[slot] = ok;
+  std::copy(tabs[slot], tabs[slot] + kB2CatSlots * 12, wv);
+  return ok ? nx : 0;
+}
+
 B2Plan plan_b2_multi(int nsrc, const int64_t* n, int64_t BH, int64_t C, B2Seg& sg) {
   B2Plan p{};
   sg.count = nsrc;
+  if (const int nx = plan_b2_cat(nsrc, n, BH, C, sg.wv)) {
+    sg.cat = 1;
+    for (int i = 0; i < nsrc; ++i) sg.N[i] = (int)n[i];
+    const B2Plan p0 = plan_b2(BH, n[0], 49, C);
+    p.nx = nx;
+    p.ncb = p0.ncb;
+    p.lds = p0.lds;
+    p.partialElems = (size_t)BH * p.ncb * p.nx * 64 * 49;
+    return p;
+  }
+  sg.cat = 0;
   for (int i = 0; i < nsrc; ++i) {
     const B2Plan pi = plan_b2(BH, n[i], 49, C);
     sg.nx[i] = pi.nx;

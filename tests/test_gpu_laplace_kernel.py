@@ -169,18 +169,23 @@ def test_kernel_gradcheck_f64(gpu):
     assert torch.autograd.gradcheck(lambda a, b: lf.laplace_kernel(a, b, 0.7), (q, k), eps=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("lens", [(784, 784, 49), (65, 1, 200), (130, 7)], ids=lambda s: "-".join(map(str, s)))
-def test_kernel_backward_multi(gpu, lens):
+@pytest.mark.parametrize("lens,bh", [((784, 784, 49), (2, 2)), ((65, 1, 200), (2, 2)), ((130, 7), (2, 2)),
+                                     ((49, 784, 784), (16, 2)), ((65, 1, 200), (16, 2)), ((784, 784, 49), (16, 2))],
+                         ids=lambda s: "-".join(map(str, s)))
+def test_kernel_backward_multi(gpu, lens, bh):
     """lfamd_laplace_kernel_backward_multi: up to three row sources against one key in one launch.
-    Each source's grad_query is bit-identical to its own lfamd_laplace_kernel_backward call (the
-    same rows per workgroup and wave); grad_key, the sum over the sources, is held to the oracle's
-    fp64 sum with the usual bound."""
+    Each source's grad_query is bit-identical to its own lfamd_laplace_kernel_backward call (a
+    row's grad_query does not depend on the workgroup or wave that takes it); grad_key, the sum
+    over the sources, is held to the oracle's fp64 sum with the usual bound. With 4 slices each
+    source takes workgroups of its own; with 32 slices (at most 8 workgroups per slice) the
+    slice's rows are cut into equal workgroup ranges across the sources, waves keeping to one
+    source (a 1-row source, a range starting inside K_mm's 49 rows, and sources in both orders)."""
     import ctypes
 
     import laplacianformer_amd as lf
 
-    B, H, M, C = 2, 2, 49, 64
-    print(f"laplace kernel backward multi {lens}", flush=True)
+    (B, H), M, C = bh, 49, 64
+    print(f"laplace kernel backward multi {lens} B={B} H={H}", flush=True)
     lib = lf.capi()
     s = 1.0 / math.sqrt(C)
     k = gen((B, H, C, M), 831, "f16")
