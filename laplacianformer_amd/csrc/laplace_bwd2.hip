@@ -51,25 +51,20 @@
 #include "lf_common.h"
 #include "lf_internal.h"
 #include "l1_asm_gen.h"
+#include "b2_plan.h"
 
 namespace lfamd {
 
 namespace {
 
 constexpr int kB2Unroll = 4;    // rows per iteration of the asm row loop (its query prefetch depth)
-constexpr int kB2MaxRows = 512;  // most grad rows of one workgroup (staged in LDS at once)
 constexpr int kB2SoloRows = 64;  // slices up to this many rows take one workgroup each
 
 // Waves per workgroup for key count M (12 needs the 168-VGPR row loops).
 __host__ __device__ constexpr int b2_waves(int M) { return M == 49 ? 12 : 8; }
 
-// Rows of a workgroup's range before wave w (w = WAVES: all n). With 12 waves
-// (waves w, w + 4, w + 8 share SIMD w % 4) the three places of a SIMD get
-// kB2P0, kB2P1, kB2P2 parts of its rows: with an even split the youngest wave
-// of each SIMD finished ~25 % after the others and then ran alone at half
-// rate. (Per place, the middle wave runs its rows ~10 % faster than the oldest,
-// but giving it more rows, 34 / 37 / 28, changed the kernel by < 0.2 %.)
-constexpr int kB2P0 = 35, kB2P1 = 35, kB2P2 = 29, kB2PSum = 4 * (kB2P0 + kB2P1 + kB2P2);
+// Rows of a workgroup's range before wave w (w = WAVES: all n), split by the
+// kB2P0 : kB2P1 : kB2P2 weights of b2_plan.h for 12 waves, evenly otherwise.
 template <int WAVES>
 __device__ __forceinline__ int b2_wave_start(int w, int n) {
   if constexpr (WAVES == 12) {
@@ -82,12 +77,6 @@ __device__ __forceinline__ int b2_wave_start(int w, int n) {
   } else {
     return (int)((int64_t)w * n / WAVES);
   }
-}
-__host__ __device__ constexpr int b2_max_wave_rows(int waves) {
-  // floor(u1 n / S) - floor(u0 n / S) <= ceil((u1 - u0) n / S)
-  return waves == 12 ? (kB2MaxRows * (kB2P0 > kB2P1 ? (kB2P0 > kB2P2 ? kB2P0 : kB2P2) : (kB2P1 > kB2P2 ? kB2P1 : kB2P2)) +
-                        kB2PSum - 1) / kB2PSum
-                     : (kB2MaxRows + waves - 1) / waves;
 }
 
 // Layout constants shared by the kernel and the host plan.
@@ -217,7 +206,6 @@ __device__ __forceinline__ void scatter_words(const uint32_t (&wd)[MAXW], int sk
 // wave keeps to one source, and wv[x * 12 + w] gives wave w of workgroup x its
 // rows: source (bits 0-1), row count (2-8), first LDS row (9-18) and first row
 // within the source (19-31).
-constexpr int kB2CatSlots = 8;  // most workgroups per slice with cat
 struct B2Seg {
   int count;
   int nx[3], N[3];
@@ -633,106 +621,14 @@ int b2_launch(int dtype, const void* g, const void* q, const void* k, void* dq, 
 
 namespace {
 // Workgroups per source of a segmented launch and the partials they write.
-// Modelled duration of one SIMD's row work (M = 49, 12 waves) whose oldest,
-// middle and youngest waves have r[0], r[1], r[2] rows: three busy waves
-// issue at rate 1 and share it 35 : 35 : 29 (the b2_wave_start split that makes
-// them end together), two at 0.864 (the measured 118 against 102 cycles per
-// row of 8- and 12-wave workgroups) and one alone at 0.5, shared evenly.
-double b2_simd_time(const int (&r)[3]) {
-  double rem[3] = {(double)r[0], (double)r[1], (double)r[2]}, t = 0.0;
-  const double w3[3] = {kB2P0 / 99.0, kB2P1 / 99.0, kB2P2 / 99.0};
-  for (;;) {
-    int act[3], na = 0;
-    for (int i = 0; i < 3; ++i)
-      if (rem[i] > 1e-9) act[na++] = i;
-    if (na == 0) return t;
-    double sh[3], dt = 1e300;
-    for (int a = 0; a < na; ++a) {
-      sh[a] = na == 3 ? w3[act[a]] : (na == 2 ? 0.864 : 0.5) / na;
-      dt = std::min(dt, rem[act[a]] / sh[a]);
-    }
-    for (int a = 0; a < na; ++a) rem[act[a]] -= sh[a] * dt;
-    t += dt;
-  }
-}
-
-// Waves of one workgroup of a concatenated plan: the pieces (source, first
-// row, length) of its row range, in order, become wave table entries (see
-// B2Seg). Each piece gets a run of waves, taken from the youngest places first
-// (a short piece on the waves that get the fewest rows) and split over them by
-// the b2_wave_start weights; the counts and the order of the pieces are
-// searched for the least modelled time of the slowest SIMD. False when some
-// wave would get more than b2_max_wave_rows(12) rows.
-bool b2_cat_waves(int k, const int (&src)[3], const int (&start)[3], const int (&len)[3], uint32_t* wv) {
-  static constexpr int kPref[12] = {8, 9, 10, 11, 4, 5, 6, 7, 0, 1, 2, 3};  // youngest places first
-  auto units = [](int w) { return w < 4 ? kB2P0 : w < 8 ? kB2P1 : kB2P2; };
-  double best = 1e300;
-  int c[3] = {0, 0, 0};
-  for (c[0] = 1; c[0] <= 12; ++c[0])
-    for (c[1] = k > 1 ? 1 : 0; c[1] <= (k > 1 ? 12 : 0); ++c[1]) {
-      c[2] = k > 2 ? 12 - c[0] - c[1] : 0;
-      if (c[0] + c[1] + c[2] != 12 || (k > 2 && c[2] < 1)) continue;
-      bool fits = true;
-      for (int j = 0; j < k; ++j) fits = fits && c[j] <= std::max(1, len[j]);
-      if (!fits) continue;
-      int perm[3] = {0, 1, 2};
-      do {
-        int rows[12] = {}, first[12] = {}, from[12] = {}, pos = 0;
-        for (int a = 0; a < k; ++a) {
-          const int j = perm[a];
-          int ws[12];
-          for (int i = 0; i < c[j]; ++i) ws[i] = kPref[pos + i];
-          pos += c[j];
-          std::sort(ws, ws + c[j]);
-          int tot = 0, cum = 0, prev = 0, off = start[j];
-          for (int i = 0; i < c[j]; ++i) tot += units(ws[i]);
-          for (int i = 0; i < c[j]; ++i) {
-            cum += units(ws[i]);
-            const int next = (int)((int64_t)cum * len[j] / tot);
-            rows[ws[i]] = next - prev;
-            from[ws[i]] = j;
-            first[ws[i]] = rows[ws[i]] > 0 ? off : start[j];
-            off += next - prev;
-            prev = next;
-          }
-        }
-        int mx = 0;
-        for (int w = 0; w < 12; ++w) mx = std::max(mx, rows[w]);
-        if (mx > b2_max_wave_rows(12)) continue;
-        double cost = 0.0;
-        for (int s = 0; s < 4; ++s) {
-          const int r3[3] = {rows[s], rows[s + 4], rows[s + 8]};
-          cost = std::max(cost, b2_simd_time(r3));
-        }
-        if (cost < best) {
-          best = cost;
-          int lds = 0;
-          for (int w = 0; w < 12; ++w) {
-            const int l = rows[w] > 0 ? lds : 0;
-            wv[w] = (uint32_t)src[from[w]] | (uint32_t)rows[w] << 2 | (uint32_t)l << 9 | (uint32_t)first[w] << 19;
-            lds += rows[w];
-          }
-        }
-      } while (std::next_permutation(perm, perm + k));
-    }
-  return best < 1e300;
-}
-
 // The concatenated plan (B2Seg::cat) for sources of n[i] rows: nx workgroups
-// per slice by plan_b2's rule for the total, at most kB2CatSlots of them; zero
-// when the sources would not gain from it or do not fit it (then each source
-// takes its own workgroups). The wave table is searched once per shape and host
-// thread (~0.8 ms) and kept for the last few shapes.
+// per slice (b2_cat_nx), zero when the sources do not fit it (then each source
+// takes its own workgroups). The wave tables (b2_cat_tables) are searched once
+// per shape and host thread (~0.8 ms) and kept for the last few shapes.
 int plan_b2_cat(int nsrc, const int64_t* n, int64_t BH, int64_t C, uint32_t* wv) {
   if (nsrc < 2) return 0;
-  int64_t tot = 0;
-  for (int i = 0; i < nsrc; ++i) tot += n[i];
-  const int64_t slices = BH * (C / 64);
-  const int64_t nx64 = std::max<int64_t>((tot + kB2MaxRows - 1) / kB2MaxRows,
-                                         std::max<int64_t>(1, std::min<int64_t>(num_cus() / std::max<int64_t>(slices, 1),
-                                                                                (tot + 7) / 8)));
-  if (nx64 > kB2CatSlots || tot > (int64_t)kB2CatSlots * kB2MaxRows) return 0;
-  const int nx = (int)nx64;
+  const int nx = b2_cat_nx(nsrc, n, BH * (C / 64), num_cus());
+  if (nx == 0) return 0;
   struct Key {
     int nsrc, nx;
     int64_t n[3];
@@ -752,23 +648,7 @@ int plan_b2_cat(int nsrc, const int64_t* n, int64_t BH, int64_t C, uint32_t* wv)
   const int slot = used < kCache ? used++ : next;
   next = (slot + 1) % kCache;
   keys[slot] = key;
-  bool ok = true;
-  for (int x = 0; x < nx && ok; ++x) {
-    const int64_t a = (int64_t)x * tot / nx, b = (int64_t)(x + 1) * tot / nx;
-    int k = 0, src[3] = {}, start[3] = {}, len[3] = {};
-    int64_t s0 = 0;
-    for (int i = 0; i < nsrc; ++i) {
-      const int64_t lo = std::max(a, s0), hi = std::min(b, s0 + n[i]);
-      if (hi > lo) {
-        src[k] = i;
-        start[k] = (int)(lo - s0);
-        len[k] = (int)(hi - lo);
-        ++k;
-      }
-      s0 += n[i];
-    }
-    ok = b2_cat_waves(k, src, start, len, tabs[slot] + x * 12);
-  }
+  const bool ok = b2_cat_tables(nsrc, n, nx, tabs[slot]);
   okay[slot] = ok;
   std::copy(tabs[slot], tabs[slot] + kB2CatSlots * 12, wv);
   return ok ? nx : 0;
