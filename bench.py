@@ -223,6 +223,29 @@ def bench_newton(args, dev):
             "n": n, "iters": iters, "stage1": stage1}
 
 
+def layer_floors(B=64, H=2, N=784, M=49, d=64, iters=10):
+    """Per-part lower bounds (us) of one config-5 layer step (fwd + bwd) on MI355X, from the
+    algorithmic work at the published peaks: the three distances' VALU work (forward 3 and
+    backward 8 flop per (row, landmark, channel) triple, fp32 vector 157.3 TFLOP/s);
+    NewtonInverse (4 M^3 flop per iteration and 4 M^3 backward per matrix, fp32 MFMA 157.3
+    TFLOP/s); the six N-row products and the pooling as HBM bytes at 8 TB/s (fp32 K_qm / K_km
+    and their gradients [BH, N, M], fp16 q, k, v, out, grad [BH, N, d]). The products' flops
+    (2 N M d each) run exactly on the bf16 matrix cores in well under their HBM time."""
+    BH = B * H
+    T = BH * (2 * N * M + M * M) * d
+    kmat = BH * N * M * 4          # K_qm or K_km (or a gradient of one), fp32
+    tok = BH * N * d * 2           # q, k, v, out or grad_out, fp16
+    prod = 6 * (kmat + tok)        # K_km^T V, K_qm W; K_qm^T G, G W^T, K_km dkv, V dkv^T
+    pool = 3 * tok                 # pooling reads k; its backward reads and writes grad_k
+    parts = {
+        "distances_valu": 11 * T / 157.3e12 * 1e6,
+        "newton_mfma": BH * (iters + 1) * 4 * M ** 3 / 157.3e12 * 1e6,
+        "products_hbm": prod / 8e12 * 1e6,
+        "pooling_hbm": pool / 8e12 * 1e6,
+    }
+    return parts, {"triples": T, "product_bytes": prod, "pooling_bytes": pool}
+
+
 def bench_layer(args, dev):
     """LaplacianFormer attention layer fwd+bwd (B=64 H=2 N=784 d=64 fp16,
     4x4-pooled landmarks M=49, NewtonInverse 10 it) through the autograd API."""
@@ -251,10 +274,17 @@ def bench_layer(args, dev):
                              [q, k, v], g)
     graph = time_windows([graphed.replay], steps, args.warmup)
     T = B * H * (2 * N * 49 + 49 * 49) * d
+    parts, work = layer_floors(B, H, N, 49, d, 10)
+    floor_us = sum(parts.values())
     return {"workload": "BASELINE config 5: LaplacianFormer attention fwd+bwd, B=64 H=2 N=784 (28x28) d=64 "
                         "fp16, M=49 (4x4 pooled K), NewtonInverse 10 it",
             "ms_per_step": eager["median"], "ms_per_step_hip_graph": graph["median"], "eager": eager,
-            "hip_graph": graph, "l1_triples": T, "steps_per_window": steps}
+            "hip_graph": graph, "l1_triples": T, "steps_per_window": steps,
+            "roofline": {"bound": "mixed (distances VALU, NewtonInverse MFMA, products and pooling HBM)",
+                         "floor_us": floor_us, "parts_us": parts, "work": work,
+                         "frac": floor_us / (eager["median"] * 1000.0),
+                         "what": "sum of the parts' floors at MI355X peaks (157.3 TFLOP/s fp32 vector and "
+                                 "MFMA, 8 TB/s) over the eager step"}}
 
 
 def bench_cfg4(args, dev):
